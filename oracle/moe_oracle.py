@@ -1,0 +1,492 @@
+"""CPU restatement (numpy, float64 by default) of the reference MoE-layer hot path.
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py``; never by the product package.
+
+Every function cites the reference file:line it restates (paths relative to the
+reference repository root). Where the reference leaves an order unspecified this
+module fixes the contract the HIP path must meet bit-exactly:
+
+* top-k slots are ordered by (biased score descending, expert index ascending);
+  NaN ranks above every number (as ``torch.topk`` does), NaNs tie by index;
+* the expert sort is stable by flat slot id ``t*k + j``.
+
+Pinning (what checks each function, all in ``tests/test_oracle.py``):
+
+* ``sigmoid_f32``          closed form at 0, symmetry p(x)+p(-x)=1, saturation.
+* ``route_topk``           brute force (pure-Python full sort) on tiny E; equal
+                           scores select 0..k-1; a huge bias forces selection while
+                           the weight keeps the unbiased p; b=0 gives top-k of p;
+                           weights sum to 1; NaN policy.
+* ``flatten_sort_count``   brute force ``sorted(range(R), key=(e, i))``;
+                           permutation; counts = histogram; inclusive offsets.
+* ``group``                direct indexing identity on random data.
+* ``scatter2scatter``      per-row dense loop (textbook matmul per row).
+* ``group_bwd_w``          per-row outer-product accumulation; empty expert = 0.
+* ``rowwise_sum_product``  einsum.
+* ``parallel_linear_*`` / ``glu_mlp_*`` / ``gate_*`` / ``moe_layer_*`` backward:
+                           torch autograd of an independent dense formulation and
+                           float64 central finite differences on tiny shapes.
+* ``bias_update``          closed form on a hand-built histogram.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "bf16_round",
+    "sigmoid_f32",
+    "route_topk",
+    "route_topk_backward",
+    "expert_counts",
+    "flatten_sort_count",
+    "inverse_permutation",
+    "group",
+    "scatter2scatter",
+    "group_bwd_w",
+    "rowwise_sum_product",
+    "parallel_linear_forward",
+    "parallel_linear_backward",
+    "glu_mlp_forward",
+    "glu_mlp_backward",
+    "swiglu",
+    "swiglu_backward",
+    "shared_expert_forward",
+    "shared_expert_backward",
+    "MoELayerOracle",
+    "bias_update",
+    "moe_load_metrics",
+]
+
+
+# --------------------------------------------------------------------------- #
+# numeric helpers
+# --------------------------------------------------------------------------- #
+def bf16_round(x):
+    """Round float32 values to the nearest bfloat16 (ties to even); returns float32.
+
+    This is the rounding ``tensor.to(torch.bfloat16)`` performs. NaN stays NaN.
+    """
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = x.view(np.uint32).astype(np.uint64)
+    lsb = (u >> np.uint64(16)) & np.uint64(1)
+    r = ((u + np.uint64(0x7FFF) + lsb) >> np.uint64(16)) << np.uint64(16)
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), x, out).astype(np.float32)
+
+
+def sigmoid_f32(logits):
+    """sigmoid evaluated in float64 and rounded once to float32.
+
+    Restates ``torch.sigmoid(gate_output)`` (modeling/moe_gate.py:27). The HIP
+    kernel evaluates the same float64 expression, so p agrees bit-for-bit.
+    """
+    z = np.asarray(logits, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        p = 1.0 / (1.0 + np.exp(-z))
+    return p.astype(np.float32)
+
+
+# --------------------------------------------------------------------------- #
+# a1: routing (modeling/moe_gate.py:19-36)
+# --------------------------------------------------------------------------- #
+def route_topk(logits, expert_biases, k, round_probs_bf16=False):
+    """Aux-loss-free sigmoid routing after the gate projection.
+
+    Restates modeling/moe_gate.py:26-34:
+      p = sigmoid(logits)                 (:27)
+      s = p + expert_biases               (:29, bias after the sigmoid, fp32)
+      idx = topk(s, k)                    (:30, selection only)
+      w = gather(p, idx)                  (:33, unbiased p)
+      w = w / max(sum(|w|), 1e-12)        (:34, F.normalize(p=1))
+
+    ``round_probs_bf16`` reproduces the reference under bf16 autocast, where the
+    sigmoid output is a bf16 tensor before the fp32 bias add.
+
+    Returns (idx int64 [T,k], weights float32 [T,k], p_selected float32 [T,k]).
+    """
+    logits = np.asarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    if not (0 < k <= E):
+        raise ValueError("k must be in [1, E]")
+    p = sigmoid_f32(logits)
+    if round_probs_bf16:
+        p = bf16_round(p)
+    s = (p + np.asarray(expert_biases, dtype=np.float32)[None, :]).astype(np.float32)
+    nan = np.isnan(s)
+    neg = np.where(nan, np.float32(0.0), -s)
+    e_idx = np.broadcast_to(np.arange(E), (T, E))
+    # np.lexsort: last key is primary. NaN first, then score desc, then index asc.
+    order = np.lexsort((e_idx, neg, ~nan), axis=-1)
+    idx = order[:, :k].astype(np.int64)
+    p_sel = np.take_along_axis(p, idx, axis=1).astype(np.float32)
+    denom = np.maximum(np.abs(p_sel.astype(np.float64)).sum(axis=1, keepdims=True), 1e-12)
+    w = (p_sel.astype(np.float64) / denom).astype(np.float32)
+    return idx, w, p_sel
+
+
+def route_topk_backward(d_weight, p_selected, idx, E):
+    """Gradient of the routing weights w.r.t. the gate logits (float64).
+
+    Autograd of modeling/moe_gate.py:27,33-34: through F.normalize(p=1)
+    (w_j = p_j / S, S = max(sum p, eps)), the gather, and the sigmoid
+    (dp/dz = p (1 - p)). Returns a dense [T, E] gradient (zero off the top-k).
+    """
+    dw = np.asarray(d_weight, dtype=np.float64)
+    p = np.asarray(p_selected, dtype=np.float64)
+    S_raw = np.abs(p).sum(axis=1, keepdims=True)
+    S = np.maximum(S_raw, 1e-12)
+    w = p / S
+    # d(p_j/S)/dp_i = delta_ij / S - p_j sign(p_i) / S^2  (only while S > eps)
+    inner = (dw * w).sum(axis=1, keepdims=True)
+    dp = np.where(S_raw > 1e-12, (dw - inner * np.sign(p)) / S, dw / S)
+    dz_sel = dp * p * (1.0 - p)
+    T = dw.shape[0]
+    dz = np.zeros((T, E), dtype=np.float64)
+    np.put_along_axis(dz, np.asarray(idx, dtype=np.int64), dz_sel, axis=1)
+    return dz
+
+
+# --------------------------------------------------------------------------- #
+# a3/a4: counts and the expert sort (scattermoe/parallel_experts.py:6-28)
+# --------------------------------------------------------------------------- #
+def expert_counts(expert_idxs, E):
+    """``compileable_bincount`` (scattermoe/parallel_experts.py:6-15): int64 [E]."""
+    flat = np.asarray(expert_idxs, dtype=np.int64).reshape(-1)
+    if flat.size and (flat.min() < 0 or flat.max() >= E):
+        raise ValueError("expert index out of range")
+    return np.bincount(flat, minlength=E).astype(np.int64)
+
+
+def flatten_sort_count(expert_idxs, E):
+    """scattermoe/parallel_experts.py:21-28.
+
+    sorted_expert_idxs, sorted_scattered_idxs = sort(expert_idxs.flatten())  (:25)
+    expert_offsets = cumsum(bincount)  inclusive ends, no leading zero      (:26-27)
+    The sort is stable: equal experts keep flat-slot order.
+    """
+    flat = np.asarray(expert_idxs, dtype=np.int64).reshape(-1)
+    counts = expert_counts(flat, E)
+    order = np.argsort(flat, kind="stable").astype(np.int64)
+    return flat[order], order, np.cumsum(counts).astype(np.int64)
+
+
+def inverse_permutation(sorted_scattered_idxs):
+    """inv[slot] = position of that slot in expert-sorted order."""
+    s = np.asarray(sorted_scattered_idxs, dtype=np.int64)
+    inv = np.empty_like(s)
+    inv[s] = np.arange(s.size, dtype=np.int64)
+    return inv
+
+
+# --------------------------------------------------------------------------- #
+# a5: group (scattermoe/kernels/ops.py:449-529)
+# --------------------------------------------------------------------------- #
+def group(A, sorted_idxs, coeff=None, fan_out=1):
+    """Y[n] = A[idx[n] // fan_out] * coeff[idx[n]]  (ops.py:504-519)."""
+    A = np.asarray(A, dtype=np.float64)
+    idx = np.asarray(sorted_idxs, dtype=np.int64)
+    Y = A[idx // fan_out]
+    if coeff is not None:
+        c = np.asarray(coeff, dtype=np.float64).reshape(-1)
+        Y = Y * c[idx][:, None]
+    return Y
+
+
+# --------------------------------------------------------------------------- #
+# a6: scatter2scatter (scattermoe/kernels/ops.py:122-255)
+# --------------------------------------------------------------------------- #
+def _expert_ranges(sorted_expert_idxs, E):
+    se = np.asarray(sorted_expert_idxs, dtype=np.int64)
+    ends = np.searchsorted(se, np.arange(E), side="right")
+    starts = np.concatenate([[0], ends[:-1]])
+    return starts, ends
+
+
+def scatter2scatter(X, W, sorted_expert_idxs, sorted_scattered_idxs, k, b=None,
+                    x_grouped=False, y_grouped=False):
+    """Grouped linear over expert-sorted rows (ops.py:144-190).
+
+    Sorted row i uses expert e = sorted_expert_idxs[i]; its input row is X[i] if
+    ``x_grouped`` else X[sorted_scattered_idxs[i] // k] (:165-168); its output row
+    is Y[i] if ``y_grouped`` else Y[sorted_scattered_idxs[i]] (:185-189).
+    ``W`` is the logical [E, K, N] operand (the reference passes
+    ``weight.permute(0, 2, 1)``); optional bias ``b`` [E, N] (:181-183).
+    """
+    X = np.asarray(X, dtype=np.float64)
+    W = np.asarray(W, dtype=np.float64)
+    se = np.asarray(sorted_expert_idxs, dtype=np.int64)
+    ss = np.asarray(sorted_scattered_idxs, dtype=np.int64)
+    R = se.size
+    E, _, N = W.shape
+    rows_in = np.arange(R) if x_grouped else ss // k
+    rows_out = np.arange(R) if y_grouped else ss
+    Y = np.zeros((R, N), dtype=np.float64)
+    starts, ends = _expert_ranges(se, E)
+    for e in range(E):
+        s, t = starts[e], ends[e]
+        if t <= s:
+            continue
+        blk = X[rows_in[s:t]] @ W[e]
+        if b is not None:
+            blk = blk + np.asarray(b, dtype=np.float64)[e][None, :]
+        Y[rows_out[s:t]] = blk
+    return Y
+
+
+# --------------------------------------------------------------------------- #
+# a7: group_bwd_W (scattermoe/kernels/ops.py:263-438)
+# --------------------------------------------------------------------------- #
+def group_bwd_w(DY, X, expert_offsets, E, has_bias=False):
+    """DW[e] = X[s_e:t_e]^T @ DY[s_e:t_e] over each expert's sorted row range.
+
+    ops.py:344-348 (range from inclusive offsets), :412-435 (accumulate), :264
+    (pre-zeroed, so an empty expert gets exactly 0). Returns DW [E, K, N] (the
+    logical view the reference returns) and Db [E, N] or None (:430-438).
+    """
+    DY = np.asarray(DY, dtype=np.float64)
+    X = np.asarray(X, dtype=np.float64)
+    off = np.asarray(expert_offsets, dtype=np.int64)
+    K, N = X.shape[1], DY.shape[1]
+    DW = np.zeros((E, K, N), dtype=np.float64)
+    Db = np.zeros((E, N), dtype=np.float64) if has_bias else None
+    start = 0
+    for e in range(E):
+        end = int(off[e])
+        if end > start:
+            DW[e] = X[start:end].T @ DY[start:end]
+            if has_bias:
+                Db[e] = DY[start:end].sum(axis=0)
+        start = end
+    return DW, Db
+
+
+# --------------------------------------------------------------------------- #
+# a8: rowwise_sum_product (scattermoe/kernels/ops.py:9-80)
+# --------------------------------------------------------------------------- #
+def rowwise_sum_product(A, B):
+    """out[t, j] = sum_h A[t, j, h] * B[t, h]  (ops.py:79)."""
+    return np.einsum("tjh,th->tj", np.asarray(A, dtype=np.float64), np.asarray(B, dtype=np.float64))
+
+
+# --------------------------------------------------------------------------- #
+# a9/a10: ParallelLinear (scattermoe/parallel_experts.py:32-135)
+# --------------------------------------------------------------------------- #
+def parallel_linear_forward(x, W, k, sorted_expert_idxs, sorted_scattered_idxs,
+                            expert_offsets, b=None, gates=None,
+                            grouped_in=False, grouped_out=False):
+    """ParallelLinear.forward (parallel_experts.py:34-68). W is logical [E, K, N].
+
+    Returns (output, output_expanded) where output_expanded is the [T, k, N]
+    per-slot output saved for backward when ``gates`` is given (:50-55).
+    """
+    out = scatter2scatter(x, W, sorted_expert_idxs, sorted_scattered_idxs, k, b=b,
+                          x_grouped=grouped_in, y_grouped=grouped_out)
+    if gates is None:
+        return out, None
+    g = np.asarray(gates, dtype=np.float64)
+    T, kk = g.shape
+    expanded = out.reshape(T, kk, out.shape[-1])
+    return np.einsum("tj,tjn->tn", g, expanded), expanded
+
+
+def parallel_linear_backward(grad_out, x, W, k, sorted_expert_idxs, sorted_scattered_idxs,
+                             expert_offsets, b=None, gates=None, output_expanded=None,
+                             grouped_in=False, grouped_out=False):
+    """ParallelLinear.backward (parallel_experts.py:70-135).
+
+    Returns (d_input, d_weights [E, K, N], d_biases or None, d_gates or None).
+    """
+    grad_out = np.asarray(grad_out, dtype=np.float64)
+    E = np.asarray(W).shape[0]
+    if gates is not None:
+        d_gates = rowwise_sum_product(output_expanded, grad_out)             # :82
+        gates_flat = np.asarray(gates, dtype=np.float64).reshape(-1)
+        gate_fan = np.asarray(gates).shape[1]
+    else:
+        d_gates, gates_flat, gate_fan = None, None, 1
+    if grouped_out:
+        grouped_grad_out = grad_out                                            # :93
+    else:
+        grouped_grad_out = group(grad_out, sorted_scattered_idxs,              # :95-97
+                                 coeff=gates_flat, fan_out=gate_fan)
+    grouped_x = x if grouped_in else group(x, sorted_scattered_idxs, fan_out=k)  # :98-103
+    d_w, d_b = group_bwd_w(grouped_grad_out, grouped_x, expert_offsets, E,       # :105-110
+                           has_bias=b is not None)
+    Wt = np.transpose(np.asarray(W, dtype=np.float64), (0, 2, 1))
+    d_exp = scatter2scatter(grouped_grad_out, Wt, sorted_expert_idxs,            # :112-120
+                            sorted_scattered_idxs, 1, x_grouped=True, y_grouped=grouped_in)
+    if k == 1:
+        d_input = d_exp
+    else:
+        d_input = d_exp.reshape(np.asarray(x).shape[0], k, -1).sum(axis=1)      # :125
+    return d_input, d_w, d_b, d_gates
+
+
+# --------------------------------------------------------------------------- #
+# a12: GLUMLP (scattermoe/mlp.py:51-95)
+# --------------------------------------------------------------------------- #
+def _silu(z):
+    return z / (1.0 + np.exp(-z))
+
+
+def swiglu(H):
+    """chunk(2) then silu(second half) * first half (mlp.py:81-87)."""
+    f = H.shape[-1] // 2
+    h, g = H[..., :f], H[..., f:]
+    return _silu(g) * h
+
+
+def swiglu_backward(dA, H):
+    """Gradient of swiglu w.r.t. H = [h | g]."""
+    f = H.shape[-1] // 2
+    h, g = H[..., :f], H[..., f:]
+    s = 1.0 / (1.0 + np.exp(-g))
+    dh = dA * g * s
+    dg = dA * h * s * (1.0 + g * (1.0 - s))
+    return np.concatenate([dh, dg], axis=-1)
+
+
+def glu_mlp_forward(x, expert_p, expert_idxs, W1, W2):
+    """GLUMLP.forward (mlp.py:74-95).
+
+    x [T, d]; expert_p, expert_idxs [T, k]; W1 [E, 2f, d] and W2 [E, d, f] in
+    ``nn.Parameter`` storage (the reference permutes them to [E, in, out]).
+    Returns (y [T, d], cache) with the tensors the reference saves.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    T, k = np.asarray(expert_idxs).shape
+    E = np.asarray(W1).shape[0]
+    se, ss, off = flatten_sort_count(expert_idxs, E)                          # :77-78
+    W1l = np.transpose(np.asarray(W1, dtype=np.float64), (0, 2, 1))
+    W2l = np.transpose(np.asarray(W2, dtype=np.float64), (0, 2, 1))
+    H, _ = parallel_linear_forward(x, W1l, k, se, ss, off, grouped_out=True)  # :79-84
+    A = swiglu(H)                                                             # :85-87
+    y, y_exp = parallel_linear_forward(A, W2l, 1, se, ss, off, gates=expert_p,  # :88-93
+                                       grouped_in=True)
+    cache = dict(x=x, se=se, ss=ss, off=off, H=H, A=A, y_exp=y_exp,
+                 gates=np.asarray(expert_p, dtype=np.float64), k=k, W1l=W1l, W2l=W2l)
+    return y, cache
+
+
+def glu_mlp_backward(dy, cache):
+    """Autograd of GLUMLP: returns (dx [T, d], dW1 [E, 2f, d], dW2 [E, d, f], d_gates [T, k])."""
+    c = cache
+    dA, dW2l, _, d_gates = parallel_linear_backward(
+        dy, c["A"], c["W2l"], 1, c["se"], c["ss"], c["off"], gates=c["gates"],
+        output_expanded=c["y_exp"], grouped_in=True)
+    dH = swiglu_backward(dA, c["H"])
+    dx, dW1l, _, _ = parallel_linear_backward(
+        dH, c["x"], c["W1l"], c["k"], c["se"], c["ss"], c["off"], grouped_out=True)
+    return dx, np.transpose(dW1l, (0, 2, 1)), np.transpose(dW2l, (0, 2, 1)), d_gates
+
+
+# --------------------------------------------------------------------------- #
+# a14: shared expert (modeling/expert_layer.py:23-24)
+# --------------------------------------------------------------------------- #
+def shared_expert_forward(x, Wg, Wu, Wd):
+    """down(silu(gate(x)) * up(x)) with nn.Linear weights [out, in]."""
+    x = np.asarray(x, dtype=np.float64)
+    g = x @ np.asarray(Wg, dtype=np.float64).T
+    u = x @ np.asarray(Wu, dtype=np.float64).T
+    a = _silu(g) * u
+    return a @ np.asarray(Wd, dtype=np.float64).T, (x, g, u, a)
+
+
+def shared_expert_backward(dy, cache, Wg, Wu, Wd):
+    x, g, u, a = cache
+    dy = np.asarray(dy, dtype=np.float64)
+    Wg = np.asarray(Wg, dtype=np.float64)
+    Wu = np.asarray(Wu, dtype=np.float64)
+    Wd = np.asarray(Wd, dtype=np.float64)
+    dWd = dy.T @ a
+    da = dy @ Wd
+    s = 1.0 / (1.0 + np.exp(-g))
+    du = da * g * s
+    dg = da * u * s * (1.0 + g * (1.0 - s))
+    dx = dg @ Wg + du @ Wu
+    return dx, dg.T @ x, du.T @ x, dWd
+
+
+# --------------------------------------------------------------------------- #
+# a13: MoELayer (modeling/moe_layer.py:38-59)
+# --------------------------------------------------------------------------- #
+class MoELayerOracle:
+    """Forward and backward of ``MoELayer`` on the valid tokens.
+
+    Parameters follow the reference state dict: gate ``weight [E, d]`` and
+    ``expert_biases [E]`` (moe_gate.py:12-13); ``W1 [E, 2f, d]``, ``W2 [E, d, f]``
+    (mlp.py:58-59); shared ``gate/up/down_proj`` (expert_layer.py:12-14), or
+    ``None`` for no shared expert.
+
+    ``logits`` may be supplied to forward() so the routing starts from exactly the
+    gate projection the device computed (the projection itself is checked with a
+    tolerance; routing from given logits is checked bit-exactly).
+    """
+
+    def __init__(self, Wgate, expert_biases, W1, W2, k, shared=None, round_probs_bf16=False):
+        self.Wgate = np.asarray(Wgate, dtype=np.float64)
+        self.bias = np.asarray(expert_biases, dtype=np.float32)
+        self.W1 = np.asarray(W1, dtype=np.float64)
+        self.W2 = np.asarray(W2, dtype=np.float64)
+        self.k = int(k)
+        self.shared = None if shared is None else tuple(np.asarray(w, dtype=np.float64) for w in shared)
+        self.round_probs_bf16 = round_probs_bf16
+
+    def forward(self, x, logits=None):
+        x = np.asarray(x, dtype=np.float64)
+        if logits is None:
+            logits = (x @ self.Wgate.T).astype(np.float32)                    # moe_gate.py:26
+        idx, w, p_sel = route_topk(logits, self.bias, self.k, self.round_probs_bf16)
+        y, mcache = glu_mlp_forward(x, w, idx, self.W1, self.W2)               # moe_layer.py:51
+        out = y
+        scache = None
+        if self.shared is not None:
+            ys, scache = shared_expert_forward(x, *self.shared)                # moe_layer.py:47
+            out = ys + y                                                       # moe_layer.py:53
+        self._cache = dict(x=x, idx=idx, w=w, p_sel=p_sel, mcache=mcache, scache=scache)
+        return out, idx, w
+
+    def backward(self, dout):
+        """Returns dict of float64 grads: x, gate_weight, W1, W2 (+ shared_*)."""
+        c = self._cache
+        dout = np.asarray(dout, dtype=np.float64)
+        dx, dW1, dW2, d_gates = glu_mlp_backward(dout, c["mcache"])
+        E = self.Wgate.shape[0]
+        dz = route_topk_backward(d_gates, c["p_sel"], c["idx"], E)
+        grads = {}
+        dx = dx + dz @ self.Wgate
+        grads["gate_weight"] = dz.T @ c["x"]
+        if self.shared is not None:
+            dxs, dWg, dWu, dWd = shared_expert_backward(dout, c["scache"], *self.shared)
+            dx = dx + dxs
+            grads.update(shared_gate=dWg, shared_up=dWu, shared_down=dWd)
+        grads.update(x=dx, W1=dW1, W2=dW2, d_gates=d_gates, d_logits=dz)
+        return grads
+
+
+# --------------------------------------------------------------------------- #
+# (f)-1: aux-loss-free bias update and load metrics
+# --------------------------------------------------------------------------- #
+def bias_update(expert_biases, topk_idx, E, update_rate):
+    """main.py:161-175: b += gamma * sign(mean(counts) - counts), in float32."""
+    counts = expert_counts(topk_idx, E).astype(np.float32)
+    if np.asarray(topk_idx).size == 0:
+        return np.asarray(expert_biases, dtype=np.float32).copy()
+    err = np.float32(counts.mean(dtype=np.float32)) - counts
+    return (np.asarray(expert_biases, dtype=np.float32)
+            + np.float32(update_rate) * np.sign(err).astype(np.float32)).astype(np.float32)
+
+
+def moe_load_metrics(topk_idx, E):
+    """utils/trainutils.py:124-135 per-layer metrics from the expert histogram."""
+    counts = expert_counts(topk_idx, E)
+    total = np.asarray(topk_idx).size
+    expected = total / E
+    return dict(
+        pct_experts_used=100.0 * float((counts > 0).sum()) / E,
+        load_imbalance=float(np.abs(counts / expected - 1.0).mean()),
+        max_expert_pct=float(counts.max()) * 100.0 / total,
+        min_expert_pct=float(counts.min()) * 100.0 / total,
+    )

@@ -1,0 +1,299 @@
+"""Pins the CPU oracle against brute force, closed forms, invariants, an
+independent torch-autograd formulation and float64 finite differences.
+
+The reference ships no tests or golden vectors for the MoE path, so each oracle
+function is pinned here by mathematics chosen so that a plausible mistake (a
+dropped term, a wrong sign or index, a transposed operand) fails a check.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# ----------------------------------------------------------------- numerics
+def test_bf16_round_matches_torch():
+    x = rng(1).standard_normal(4096).astype(np.float32) * 10
+    x[:4] = [0.0, -0.0, np.inf, -np.inf]
+    ref = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(O.bf16_round(x), ref)
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32)))[0]
+
+
+def test_sigmoid_closed_forms():
+    assert O.sigmoid_f32(np.array([0.0]))[0] == np.float32(0.5)
+    x = rng(2).standard_normal(1000) * 8
+    p, q = O.sigmoid_f32(x).astype(np.float64), O.sigmoid_f32(-x).astype(np.float64)
+    np.testing.assert_allclose(p + q, 1.0, atol=2e-7)
+    assert O.sigmoid_f32(np.array([-1000.0]))[0] == 0.0
+    assert O.sigmoid_f32(np.array([1000.0]))[0] == 1.0
+    # correctly rounded: agrees with float64 math.exp for a few values
+    for v in (0.25, -3.5, 7.0):
+        assert O.sigmoid_f32(np.array([v]))[0] == np.float32(1.0 / (1.0 + math.exp(-v)))
+
+
+# ----------------------------------------------------------------- routing
+def _brute_route(logits, bias, k, round_bf16=False):
+    T, E = logits.shape
+    p = O.sigmoid_f32(logits)
+    if round_bf16:
+        p = O.bf16_round(p)
+    s = (p + bias[None, :]).astype(np.float32)
+    idx = np.zeros((T, k), np.int64)
+    for t in range(T):
+        def key(e):
+            v = float(s[t, e])
+            return (0 if math.isnan(v) else 1, 0.0 if math.isnan(v) else -v, e)
+        order = sorted(range(E), key=key)
+        idx[t] = order[:k]
+    return idx, p
+
+
+@pytest.mark.parametrize("round_bf16", [False, True])
+def test_route_topk_brute_force(round_bf16):
+    r = rng(3)
+    T, E, k = 64, 7, 3
+    logits = r.standard_normal((T, E)).astype(np.float32)
+    logits[:8] = np.round(logits[:8])  # exact ties inside rows
+    bias = (r.standard_normal(E) * 0.1).astype(np.float32)
+    bias[:3] = 0.0
+    idx, w, p_sel = O.route_topk(logits, bias, k, round_probs_bf16=round_bf16)
+    bidx, p = _brute_route(logits, bias, k, round_bf16)
+    np.testing.assert_array_equal(idx, bidx)
+    np.testing.assert_array_equal(p_sel, np.take_along_axis(p, bidx, 1))
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=0, atol=k * 2e-7)
+    assert (w > 0).all()
+
+
+def test_route_equal_scores_pick_lowest_indices():
+    idx, w, _ = O.route_topk(np.zeros((5, 16), np.float32), np.zeros(16, np.float32), 4)
+    np.testing.assert_array_equal(idx, np.tile(np.arange(4), (5, 1)))
+    np.testing.assert_allclose(w, 0.25)
+
+
+def test_route_bias_selects_but_weight_uses_unbiased_p():
+    r = rng(4)
+    logits = r.standard_normal((10, 8)).astype(np.float32)
+    bias = np.zeros(8, np.float32)
+    bias[5] = 100.0
+    idx, w, p_sel = O.route_topk(logits, bias, 2)
+    assert (idx[:, 0] == 5).all()
+    p = O.sigmoid_f32(logits)
+    np.testing.assert_array_equal(p_sel[:, 0], p[:, 5])
+    # with b = 0 selection is the top-k of p
+    idx0, _, _ = O.route_topk(logits, np.zeros(8, np.float32), 2)
+    np.testing.assert_array_equal(np.sort(idx0, 1), np.sort(np.argsort(-p, 1, kind="stable")[:, :2], 1))
+
+
+def test_route_nan_ranks_first():
+    logits = np.zeros((1, 6), np.float32)
+    logits[0, 4] = np.nan
+    logits[0, 2] = 3.0
+    idx, _, _ = O.route_topk(logits, np.zeros(6, np.float32), 3)
+    np.testing.assert_array_equal(idx[0], [4, 2, 0])
+
+
+def test_route_backward_matches_autograd():
+    r = rng(5)
+    T, E, k = 12, 9, 3
+    logits = r.standard_normal((T, E))
+    idx, w, p_sel = O.route_topk(logits.astype(np.float32), np.zeros(E, np.float32), k)
+    dw = r.standard_normal((T, k))
+    z = torch.tensor(logits.astype(np.float32).astype(np.float64), requires_grad=True)
+    p = torch.sigmoid(z)
+    wt = torch.nn.functional.normalize(p.gather(1, torch.from_numpy(idx)), p=1, dim=-1)
+    (wt * torch.from_numpy(dw)).sum().backward()
+    # the oracle starts from float32 p; compare at float32 resolution
+    dz = O.route_topk_backward(dw, p_sel, idx, E)
+    np.testing.assert_allclose(dz, z.grad.numpy(), rtol=1e-5, atol=1e-6)
+
+
+# ----------------------------------------------------------------- sort / count
+def test_flatten_sort_count_brute_force():
+    r = rng(6)
+    T, k, E = 50, 4, 9
+    idx = np.stack([r.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+    se, ss, off = O.flatten_sort_count(idx, E)
+    flat = idx.reshape(-1)
+    order = sorted(range(flat.size), key=lambda i: (flat[i], i))
+    np.testing.assert_array_equal(ss, order)
+    np.testing.assert_array_equal(se, flat[order])
+    counts = [int((flat == e).sum()) for e in range(E)]
+    np.testing.assert_array_equal(off, np.cumsum(counts))
+    assert off[-1] == T * k
+    np.testing.assert_array_equal(np.sort(ss), np.arange(T * k))
+    inv = O.inverse_permutation(ss)
+    np.testing.assert_array_equal(ss[inv], np.arange(T * k))
+
+
+def test_counts_reject_out_of_range():
+    with pytest.raises(ValueError):
+        O.expert_counts(np.array([0, 5]), 5)
+
+
+# ----------------------------------------------------------------- group / gemm
+def test_group_identity():
+    r = rng(7)
+    A = r.standard_normal((6, 5))
+    idx = r.permutation(12)
+    c = r.standard_normal(12)
+    Y = O.group(A, idx, coeff=c, fan_out=2)
+    for n in range(12):
+        np.testing.assert_allclose(Y[n], A[idx[n] // 2] * c[idx[n]])
+
+
+@pytest.mark.parametrize("xg,yg", [(False, True), (True, False), (True, True), (False, False)])
+def test_scatter2scatter_rowwise_loop(xg, yg):
+    r = rng(8)
+    T, k, E, K, N = 11, 2, 4, 6, 5
+    idx = np.stack([r.choice(E, k, replace=False) for _ in range(T)])
+    se, ss, _ = O.flatten_sort_count(idx, E)
+    X = r.standard_normal((T * k if xg else T, K))
+    W = r.standard_normal((E, K, N))
+    b = r.standard_normal((E, N))
+    Y = O.scatter2scatter(X, W, se, ss, k, b=b, x_grouped=xg, y_grouped=yg)
+    for i in range(T * k):
+        xin = X[i] if xg else X[ss[i] // k]
+        row = i if yg else ss[i]
+        ref = np.array([sum(xin[q] * W[se[i], q, n] for q in range(K)) + b[se[i], n] for n in range(N)])
+        np.testing.assert_allclose(Y[row], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_group_bwd_w_outer_products_and_empty_expert():
+    r = rng(9)
+    E, K, N = 5, 3, 4
+    counts = np.array([3, 0, 2, 4, 0])
+    off = np.cumsum(counts)
+    M = off[-1]
+    X, DY = r.standard_normal((M, K)), r.standard_normal((M, N))
+    DW, Db = O.group_bwd_w(DY, X, off, E, has_bias=True)
+    start = 0
+    for e in range(E):
+        ref = np.zeros((K, N))
+        for i in range(start, off[e]):
+            ref += np.outer(X[i], DY[i])
+        np.testing.assert_allclose(DW[e], ref, atol=1e-12)
+        start = off[e]
+    assert not DW[1].any() and not DW[4].any() and not Db[1].any()
+
+
+def test_rowwise_sum_product():
+    r = rng(10)
+    A, B = r.standard_normal((4, 3, 7)), r.standard_normal((4, 7))
+    out = O.rowwise_sum_product(A, B)
+    for t in range(4):
+        for j in range(3):
+            assert abs(out[t, j] - sum(A[t, j, h] * B[t, h] for h in range(7))) < 1e-12
+
+
+# ----------------------------------------------------------------- layer backward
+def _tiny_layer(seed, shared=True, T=6, d=8, E=4, k=2, f=4, fs=4):
+    r = rng(seed)
+    P = dict(
+        x=r.standard_normal((T, d)),
+        Wg=r.standard_normal((E, d)) * 0.5,
+        bias=(r.standard_normal(E) * 0.1).astype(np.float32),
+        W1=r.standard_normal((E, 2 * f, d)) / math.sqrt(d),
+        W2=r.standard_normal((E, d, f)) / math.sqrt(f),
+        shared=(r.standard_normal((fs, d)) / math.sqrt(d), r.standard_normal((fs, d)) / math.sqrt(d),
+                r.standard_normal((d, fs)) / math.sqrt(fs)) if shared else None,
+        k=k,
+    )
+    return P
+
+
+def _torch_dense_layer(P, idx):
+    """Independent dense formulation (per-token loop) for torch autograd."""
+    t = lambda a: torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    x, Wg, W1, W2 = t(P["x"]), t(P["Wg"]), t(P["W1"]), t(P["W2"])
+    shared = [t(w) for w in P["shared"]] if P["shared"] is not None else None
+    p = torch.sigmoid((x @ Wg.T).float().double())
+    sel = torch.from_numpy(idx)
+    w = torch.nn.functional.normalize(p.gather(1, sel), p=1, dim=-1)
+    f = W1.shape[1] // 2
+    rows = []
+    for ti in range(x.shape[0]):
+        acc = 0
+        for j in range(idx.shape[1]):
+            e = int(idx[ti, j])
+            hg = W1[e] @ x[ti]
+            a = torch.nn.functional.silu(hg[f:]) * hg[:f]
+            acc = acc + w[ti, j] * (W2[e] @ a)
+        rows.append(acc)
+    out = torch.stack(rows)
+    if shared is not None:
+        g, u, dn = shared
+        out = out + (torch.nn.functional.silu(x @ g.T) * (x @ u.T)) @ dn.T
+    return out, (x, Wg, W1, W2, shared)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_layer_forward_backward_vs_torch_autograd(shared):
+    P = _tiny_layer(11, shared=shared)
+    orc = O.MoELayerOracle(P["Wg"], P["bias"], P["W1"], P["W2"], P["k"], shared=P["shared"])
+    # route from float32 logits computed identically on both sides
+    logits = (P["x"] @ P["Wg"].T).astype(np.float32)
+    out, idx, _ = orc.forward(P["x"], logits=logits)
+    dout = rng(12).standard_normal(out.shape)
+    g = orc.backward(dout)
+    tout, (x, Wg, W1, W2, sh) = _torch_dense_layer(P, idx)
+    np.testing.assert_allclose(out, tout.detach().numpy(), rtol=1e-6, atol=1e-6)
+    (tout * torch.from_numpy(dout)).sum().backward()
+    # The oracle's p is float32-rounded; the torch path rounds logits to float32 too.
+    tol = dict(rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(g["W1"], W1.grad.numpy(), **tol)
+    np.testing.assert_allclose(g["W2"], W2.grad.numpy(), **tol)
+    np.testing.assert_allclose(g["x"], x.grad.numpy(), **tol)
+    np.testing.assert_allclose(g["gate_weight"], Wg.grad.numpy(), **tol)
+    if shared:
+        np.testing.assert_allclose(g["shared_gate"], sh[0].grad.numpy(), **tol)
+        np.testing.assert_allclose(g["shared_up"], sh[1].grad.numpy(), **tol)
+        np.testing.assert_allclose(g["shared_down"], sh[2].grad.numpy(), **tol)
+
+
+def test_glu_mlp_finite_differences():
+    """Central differences of the routed experts in float64 (routing held fixed)."""
+    P = _tiny_layer(13, shared=False, T=4, d=5, E=3, k=2, f=3)
+    r = rng(14)
+    idx = np.stack([r.choice(3, 2, replace=False) for _ in range(4)])
+    gates = r.random((4, 2)) + 0.1
+    dy = r.standard_normal((4, 5))
+
+    def loss(x, W1, W2, gates):
+        y, _ = O.glu_mlp_forward(x, gates, idx, W1, W2)
+        return float((y * dy).sum())
+
+    y, cache = O.glu_mlp_forward(P["x"], gates, idx, P["W1"], P["W2"])
+    dx, dW1, dW2, dg = O.glu_mlp_backward(dy, cache)
+    eps = 1e-6
+    args = dict(x=P["x"].copy(), W1=P["W1"].copy(), W2=P["W2"].copy(), gates=gates.copy())
+    for name, analytic in (("x", dx), ("W1", dW1), ("W2", dW2), ("gates", dg)):
+        a = args[name]
+        flat = a.reshape(-1)
+        for q in r.choice(flat.size, min(12, flat.size), replace=False):
+            old = flat[q]
+            flat[q] = old + eps
+            lp = loss(**args)
+            flat[q] = old - eps
+            lm = loss(**args)
+            flat[q] = old
+            num = (lp - lm) / (2 * eps)
+            assert abs(num - analytic.reshape(-1)[q]) < 1e-6 * max(1.0, abs(num)), (name, q)
+
+
+# ----------------------------------------------------------------- bias update
+def test_bias_update_closed_form():
+    idx = np.array([[0, 1], [0, 2], [0, 1]])  # counts [3, 2, 1, 0], mean 1.5
+    b = O.bias_update(np.zeros(4, np.float32), idx, 4, 1e-3)
+    np.testing.assert_array_equal(b, np.array([-1e-3, -1e-3, 1e-3, 1e-3], np.float32))
+    m = O.moe_load_metrics(idx, 4)
+    assert m["pct_experts_used"] == 75.0 and m["max_expert_pct"] == 50.0 and m["min_expert_pct"] == 0.0
+    assert abs(m["load_imbalance"] - np.mean(np.abs(np.array([3, 2, 1, 0]) / 1.5 - 1))) < 1e-12
