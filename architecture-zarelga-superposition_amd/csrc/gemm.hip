@@ -1,0 +1,885 @@
+// Grouped expert GEMMs for gfx950 (scattermoe/kernels/ops.py:122-255 and
+// :263-438, plus the fused SwiGLU forward/backward of scattermoe/mlp.py:96-102).
+//
+// Two kernels share one tile machinery:
+//   * grouped_rows_kernel:  C[i, :] = A(i, :) @ B_e   for the sorted rows i of
+//     expert e (forward and input-grad GEMMs). Tiles never straddle experts: the
+//     M tiles of each expert are laid out back to back, so boundary rows cost at
+//     most one partial tile per expert instead of a K-loop per expert present.
+//   * grouped_wgrad_kernel: C_e[m, n] = sum_{i in e} DY[i, m] X(i)[n]  (weight grads).
+//
+// Tile machinery (256 threads = 4 waves in a 2x2 grid, BM x BN tile):
+//   * LDS holds both operands as [rows][128 bytes] with the reduction dimension
+//     contiguous (64 bf16 or 32 f32 per row), 16-byte chunks XOR-swizzled by
+//     ((row>>1) ^ (row>>3)) & 7 so that MFMA fragment reads and both store
+//     patterns are bank-conflict free. Two stages; the next tile's global loads
+//     are issued before the current tile's MFMAs and written to the other stage
+//     afterwards, one barrier per K step.
+//   * Operands whose reduction dimension is contiguous in HBM (x rows, nn.Linear
+//     weights) are copied chunk by chunk. Operands whose reduction dimension is
+//     strided (weights read transposed, and both wgrad operands) are loaded as
+//     VEC x VEC blocks and transposed in registers (v_perm_b32 for bf16).
+//   * bf16: v_mfma_f32_32x32x16_bf16; f32: 4 x v_mfma_f32_32x32x2f32 per chunk.
+//     The B tile is fed as the MFMA's first operand, so each lane ends up holding
+//     4 consecutive output columns of one output row.
+//   * Epilogue: accumulators go through LDS (rounded to the output type, as the
+//     reference stores its GEMM outputs) and leave as coalesced 16-byte stores
+//     to grouped or scattered rows, optionally through SwiGLU or its backward.
+//   * Workgroup -> tile: XCD-aware. Workgroup b runs on XCD b % 8; each XCD takes
+//     a contiguous range of the (expert, m-tile, n-tile) sequence so that tiles
+//     sharing an expert's weights and rows run on one XCD and share its L2.
+#include "zmoe_internal.h"
+
+namespace zmoe {
+
+constexpr int kGemmThreads = 256;
+constexpr int kRowBytes = 128;
+constexpr int kGemmMaxE = 1024;
+constexpr int kXcds = 8;
+
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2 };
+
+__device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
+  return (uint32_t)(row * kRowBytes + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 7)) << 4));
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int w) {
+  return w == 0 ? v.x : (w == 1 ? v.y : (w == 2 ? v.z : v.w));
+}
+
+// 8x8 bf16 transpose: in[r] holds columns 0..7 of row r; out[c] holds rows 0..7 of column c.
+__device__ __forceinline__ void transpose_block(const uint4 (&in)[8], uint4 (&out)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+    const int w = c >> 1;
+    out[c].x = __builtin_amdgcn_perm(word_of(in[1], w), word_of(in[0], w), sel);
+    out[c].y = __builtin_amdgcn_perm(word_of(in[3], w), word_of(in[2], w), sel);
+    out[c].z = __builtin_amdgcn_perm(word_of(in[5], w), word_of(in[4], w), sel);
+    out[c].w = __builtin_amdgcn_perm(word_of(in[7], w), word_of(in[6], w), sel);
+  }
+}
+// 4x4 f32 transpose.
+__device__ __forceinline__ void transpose_block(const uint4 (&in)[4], uint4 (&out)[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    out[c].x = word_of(in[0], c);
+    out[c].y = word_of(in[1], c);
+    out[c].z = word_of(in[2], c);
+    out[c].w = word_of(in[3], c);
+  }
+}
+
+__device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void sts16(char* lds, uint32_t off, const uint4& v) {
+  *reinterpret_cast<uint4*>(lds + off) = v;
+}
+__device__ __forceinline__ uint4 lds16(const char* lds, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(lds + off);
+}
+
+// ------------------------------------------------------------------ MFMA core
+template <typename T> struct Mma;
+
+template <> struct Mma<uint16_t> {
+  static constexpr int VEC = 8;
+  template <int MI, int NI>
+  __device__ __forceinline__ static void step(const char* la, const char* lb, int wm0, int wn0,
+                                              f32x16_t (&acc)[MI][NI]) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8_t a[MI], b[NI];
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+        a[mi] = __builtin_bit_cast(bf16x8_t, lds16(la, lds_off(wm0 + mi * 32 + r, 2 * s + g)));
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        b[ni] = __builtin_bit_cast(bf16x8_t, lds16(lb, lds_off(wn0 + ni * 32 + r, 2 * s + g)));
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[ni], a[mi], acc[mi][ni], 0, 0, 0);
+    }
+  }
+};
+
+template <> struct Mma<float> {
+  static constexpr int VEC = 4;
+  template <int MI, int NI>
+  __device__ __forceinline__ static void step(const char* la, const char* lb, int wm0, int wn0,
+                                              f32x16_t (&acc)[MI][NI]) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      f32x4_t a[MI], b[NI];
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+        a[mi] = __builtin_bit_cast(f32x4_t, lds16(la, lds_off(wm0 + mi * 32 + r, 2 * s + g)));
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        b[ni] = __builtin_bit_cast(f32x4_t, lds16(lb, lds_off(wn0 + ni * 32 + r, 2 * s + g)));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ni][j], a[mi][j], acc[mi][ni], 0, 0, 0);
+    }
+  }
+};
+
+// ------------------------------------------------------------------ operand loaders
+// Rows operand: ROWS rows x 8 chunks, reduction dim contiguous in HBM.
+// Thread t owns chunk column t & 7 of rows (t >> 3) + 32 j.
+template <typename T, int ROWS>
+struct RowsOperand {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int NJ = ROWS / 32;
+  const T* ptr[NJ];  // row base + chunk column offset, or null for rows past the tile
+  uint4 reg[NJ];
+
+  __device__ __forceinline__ void load(int k0, int K) {
+    const int kc = k0 + (threadIdx.x & 7) * VEC;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (ptr[j] != nullptr && kc < K) reg[j] = ldg16(ptr[j] + k0);
+      else reg[j] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void store(char* lds) const {
+    const int c = threadIdx.x & 7;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) sts16(lds, lds_off((threadIdx.x >> 3) + 32 * j, c), reg[j]);
+  }
+};
+
+// Transposed operand: a [8*VEC reduction rows] x [COLS] tile whose COLS are
+// contiguous in HBM. Block (mb, kg) = VEC reduction rows x VEC columns.
+template <typename T, int COLS>
+struct TransOperand {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int MB = COLS / VEC;
+  static constexpr int NBLK = MB * 8;
+  static constexpr int NB = (NBLK + kGemmThreads - 1) / kGemmThreads;
+  uint4 reg[NB][VEC];
+
+  __device__ __forceinline__ static int blk(int q) { return (int)threadIdx.x + q * kGemmThreads; }
+
+  // row_ptr(kr) -> pointer to column 0 of reduction row kr (kr relative to the tile), or null
+  template <typename RowPtr>
+  __device__ __forceinline__ void load(RowPtr row_ptr, int col0, int ncols) {
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int b = blk(q);
+      const int mb = b % MB, kg = b / MB;
+      const int col = col0 + mb * VEC;
+      const bool colok = (NBLK % kGemmThreads == 0 || b < NBLK) && col < ncols;
+#pragma unroll
+      for (int rr = 0; rr < VEC; ++rr) {
+        const T* p = colok ? row_ptr(kg * VEC + rr) : nullptr;
+        reg[q][rr] = p != nullptr ? ldg16(p + col) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(char* lds) const {
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int b = blk(q);
+      if (NBLK % kGemmThreads != 0 && b >= NBLK) continue;
+      const int mb = b % MB, kg = b / MB;
+      uint4 t[VEC];
+      transpose_block(reg[q], t);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) sts16(lds, lds_off(mb * VEC + c, kg), t[c]);
+    }
+  }
+};
+
+// ------------------------------------------------------------------ block scan
+__device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kGemmThreads / 64; ++w) {
+    const int t = tmp[w];
+    if (w < wave) base += t;
+    tot += t;
+  }
+  *total = tot;
+  return base + x - v;
+}
+
+// tstart[e] = first m-tile of expert e (tiles of BM rows, back to back); tstart[E] = total.
+template <int BM>
+__device__ int build_tile_starts(const int64_t* __restrict__ off, int E, int* tstart, int* tmp) {
+  const int ept = (E + kGemmThreads - 1) / kGemmThreads;  // <= 4
+  const int e0 = threadIdx.x * ept;
+  int nt[4] = {0, 0, 0, 0};
+  int local = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = e0 + q;
+    if (q < ept && e < E) {
+      const int64_t a = e ? off[e - 1] : 0;
+      int64_t c = off[e] - a;
+      c = c < 0 ? 0 : c;
+      nt[q] = (int)((c + BM - 1) / BM);
+      local += nt[q];
+    }
+  }
+  int total;
+  int run = block_exclusive_scan(local, tmp, &total);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = e0 + q;
+    if (q < ept && e < E) {
+      tstart[e] = run;
+      run += nt[q];
+    }
+  }
+  if (threadIdx.x == 0) tstart[E] = total;
+  __syncthreads();
+  return total;
+}
+
+// Logical tile of this workgroup under the XCD-aware mapping, or -1.
+__device__ __forceinline__ int xcd_logical_tile(int total) {
+  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+  const int chunk = (total + kXcds - 1) / kXcds;
+  const int logical = xcd * chunk + slot;
+  return (slot < chunk && logical < total) ? logical : -1;
+}
+
+// ------------------------------------------------------------------ params
+struct RowsParams {
+  const void* a;
+  int64_t lda;
+  const int64_t* a_rows;  // gather: A row of sorted row i = a_rows[i] / a_div (null: i)
+  int a_div;
+  const void* b;
+  int64_t b_estride, ldb;
+  void* c;
+  int64_t ldc;
+  const int64_t* c_rows;  // scatter: output row of sorted row i = c_rows[i] (null: i)
+  void* c2;               // SwiGLU activation output
+  int64_t ldc2;
+  const void* aux;        // H for the SwiGLU backward
+  int64_t ld_aux;
+  const void* bias;       // [E, N] or null
+  int64_t bias_estride;
+  const int64_t* offsets; // inclusive expert ends [E]
+  int K, N, E;
+  int half;               // SwiGLU pair width f
+  int n_tiles;
+};
+
+struct WgradParams {
+  const void* dy;
+  int64_t lddy;
+  const void* x;
+  int64_t ldx;
+  const int64_t* x_rows;
+  int x_div;
+  void* dw;  // [E, Ndy, Kx]
+  const int64_t* offsets;
+  int Ndy, Kx, E;
+  int m_tiles, n_tiles;
+};
+
+// ------------------------------------------------------------------ epilogue helpers
+template <typename T, int WM, int WN>
+struct Stage {
+  static constexpr int PITCH = WN * (int)sizeof(T) + 16;  // bytes per staged row
+  static constexpr int BYTES = WM * PITCH;                // per wave
+};
+
+// Write this wave's accumulators (plus optional bias) into its staging area.
+template <typename T, int MI, int NI>
+__device__ __forceinline__ void stage_acc(char* st, int pitch, const f32x16_t (&acc)[MI][NI], const T* bias_row,
+                                          int col0, int N) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = mi * 32 + r;
+        const int col = ni * 32 + 8 * q + 4 * g;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          v[u] = acc[mi][ni][4 * q + u];
+          if (bias_row != nullptr && col0 + col + u < N) v[u] += to_f32(bias_row[col0 + col + u]);
+        }
+        char* p = st + row * pitch + col * (int)sizeof(T);
+        if constexpr (sizeof(T) == 2) {
+          uint2 w;
+          w.x = pack_bf16x2(v[0], v[1]);
+          w.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(p) = w;
+        } else {
+          *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+}
+
+// ------------------------------------------------------------------ rows kernel
+template <typename T, int BM, int BN, bool B_KN, int EPI>
+__global__ __launch_bounds__(kGemmThreads) void grouped_rows_kernel(RowsParams p) {
+  extern __shared__ __align__(16) char smem[];
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int BK = 8 * VEC;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MI = WM / 32, NI = WN / 32;
+  static_assert(EPI != EPI_SWIGLU || WN % 64 == 0, "SwiGLU pairs 32-column blocks inside a wave");
+
+  // ---- tile decode
+  int* tstart = reinterpret_cast<int*>(smem);
+  int* tmp = tstart + kGemmMaxE + 4;
+  const int mtiles = build_tile_starts<BM>(p.offsets, p.E, tstart, tmp);
+  const int logical = xcd_logical_tile(mtiles * p.n_tiles);
+  if (logical < 0) return;  // uniform per workgroup
+  const int mt = logical / p.n_tiles, nt = logical % p.n_tiles;
+  int lo = 0, hi = p.E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tstart[mid] <= mt) lo = mid;
+    else hi = mid - 1;
+  }
+  const int e = lo;
+  const int64_t e_begin = e ? p.offsets[e - 1] : 0;
+  const int64_t row0 = e_begin + (int64_t)(mt - tstart[e]) * BM;
+  const int rows = (int)min((int64_t)BM, p.offsets[e] - row0);
+  __syncthreads();  // tstart is dead; LDS becomes operand stages
+
+  constexpr int kStage = (BM + BN) * kRowBytes;
+  auto stage_a = [&](int st) { return smem + st * kStage; };
+  auto stage_b = [&](int st) { return smem + st * kStage + BM * kRowBytes; };
+
+  const T* A = reinterpret_cast<const T*>(p.a);
+  const T* Bw = reinterpret_cast<const T*>(p.b) + (int64_t)e * p.b_estride;
+
+  // ---- A operand (gathered rows)
+  RowsOperand<T, BM> opa;
+#pragma unroll
+  for (int j = 0; j < BM / 32; ++j) {
+    const int r = (threadIdx.x >> 3) + 32 * j;
+    if (r < rows) {
+      const int64_t i = row0 + r;
+      const int64_t src = p.a_rows ? p.a_rows[i] / p.a_div : i;
+      opa.ptr[j] = A + src * p.lda + (threadIdx.x & 7) * VEC;
+    } else {
+      opa.ptr[j] = nullptr;
+    }
+  }
+
+  // ---- B operand (expert weights)
+  RowsOperand<T, B_KN ? 32 : BN> opb_rows;
+  TransOperand<T, B_KN ? BN : 32> opb_t;
+  if constexpr (!B_KN) {
+#pragma unroll
+    for (int j = 0; j < BN / 32; ++j) {
+      const int r = (threadIdx.x >> 3) + 32 * j;
+      int n;
+      bool ok;
+      if constexpr (EPI == EPI_SWIGLU) {
+        // B row r -> W1 row: 64-row pair blocks [up 32 | gate 32] of the tile's pair columns
+        const int jj = nt * (BN / 2) + (r >> 6) * 32 + (r & 31);
+        ok = jj < p.half;
+        n = (r & 32) ? p.half + jj : jj;
+      } else {
+        n = nt * BN + r;
+        ok = n < p.N;
+      }
+      opb_rows.ptr[j] = ok ? Bw + (int64_t)n * p.ldb + (threadIdx.x & 7) * VEC : nullptr;
+    }
+  }
+  const int ncol0 = nt * BN;
+  auto b_row_ptr = [&](int k0) {
+    return [=](int kr) -> const T* {
+      const int kk = k0 + kr;
+      return kk < p.K ? Bw + (int64_t)kk * p.ldb : nullptr;
+    };
+  };
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+
+  const int nk = (p.K + BK - 1) / BK;
+  // prologue
+  opa.load(0, p.K);
+  if constexpr (B_KN) opb_t.load(b_row_ptr(0), ncol0, p.N);
+  else opb_rows.load(0, p.K);
+  opa.store(stage_a(0));
+  if constexpr (B_KN) opb_t.store(stage_b(0));
+  else opb_rows.store(stage_b(0));
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      const int k1 = (kt + 1) * BK;
+      opa.load(k1, p.K);
+      if constexpr (B_KN) opb_t.load(b_row_ptr(k1), ncol0, p.N);
+      else opb_rows.load(k1, p.K);
+    }
+    Mma<T>::template step<MI, NI>(stage_a(cur), stage_b(cur), wm0, wn0, acc);
+    if (more) {
+      opa.store(stage_a(cur ^ 1));
+      if constexpr (B_KN) opb_t.store(stage_b(cur ^ 1));
+      else opb_rows.store(stage_b(cur ^ 1));
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue
+  using S = Stage<T, WM, WN>;
+  char* st = smem + wave * S::BYTES;
+  const T* bias_row = (EPI == EPI_STORE && p.bias) ? reinterpret_cast<const T*>(p.bias) + e * p.bias_estride : nullptr;
+  stage_acc<T, MI, NI>(st, S::PITCH, acc, bias_row, ncol0 + wn0, p.N);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  T* C = reinterpret_cast<T*>(p.c);
+  if constexpr (EPI == EPI_STORE) {
+    constexpr int CPR = WN / VEC;  // chunks per staged row
+    for (int idx = lane; idx < WM * CPR; idx += 64) {
+      const int rr = idx / CPR, cc = idx % CPR;
+      const int r = wm0 + rr;
+      const int col = ncol0 + wn0 + cc * VEC;
+      if (r < rows && col < p.N) {
+        const int64_t i = row0 + r;
+        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) =
+            *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    // staged cols: per 64-col pair block pb: [h 32 | g 32] for pair columns jj0 + pb*32 + 0..31
+    constexpr int PB = WN / 64;
+    constexpr int CPP = 32 / VEC;  // chunks per 32 columns
+    T* A2 = reinterpret_cast<T*>(p.c2);
+    for (int idx = lane; idx < WM * PB * CPP; idx += 64) {
+      const int rr = idx / (PB * CPP);
+      const int rem = idx % (PB * CPP);
+      const int pb = rem / CPP, cc = rem % CPP;
+      const int r = wm0 + rr;
+      const int jj = nt * (BN / 2) + (wn0 / 64 + pb) * 32 + cc * VEC;
+      if (r < rows && jj < p.half) {
+        const int64_t i = row0 + r;
+        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
+        const uint4 hv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + cc * VEC) * (int)sizeof(T));
+        const uint4 gv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + 32 + cc * VEC) * (int)sizeof(T));
+        float h[VEC], g[VEC], a[VEC];
+        unpack_chunk(hv, h, T{});
+        unpack_chunk(gv, g, T{});
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) a[q] = silu_f(g[q]) * h[q];
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + jj) = hv;
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + jj) = gv;
+        *reinterpret_cast<uint4*>(A2 + orow * p.ldc2 + jj) = pack_chunk(a, T{});
+      }
+    }
+  } else {  // EPI_SWIGLU_BWD: staged dA for columns ncol0 + wn0 + ...
+    constexpr int CPR = WN / VEC;
+    const T* Hs = reinterpret_cast<const T*>(p.aux);
+    for (int idx = lane; idx < WM * CPR; idx += 64) {
+      const int rr = idx / CPR, cc = idx % CPR;
+      const int r = wm0 + rr;
+      const int col = ncol0 + wn0 + cc * VEC;
+      if (r < rows && col < p.N) {
+        const int64_t i = row0 + r;
+        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
+        float da[VEC], h[VEC], g[VEC], dh[VEC], dg[VEC];
+        unpack_chunk(*reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16), da, T{});
+        unpack_chunk(ldg16(Hs + i * p.ld_aux + col), h, T{});
+        unpack_chunk(ldg16(Hs + i * p.ld_aux + p.half + col), g, T{});
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const float s = sigmoid_fast(g[q]);
+          dh[q] = da[q] * g[q] * s;
+          dg[q] = da[q] * h[q] * s * (1.f + g[q] * (1.f - s));
+        }
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = pack_chunk(dh, T{});
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + col) = pack_chunk(dg, T{});
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ wgrad kernel
+template <typename T, int BM, int BN>
+__global__ __launch_bounds__(kGemmThreads) void grouped_wgrad_kernel(WgradParams p) {
+  extern __shared__ __align__(16) char smem[];
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int BK = 8 * VEC;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MI = WM / 32, NI = WN / 32;
+
+  const int per_e = p.m_tiles * p.n_tiles;
+  const int logical = xcd_logical_tile(p.E * per_e);
+  if (logical < 0) return;
+  const int e = logical / per_e;
+  const int rem = logical % per_e;
+  const int mt = rem / p.n_tiles, nt = rem % p.n_tiles;
+  const int64_t r_begin = e ? p.offsets[e - 1] : 0;
+  const int64_t r_end = p.offsets[e];
+  const int64_t nrows = r_end > r_begin ? r_end - r_begin : 0;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  constexpr int kStage = (BM + BN) * kRowBytes;
+  auto stage_a = [&](int st) { return smem + st * kStage; };
+  auto stage_b = [&](int st) { return smem + st * kStage + BM * kRowBytes; };
+
+  const T* DY = reinterpret_cast<const T*>(p.dy);
+  const T* X = reinterpret_cast<const T*>(p.x);
+  TransOperand<T, BM> opa;
+  TransOperand<T, BN> opb;
+  auto dy_rows = [&](int64_t k0) {
+    return [=](int kr) -> const T* {
+      const int64_t rr = k0 + kr;
+      return rr < nrows ? DY + (r_begin + rr) * p.lddy : nullptr;
+    };
+  };
+  auto x_rows = [&](int64_t k0) {
+    return [=](int kr) -> const T* {
+      const int64_t rr = k0 + kr;
+      if (rr >= nrows) return nullptr;
+      const int64_t i = r_begin + rr;
+      const int64_t src = p.x_rows ? p.x_rows[i] / p.x_div : i;
+      return X + src * p.ldx;
+    };
+  };
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+
+  const int nk = (int)((nrows + BK - 1) / BK);
+  if (nk > 0) {
+    opa.load(dy_rows(0), m0, p.Ndy);
+    opb.load(x_rows(0), n0, p.Kx);
+    opa.store(stage_a(0));
+    opb.store(stage_b(0));
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      const bool more = kt + 1 < nk;
+      if (more) {
+        const int64_t k1 = (int64_t)(kt + 1) * BK;
+        opa.load(dy_rows(k1), m0, p.Ndy);
+        opb.load(x_rows(k1), n0, p.Kx);
+      }
+      Mma<T>::template step<MI, NI>(stage_a(cur), stage_b(cur), wm0, wn0, acc);
+      if (more) {
+        opa.store(stage_a(cur ^ 1));
+        opb.store(stage_b(cur ^ 1));
+      }
+      __syncthreads();
+    }
+  }
+
+  using S = Stage<T, WM, WN>;
+  char* st = smem + wave * S::BYTES;
+  stage_acc<T, MI, NI>(st, S::PITCH, acc, nullptr, 0, 0);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  T* DW = reinterpret_cast<T*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
+  constexpr int CPR = WN / VEC;
+  for (int idx = lane; idx < WM * CPR; idx += 64) {
+    const int rr = idx / CPR, cc = idx % CPR;
+    const int m = m0 + wm0 + rr;
+    const int n = n0 + wn0 + cc * VEC;
+    if (m < p.Ndy && n < p.Kx)
+      *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) =
+          *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+  }
+}
+
+// Db[e, n] = sum over the expert's rows of DY[i, n] (bias grad, off the GLU path).
+template <typename T>
+__global__ void bias_grad_kernel(const T* __restrict__ DY, int64_t lddy, const int64_t* __restrict__ off, int N,
+                                 int E, T* __restrict__ Db) {
+  const int e = blockIdx.y;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N || e >= E) return;
+  const int64_t a = e ? off[e - 1] : 0, b = off[e];
+  float s = 0.f;
+  for (int64_t i = a; i < b; ++i) s += to_f32(DY[i * lddy + n]);
+  Db[(int64_t)e * N + n] = from_f32<T>(s);
+}
+
+// ------------------------------------------------------------------ host side
+template <typename T, int BM, int BN>
+constexpr int rows_lds_bytes() {
+  constexpr int main_loop = 2 * (BM + BN) * kRowBytes;
+  constexpr int staging = 4 * Stage<T, BM / 2, BN / 2>::BYTES;
+  constexpr int decode = (kGemmMaxE + 4 + 8) * 4;
+  constexpr int m = main_loop > staging ? main_loop : staging;
+  return m > decode ? m : decode;
+}
+
+template <typename K>
+int prepare(K kernel, int lds_bytes) {
+  static bool done = false;  // one attribute call per instantiation
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+    if (e != hipSuccess) return set_error(ZMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done = true;
+  }
+  return ZMOE_OK;
+}
+
+template <typename T, int BM, int BN, bool B_KN, int EPI>
+int launch_rows(const RowsParams& p, int64_t R, hipStream_t s) {
+  constexpr int lds = rows_lds_bytes<T, BM, BN>();
+  auto kern = grouped_rows_kernel<T, BM, BN, B_KN, EPI>;
+  int rc = prepare(kern, lds);
+  if (rc) return rc;
+  const int64_t mt_bound = cdiv(R, BM) + (R < p.E ? R : p.E);
+  int64_t total = mt_bound * p.n_tiles;
+  total = cdiv(total, kXcds) * kXcds;
+  ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "grouped gemm: too many tiles");
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(kGemmThreads), lds, s, p);
+  return check_launch("grouped_rows_kernel");
+}
+
+template <typename T, int BM, int BN>
+int launch_wgrad(WgradParams p, hipStream_t s) {
+  constexpr int lds = rows_lds_bytes<T, BM, BN>();
+  auto kern = grouped_wgrad_kernel<T, BM, BN>;
+  int rc = prepare(kern, lds);
+  if (rc) return rc;
+  p.m_tiles = (int)cdiv(p.Ndy, BM);
+  p.n_tiles = (int)cdiv(p.Kx, BN);
+  int64_t total = (int64_t)p.E * p.m_tiles * p.n_tiles;
+  total = cdiv(total, kXcds) * kXcds;
+  ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(kGemmThreads), lds, s, p);
+  return check_launch("grouped_wgrad_kernel");
+}
+
+// Large tiles when the average expert holds enough rows to fill them.
+inline bool use_big_tiles(int64_t R, int E, int64_t N) { return R >= (int64_t)E * 256 && N >= 256; }
+
+template <bool B_KN, int EPI>
+int dispatch_rows(int dtype, RowsParams p, int64_t R, int bn_for_tiles_div, hipStream_t s) {
+  // n_tiles: along N (or along pair columns for SwiGLU, BN/2 pairs per tile)
+  if (dtype == ZMOE_DTYPE_BF16) {
+    if (use_big_tiles(R, p.E, p.N)) {
+      p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 128 : 256);
+      return launch_rows<uint16_t, 256, 256, B_KN, EPI>(p, R, s);
+    }
+    p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 64 : 128);
+    return launch_rows<uint16_t, 128, 128, B_KN, EPI>(p, R, s);
+  }
+  p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 64 : 128);
+  return launch_rows<float, 128, 128, B_KN, EPI>(p, R, s);
+}
+
+}  // namespace zmoe
+
+using namespace zmoe;
+
+namespace {
+
+int vec_elems(int dtype) { return dtype == ZMOE_DTYPE_BF16 ? 8 : 4; }
+bool ok_rows(int dtype, const void* ptr, int64_t ld) {
+  return aligned16(ptr) && (ld % vec_elems(dtype)) == 0;
+}
+
+}  // namespace
+
+extern "C" int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const void* W, int64_t w_stride_e,
+                                    int64_t w_stride_k, int64_t w_stride_n, const void* b, int64_t b_stride_e,
+                                    const int64_t* sorted_expert_idxs, const int64_t* sorted_scattered_idxs,
+                                    const int64_t* expert_offsets, int64_t M, int64_t K, int64_t N, int E, int k,
+                                    int x_grouped, int y_grouped, int dtype, void* Y, int64_t y_stride_m,
+                                    void* stream) {
+  (void)sorted_expert_idxs;  // rows are assigned to experts through expert_offsets
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "scatter2scatter: dtype %d", dtype);
+  ZMOE_REQUIRE(M >= 0 && K >= 1 && N >= 1 && E >= 1 && E <= kGemmMaxE && k >= 1, ZMOE_ERR_SHAPE,
+               "scatter2scatter: bad sizes (M=%lld K=%lld N=%lld E=%d k=%d)", (long long)M, (long long)K,
+               (long long)N, E, k);
+  ZMOE_REQUIRE(K < (1 << 30) && N < (1 << 30), ZMOE_ERR_SHAPE, "scatter2scatter: K/N too large");
+  const int64_t R = x_grouped ? M : M * k;
+  if (R == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(X && W && Y && expert_offsets, ZMOE_ERR_NULL, "scatter2scatter: null pointer");
+  ZMOE_REQUIRE((x_grouped && y_grouped) || sorted_scattered_idxs, ZMOE_ERR_NULL,
+               "scatter2scatter: sorted_scattered_idxs required unless x_grouped and y_grouped");
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(K % v == 0 && N % v == 0 && ok_rows(dtype, X, x_stride_m) && ok_rows(dtype, Y, y_stride_m) &&
+                   aligned16(W) && w_stride_e % v == 0,
+               ZMOE_ERR_ALIGN, "scatter2scatter: K, N and strides must be multiples of %d elements", v);
+  RowsParams p{};
+  p.a = X;
+  p.lda = x_stride_m;
+  p.a_rows = x_grouped ? nullptr : sorted_scattered_idxs;
+  p.a_div = k;
+  p.b = W;
+  p.b_estride = w_stride_e;
+  p.c = Y;
+  p.ldc = y_stride_m;
+  p.c_rows = y_grouped ? nullptr : sorted_scattered_idxs;
+  p.bias = b;
+  p.bias_estride = b_stride_e;
+  p.offsets = expert_offsets;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.E = E;
+  hipStream_t s = as_stream(stream);
+  if (w_stride_k == 1) {  // W[e] stored [N][K]
+    ZMOE_REQUIRE(w_stride_n % v == 0, ZMOE_ERR_ALIGN, "scatter2scatter: weight row stride");
+    p.ldb = w_stride_n;
+    return dispatch_rows<false, EPI_STORE>(dtype, p, R, (int)N, s);
+  }
+  ZMOE_REQUIRE(w_stride_n == 1, ZMOE_ERR_SHAPE, "scatter2scatter: W needs unit stride along K or N");
+  ZMOE_REQUIRE(w_stride_k % v == 0, ZMOE_ERR_ALIGN, "scatter2scatter: weight row stride");
+  p.ldb = w_stride_k;
+  return dispatch_rows<true, EPI_STORE>(dtype, p, R, (int)N, s);
+}
+
+extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
+                                   const int64_t* sorted_expert_idxs, const int64_t* sorted_scattered_idxs,
+                                   const int64_t* expert_offsets, int64_t T, int64_t d, int64_t f, int E, int k,
+                                   int dtype, void* H, void* A, void* stream) {
+  (void)sorted_expert_idxs;
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "glu_w1_forward: dtype %d", dtype);
+  ZMOE_REQUIRE(T >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE && k >= 1, ZMOE_ERR_SHAPE,
+               "glu_w1_forward: bad sizes");
+  ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w1_forward: d/f too large");
+  const int64_t R = T * k;
+  if (R == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(X && W1 && H && A && sorted_scattered_idxs && expert_offsets, ZMOE_ERR_NULL,
+               "glu_w1_forward: null pointer");
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(d % v == 0 && f % v == 0 && ok_rows(dtype, X, x_stride_m) && aligned16(W1) && aligned16(H) &&
+                   aligned16(A),
+               ZMOE_ERR_ALIGN, "glu_w1_forward: d and f must be multiples of %d elements", v);
+  RowsParams p{};
+  p.a = X;
+  p.lda = x_stride_m;
+  p.a_rows = sorted_scattered_idxs;
+  p.a_div = k;
+  p.b = W1;
+  p.b_estride = 2 * f * d;
+  p.ldb = d;
+  p.c = H;
+  p.ldc = 2 * f;
+  p.c2 = A;
+  p.ldc2 = f;
+  p.offsets = expert_offsets;
+  p.K = (int)d;
+  p.N = (int)(2 * f);
+  p.E = E;
+  p.half = (int)f;
+  return dispatch_rows<false, EPI_SWIGLU>(dtype, p, R, (int)f, as_stream(stream));
+}
+
+extern "C" int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const void* H,
+                                       const int64_t* sorted_expert_idxs, const int64_t* expert_offsets, int64_t R,
+                                       int64_t d, int64_t f, int E, int dtype, void* dH, void* stream) {
+  (void)sorted_expert_idxs;
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "glu_w2_backward_dh: dtype %d", dtype);
+  ZMOE_REQUIRE(R >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE, ZMOE_ERR_SHAPE,
+               "glu_w2_backward_dh: bad sizes");
+  ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w2_backward_dh: d/f too large");
+  if (R == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(dYg && W2 && H && dH && expert_offsets, ZMOE_ERR_NULL, "glu_w2_backward_dh: null pointer");
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(d % v == 0 && f % v == 0 && aligned16(dYg) && aligned16(W2) && aligned16(H) && aligned16(dH),
+               ZMOE_ERR_ALIGN, "glu_w2_backward_dh: d and f must be multiples of %d elements", v);
+  RowsParams p{};
+  p.a = dYg;
+  p.lda = d;
+  p.a_rows = nullptr;
+  p.a_div = 1;
+  p.b = W2;  // logical B[kk in d][n in f] = W2[e][kk][n]
+  p.b_estride = d * f;
+  p.ldb = f;
+  p.c = dH;
+  p.ldc = 2 * f;
+  p.aux = H;
+  p.ld_aux = 2 * f;
+  p.offsets = expert_offsets;
+  p.K = (int)d;
+  p.N = (int)f;
+  p.E = E;
+  p.half = (int)f;
+  return dispatch_rows<true, EPI_SWIGLU_BWD>(dtype, p, R, (int)f, as_stream(stream));
+}
+
+extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m,
+                                const int64_t* x_gather_idxs, int x_gather_div, const int64_t* expert_offsets,
+                                int64_t M, int64_t N, int64_t K, int E, int dtype, void* DWt, void* Db,
+                                void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "group_bwd_w: dtype %d", dtype);
+  ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && E >= 1 && E <= kGemmMaxE && x_gather_div >= 1, ZMOE_ERR_SHAPE,
+               "group_bwd_w: bad sizes");
+  ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30), ZMOE_ERR_SHAPE, "group_bwd_w: N/K too large");
+  ZMOE_REQUIRE(DWt && expert_offsets, ZMOE_ERR_NULL, "group_bwd_w: null pointer");
+  ZMOE_REQUIRE(M == 0 || (DY && X), ZMOE_ERR_NULL, "group_bwd_w: null operand");
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(N % v == 0 && K % v == 0 && aligned16(DWt) && (M == 0 || (ok_rows(dtype, DY, dy_stride_m) &&
+                                                                          ok_rows(dtype, X, x_stride_m))),
+               ZMOE_ERR_ALIGN, "group_bwd_w: N, K and strides must be multiples of %d elements", v);
+  WgradParams p{};
+  p.dy = DY;
+  p.lddy = dy_stride_m;
+  p.x = X;
+  p.ldx = x_stride_m;
+  p.x_rows = x_gather_idxs;
+  p.x_div = x_gather_div;
+  p.dw = DWt;
+  p.offsets = expert_offsets;
+  p.Ndy = (int)N;
+  p.Kx = (int)K;
+  p.E = E;
+  hipStream_t s = as_stream(stream);
+  int rc;
+  if (dtype == ZMOE_DTYPE_BF16) {
+    if (use_big_tiles(M, E, N) && K >= 256) rc = launch_wgrad<uint16_t, 256, 256>(p, s);
+    else rc = launch_wgrad<uint16_t, 128, 128>(p, s);
+  } else {
+    rc = launch_wgrad<float, 128, 128>(p, s);
+  }
+  if (rc || Db == nullptr) return rc;
+  const dim3 grid((unsigned)cdiv(N, 256), (unsigned)E), block(256);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(bias_grad_kernel<uint16_t>, grid, block, 0, s, (const uint16_t*)DY, dy_stride_m,
+                       expert_offsets, (int)N, E, (uint16_t*)Db);
+  else
+    hipLaunchKernelGGL(bias_grad_kernel<float>, grid, block, 0, s, (const float*)DY, dy_stride_m, expert_offsets,
+                       (int)N, E, (float*)Db);
+  return check_launch("bias_grad_kernel");
+}

@@ -1,0 +1,417 @@
+// HBM-bound row kernels of the MoE path: dispatch gather (ops.py:449-529), the
+// weighted combine (parallel_experts.py:161-163 + moe_layer.py:53), its backward
+// (parallel_experts.py:191-208), the k-reduction of the input grad
+// (parallel_experts.py:236), rowwise_sum_product (ops.py:9-80) and stand-alone
+// SwiGLU (mlp.py:101-102).
+//
+// Layout: a row of d elements is d/VEC 16-byte chunks (VEC = 8 bf16 or 4 f32).
+// A group of TPR threads (64, 128 or 256; a whole number of waves) owns one row
+// and strides over its chunks, so every load and store is a coalesced 16-byte
+// access; a 256-thread block holds 256/TPR rows.
+#include "zmoe_internal.h"
+
+namespace zmoe {
+
+constexpr int kRowThreads = 256;
+constexpr int kMaxFanOut = 32;
+
+struct RowMap {
+  int tpr;    // threads per row
+  int rpb;    // rows per block
+};
+
+inline RowMap row_map(int64_t nchunks) {
+  int tpr = nchunks <= 64 ? 64 : (nchunks <= 128 ? 128 : 256);
+  return RowMap{tpr, kRowThreads / tpr};
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
+
+template <typename T> struct V { static constexpr int N = 16 / sizeof(T); };
+
+// ------------------------------------------------------------------ group
+template <typename T, typename CT>
+__global__ __launch_bounds__(kRowThreads) void group_kernel(const T* __restrict__ A, int64_t lda, int64_t nch,
+                                                            const int64_t* __restrict__ idx, int64_t N,
+                                                            int fan_out, const CT* __restrict__ coeff,
+                                                            T* __restrict__ Y, int64_t ldy, int tpr) {
+  constexpr int VN = V<T>::N;
+  const int rpb = kRowThreads / tpr;
+  const int64_t n = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  if (n >= N) return;
+  const int lt = threadIdx.x % tpr;
+  const int64_t src = idx[n];
+  const T* a = A + (src / fan_out) * lda;
+  T* y = Y + n * ldy;
+  const float c = coeff ? to_f32(coeff[src]) : 1.f;
+  for (int64_t ch = lt; ch < nch; ch += tpr) {
+    uint4 v = ld16(a + ch * VN);
+    if (coeff) {
+      float f[VN];
+      unpack_chunk(v, f, T{});
+#pragma unroll
+      for (int q = 0; q < VN; ++q) f[q] *= c;
+      v = pack_chunk(f, T{});
+    }
+    st16(y + ch * VN, v);
+  }
+}
+
+// ------------------------------------------------------------------ combine
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restrict__ Y, const float* __restrict__ g,
+                                                              const T* __restrict__ add, int64_t T_, int k,
+                                                              int64_t d, T* __restrict__ out, int tpr) {
+  constexpr int VN = V<T>::N;
+  const int rpb = kRowThreads / tpr;
+  const int64_t t = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  if (t >= T_) return;
+  const int lt = threadIdx.x % tpr;
+  const int64_t nch = d / VN;
+  for (int64_t ch = lt; ch < nch; ch += tpr) {
+    float acc[VN];
+    if (add) {
+      unpack_chunk(ld16(add + t * d + ch * VN), acc, T{});
+    } else {
+#pragma unroll
+      for (int q = 0; q < VN; ++q) acc[q] = 0.f;
+    }
+    float part[VN];
+#pragma unroll
+    for (int q = 0; q < VN; ++q) part[q] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const float w = g[t * k + j];
+      float y[VN];
+      unpack_chunk(ld16(Y + (t * k + j) * d + ch * VN), y, T{});
+#pragma unroll
+      for (int q = 0; q < VN; ++q) part[q] = fmaf(w, y[q], part[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < VN; ++q) acc[q] += part[q];
+    st16(out + t * d + ch * VN, pack_chunk(acc, T{}));
+  }
+}
+
+// ------------------------------------------------------------------ combine backward
+// d_gates[t,j] = <Y[t*k+j], dout[t]>; grouped[inverse[t*k+j]] = g[t,j] * dout[t].
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
+    const T* __restrict__ Y, const T* __restrict__ dout, const float* __restrict__ g,
+    const int32_t* __restrict__ inverse, int64_t T_, int k, int64_t d, float* __restrict__ d_gates,
+    T* __restrict__ grouped, int tpr) {
+  constexpr int VN = V<T>::N;
+  __shared__ float red[kRowThreads / 64][kMaxFanOut];
+  const int rpb = kRowThreads / tpr;
+  const int64_t t = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  const bool live = t < T_;
+  const int lt = threadIdx.x % tpr;
+  const int64_t nch = d / VN;
+  float dot[kMaxFanOut];
+#pragma unroll
+  for (int j = 0; j < kMaxFanOut; ++j) dot[j] = 0.f;
+  if (live) {
+    int64_t dst[kMaxFanOut];
+    float w[kMaxFanOut];
+#pragma unroll
+    for (int j = 0; j < kMaxFanOut; ++j) {
+      if (j < k) {
+        dst[j] = inverse[t * k + j];
+        w[j] = g[t * k + j];
+      }
+    }
+    for (int64_t ch = lt; ch < nch; ch += tpr) {
+      float go[VN];
+      unpack_chunk(ld16(dout + t * d + ch * VN), go, T{});
+#pragma unroll
+      for (int j = 0; j < kMaxFanOut; ++j) {
+        if (j < k) {
+          float y[VN], s[VN];
+          unpack_chunk(ld16(Y + (t * k + j) * d + ch * VN), y, T{});
+          float acc = 0.f;
+#pragma unroll
+          for (int q = 0; q < VN; ++q) {
+            acc = fmaf(y[q], go[q], acc);
+            s[q] = w[j] * go[q];
+          }
+          dot[j] += acc;
+          st16(grouped + dst[j] * d + ch * VN, pack_chunk(s, T{}));
+        }
+      }
+    }
+  }
+  // reduce the k partial dots over the row's threads (whole waves)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < kMaxFanOut; ++j) {
+    if (j < k) {
+      const float s = wave_sum(dot[j]);
+      if (lane == 0) red[wave][j] = s;
+    }
+  }
+  __syncthreads();
+  const int wpr = tpr / 64;  // waves per row
+  if (live && lt < k) {
+    const int w0 = (threadIdx.x / tpr) * wpr;
+    float s = 0.f;
+    for (int w = 0; w < wpr; ++w) s += red[w0 + w][lt];
+    d_gates[t * k + lt] = s;
+  }
+}
+
+// ------------------------------------------------------------------ k-sum
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void sum_k_kernel(const T* __restrict__ Xe, int64_t T_, int k, int64_t d,
+                                                            const T* __restrict__ a0, const T* __restrict__ a1,
+                                                            T* __restrict__ out, int tpr) {
+  constexpr int VN = V<T>::N;
+  const int rpb = kRowThreads / tpr;
+  const int64_t t = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  if (t >= T_) return;
+  const int lt = threadIdx.x % tpr;
+  const int64_t nch = d / VN;
+  for (int64_t ch = lt; ch < nch; ch += tpr) {
+    float acc[VN], x[VN];
+#pragma unroll
+    for (int q = 0; q < VN; ++q) acc[q] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      unpack_chunk(ld16(Xe + (t * k + j) * d + ch * VN), x, T{});
+#pragma unroll
+      for (int q = 0; q < VN; ++q) acc[q] += x[q];
+    }
+    if (a0) {
+      unpack_chunk(ld16(a0 + t * d + ch * VN), x, T{});
+#pragma unroll
+      for (int q = 0; q < VN; ++q) acc[q] += x[q];
+    }
+    if (a1) {
+      unpack_chunk(ld16(a1 + t * d + ch * VN), x, T{});
+#pragma unroll
+      for (int q = 0; q < VN; ++q) acc[q] += x[q];
+    }
+    st16(out + t * d + ch * VN, pack_chunk(acc, T{}));
+  }
+}
+
+// ------------------------------------------------------------------ rowwise_sum_product
+// One wave per (t, j): out[t,j] = sum_h A[t,j,h] * B[t,h]; scalar loads so any
+// H and mixed dtypes work.
+template <typename TA, typename TB, typename TO>
+__global__ __launch_bounds__(kRowThreads) void rowwise_kernel(const TA* __restrict__ A, const TB* __restrict__ B,
+                                                              int64_t T_, int F, int64_t H, TO* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
+  if (r >= T_ * F) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = r / F;
+  const TA* a = A + r * H;
+  const TB* b = B + t * H;
+  float acc = 0.f;
+  for (int64_t h = lane; h < H; h += 64) acc = fmaf(to_f32(a[h]), to_f32(b[h]), acc);
+  acc = wave_sum(acc);
+  if (lane == 0) out[r] = from_f32<TO>(acc);
+}
+
+// ------------------------------------------------------------------ swiglu
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void swiglu_kernel(const T* __restrict__ H, int64_t R, int64_t f,
+                                                             T* __restrict__ A) {
+  constexpr int VN = V<T>::N;
+  const int64_t nch = f / VN;
+  const int64_t i = (int64_t)blockIdx.x * kRowThreads + threadIdx.x;
+  if (i >= R * nch) return;
+  const int64_t r = i / nch, ch = i % nch;
+  float h[VN], g[VN], a[VN];
+  unpack_chunk(ld16(H + r * 2 * f + ch * VN), h, T{});
+  unpack_chunk(ld16(H + r * 2 * f + f + ch * VN), g, T{});
+#pragma unroll
+  for (int q = 0; q < VN; ++q) a[q] = silu_f(g[q]) * h[q];
+  st16(A + r * f + ch * VN, pack_chunk(a, T{}));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void swiglu_backward_kernel(const T* __restrict__ dA,
+                                                                      const T* __restrict__ H, int64_t R,
+                                                                      int64_t f, T* __restrict__ dH) {
+  constexpr int VN = V<T>::N;
+  const int64_t nch = f / VN;
+  const int64_t i = (int64_t)blockIdx.x * kRowThreads + threadIdx.x;
+  if (i >= R * nch) return;
+  const int64_t r = i / nch, ch = i % nch;
+  float h[VN], g[VN], da[VN], dh[VN], dg[VN];
+  unpack_chunk(ld16(H + r * 2 * f + ch * VN), h, T{});
+  unpack_chunk(ld16(H + r * 2 * f + f + ch * VN), g, T{});
+  unpack_chunk(ld16(dA + r * f + ch * VN), da, T{});
+#pragma unroll
+  for (int q = 0; q < VN; ++q) {
+    const float s = sigmoid_fast(g[q]);
+    dh[q] = da[q] * g[q] * s;
+    dg[q] = da[q] * h[q] * s * (1.f + g[q] * (1.f - s));
+  }
+  st16(dH + r * 2 * f + ch * VN, pack_chunk(dh, T{}));
+  st16(dH + r * 2 * f + f + ch * VN, pack_chunk(dg, T{}));
+}
+
+}  // namespace zmoe
+
+using namespace zmoe;
+
+namespace {
+
+int vec_of(int dtype) { return dtype == ZMOE_DTYPE_BF16 ? 8 : 4; }
+
+bool rows_aligned(int dtype, const void* p, int64_t ld) {
+  return p == nullptr || (aligned16(p) && (ld % vec_of(dtype)) == 0);
+}
+
+}  // namespace
+
+extern "C" int zmoe_group(const void* A, int64_t lda, int64_t K, int dtype, const int64_t* sorted_idxs, int64_t N,
+                          int fan_out, const void* coeff, int coeff_dtype, void* Y, int64_t ldy, void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype) && dtype_ok(coeff_dtype), ZMOE_ERR_DTYPE, "group: dtype");
+  ZMOE_REQUIRE(N >= 0 && K >= 0 && fan_out >= 1, ZMOE_ERR_SHAPE, "group: bad sizes");
+  if (N == 0 || K == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(A && sorted_idxs && Y, ZMOE_ERR_NULL, "group: null pointer");
+  ZMOE_REQUIRE(K % vec_of(dtype) == 0 && rows_aligned(dtype, A, lda) && rows_aligned(dtype, Y, ldy), ZMOE_ERR_ALIGN,
+               "group: K (%lld) and row strides must be multiples of %d elements, pointers 16-byte aligned",
+               (long long)K, vec_of(dtype));
+  const int64_t nch = K / vec_of(dtype);
+  const RowMap m = row_map(nch);
+  const dim3 grid((unsigned)cdiv(N, m.rpb)), block(kRowThreads);
+  hipStream_t s = as_stream(stream);
+#define ZMOE_GROUP_LAUNCH(T, CT)                                                                                  \
+  hipLaunchKernelGGL((group_kernel<T, CT>), grid, block, 0, s, (const T*)A, lda, nch, sorted_idxs, N, fan_out, \
+                     (const CT*)coeff, (T*)Y, ldy, m.tpr)
+  if (dtype == ZMOE_DTYPE_BF16) {
+    if (coeff_dtype == ZMOE_DTYPE_BF16) ZMOE_GROUP_LAUNCH(uint16_t, uint16_t);
+    else ZMOE_GROUP_LAUNCH(uint16_t, float);
+  } else {
+    if (coeff_dtype == ZMOE_DTYPE_BF16) ZMOE_GROUP_LAUNCH(float, uint16_t);
+    else ZMOE_GROUP_LAUNCH(float, float);
+  }
+#undef ZMOE_GROUP_LAUNCH
+  return check_launch("group");
+}
+
+extern "C" int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t T, int k, int64_t d,
+                            int dtype, void* out, void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "combine: dtype");
+  ZMOE_REQUIRE(T >= 0 && k >= 1 && d >= 0, ZMOE_ERR_SHAPE, "combine: bad sizes");
+  if (T == 0 || d == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(Y && gates && out, ZMOE_ERR_NULL, "combine: null pointer");
+  ZMOE_REQUIRE(d % vec_of(dtype) == 0 && rows_aligned(dtype, Y, d) && rows_aligned(dtype, out, d) &&
+                   rows_aligned(dtype, addend, d),
+               ZMOE_ERR_ALIGN, "combine: d must be a multiple of %d, pointers 16-byte aligned", vec_of(dtype));
+  const RowMap m = row_map(d / vec_of(dtype));
+  const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)Y, gates,
+                       (const uint16_t*)addend, T, k, d, (uint16_t*)out, m.tpr);
+  else
+    hipLaunchKernelGGL(combine_kernel<float>, grid, block, 0, as_stream(stream), (const float*)Y, gates,
+                       (const float*)addend, T, k, d, (float*)out, m.tpr);
+  return check_launch("combine");
+}
+
+extern "C" int zmoe_combine_backward(const void* Y, const void* grad_out, const float* gates, const int32_t* inverse,
+                                     int64_t T, int k, int64_t d, int dtype, float* d_gates, void* grouped_grad_out,
+                                     void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "combine_backward: dtype");
+  ZMOE_REQUIRE(T >= 0 && k >= 1 && k <= kMaxFanOut && d >= 0, ZMOE_ERR_SHAPE,
+               "combine_backward: need 1 <= k <= %d", kMaxFanOut);
+  if (T == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(Y && grad_out && gates && inverse && d_gates && grouped_grad_out, ZMOE_ERR_NULL,
+               "combine_backward: null pointer");
+  ZMOE_REQUIRE(d % vec_of(dtype) == 0 && rows_aligned(dtype, Y, d) && rows_aligned(dtype, grad_out, d) &&
+                   rows_aligned(dtype, grouped_grad_out, d),
+               ZMOE_ERR_ALIGN, "combine_backward: d must be a multiple of %d, pointers 16-byte aligned",
+               vec_of(dtype));
+  const RowMap m = row_map(d / vec_of(dtype));
+  const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(combine_backward_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)Y,
+                       (const uint16_t*)grad_out, gates, inverse, T, k, d, d_gates, (uint16_t*)grouped_grad_out,
+                       m.tpr);
+  else
+    hipLaunchKernelGGL(combine_backward_kernel<float>, grid, block, 0, as_stream(stream), (const float*)Y,
+                       (const float*)grad_out, gates, inverse, T, k, d, d_gates, (float*)grouped_grad_out, m.tpr);
+  return check_launch("combine_backward");
+}
+
+extern "C" int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype, const void* add0, const void* add1,
+                          void* out, void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "sum_k: dtype");
+  ZMOE_REQUIRE(T >= 0 && k >= 1 && d >= 0, ZMOE_ERR_SHAPE, "sum_k: bad sizes");
+  if (T == 0 || d == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(Xe && out, ZMOE_ERR_NULL, "sum_k: null pointer");
+  ZMOE_REQUIRE(d % vec_of(dtype) == 0 && rows_aligned(dtype, Xe, d) && rows_aligned(dtype, out, d) &&
+                   rows_aligned(dtype, add0, d) && rows_aligned(dtype, add1, d),
+               ZMOE_ERR_ALIGN, "sum_k: d must be a multiple of %d, pointers 16-byte aligned", vec_of(dtype));
+  const RowMap m = row_map(d / vec_of(dtype));
+  const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(sum_k_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)Xe, T, k, d,
+                       (const uint16_t*)add0, (const uint16_t*)add1, (uint16_t*)out, m.tpr);
+  else
+    hipLaunchKernelGGL(sum_k_kernel<float>, grid, block, 0, as_stream(stream), (const float*)Xe, T, k, d,
+                       (const float*)add0, (const float*)add1, (float*)out, m.tpr);
+  return check_launch("sum_k");
+}
+
+extern "C" int zmoe_rowwise_sum_product(const void* A, int a_dtype, const void* B, int b_dtype, int64_t T, int F,
+                                        int64_t H, void* out, int out_dtype, void* stream) {
+  ZMOE_REQUIRE(dtype_ok(a_dtype) && dtype_ok(b_dtype) && dtype_ok(out_dtype), ZMOE_ERR_DTYPE,
+               "rowwise_sum_product: dtype");
+  ZMOE_REQUIRE(T >= 0 && F >= 0 && H >= 0, ZMOE_ERR_SHAPE, "rowwise_sum_product: bad sizes");
+  if (T == 0 || F == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(A && B && out, ZMOE_ERR_NULL, "rowwise_sum_product: null pointer");
+  const dim3 grid((unsigned)cdiv(T * F, kRowThreads / 64)), block(kRowThreads);
+  hipStream_t s = as_stream(stream);
+#define ZMOE_RW(TA, TB, TO) \
+  hipLaunchKernelGGL((rowwise_kernel<TA, TB, TO>), grid, block, 0, s, (const TA*)A, (const TB*)B, T, F, H, (TO*)out)
+#define ZMOE_RW_O(TA, TB) \
+  if (out_dtype == ZMOE_DTYPE_BF16) ZMOE_RW(TA, TB, uint16_t); else ZMOE_RW(TA, TB, float)
+  if (a_dtype == ZMOE_DTYPE_BF16) {
+    if (b_dtype == ZMOE_DTYPE_BF16) { ZMOE_RW_O(uint16_t, uint16_t); } else { ZMOE_RW_O(uint16_t, float); }
+  } else {
+    if (b_dtype == ZMOE_DTYPE_BF16) { ZMOE_RW_O(float, uint16_t); } else { ZMOE_RW_O(float, float); }
+  }
+#undef ZMOE_RW_O
+#undef ZMOE_RW
+  return check_launch("rowwise_sum_product");
+}
+
+extern "C" int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void* A, void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "swiglu: dtype");
+  ZMOE_REQUIRE(R >= 0 && f >= 0, ZMOE_ERR_SHAPE, "swiglu: bad sizes");
+  if (R == 0 || f == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(H && A, ZMOE_ERR_NULL, "swiglu: null pointer");
+  ZMOE_REQUIRE(f % vec_of(dtype) == 0 && aligned16(H) && aligned16(A), ZMOE_ERR_ALIGN,
+               "swiglu: f must be a multiple of %d", vec_of(dtype));
+  const int64_t n = R * (f / vec_of(dtype));
+  const dim3 grid((unsigned)cdiv(n, kRowThreads)), block(kRowThreads);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(swiglu_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)H, R, f,
+                       (uint16_t*)A);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<float>, grid, block, 0, as_stream(stream), (const float*)H, R, f, (float*)A);
+  return check_launch("swiglu");
+}
+
+extern "C" int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f, int dtype, void* dH,
+                                    void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "swiglu_backward: dtype");
+  ZMOE_REQUIRE(R >= 0 && f >= 0, ZMOE_ERR_SHAPE, "swiglu_backward: bad sizes");
+  if (R == 0 || f == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(dA && H && dH, ZMOE_ERR_NULL, "swiglu_backward: null pointer");
+  ZMOE_REQUIRE(f % vec_of(dtype) == 0 && aligned16(H) && aligned16(dA) && aligned16(dH), ZMOE_ERR_ALIGN,
+               "swiglu_backward: f must be a multiple of %d", vec_of(dtype));
+  const int64_t n = R * (f / vec_of(dtype));
+  const dim3 grid((unsigned)cdiv(n, kRowThreads)), block(kRowThreads);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(swiglu_backward_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)dA,
+                       (const uint16_t*)H, R, f, (uint16_t*)dH);
+  else
+    hipLaunchKernelGGL(swiglu_backward_kernel<float>, grid, block, 0, as_stream(stream), (const float*)dA,
+                       (const float*)H, R, f, (float*)dH);
+  return check_launch("swiglu_backward");
+}

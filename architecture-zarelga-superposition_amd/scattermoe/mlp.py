@@ -1,0 +1,126 @@
+"""Expert MLPs on MI355X — the reference's scattermoe/mlp.py interface.
+
+``GLUMLP`` keeps the reference's modules and parameters (``experts`` W1
+[E, 2f, d], ``output_experts`` W2 [E, d, f]) and, by default, runs them through
+one fused autograd function over libzmoe_hip:
+
+  forward : sort -> W1 GEMM with SwiGLU epilogue (H, A) -> W2 GEMM scattered to
+            slot order (Y) -> weighted combine
+  backward: combine backward (d_gates + grouped grad) -> W2 input-grad GEMM with
+            SwiGLU-backward epilogue (dH) -> dW2, dW1 (x gathered in-kernel)
+            -> W1 input-grad GEMM -> k-sum
+
+which computes the same values as the reference's composition (mlp.py:74-95 via
+ParallelLinear). ``fused=False`` runs that composition through ParallelExperts.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from zmoe import ops as _z
+
+from .parallel_experts import ParallelExperts, flatten_sort_count
+
+
+def _compute_dtype(x: torch.Tensor) -> torch.dtype:
+    return torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled() else x.dtype
+
+
+class GLUExpertsFunction(torch.autograd.Function):
+    """y = sum_j gates[:, j] * W2[e_j] silu(W1g[e_j] x) * (W1h[e_j] x) for every token."""
+
+    @staticmethod
+    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int):
+        se, ss, off, inv = _z.flatten_sort_count(expert_idxs, num_experts)
+        H, A = _z.glu_w1_forward(x, W1, se, ss, off, k)                       # mlp.py:96-102
+        Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
+                               expert_offsets=off)                             # mlp.py:103-108
+        out = _z.combine(Y, gates, k)                                          # parallel_experts.py:161-163
+        ctx.save_for_backward(x, gates, W1, W2, se, ss, off, inv, H, A, Y)
+        ctx.k = k
+        ctx.num_experts = num_experts
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, gates, W1, W2, se, ss, off, inv, H, A, Y = ctx.saved_tensors
+        k, E = ctx.k, ctx.num_experts
+        dout = dout.to(x.dtype)
+        d_gates, dYg = _z.combine_backward(Y, dout, gates, inv)               # parallel_experts.py:191-208
+        dH = _z.glu_w2_backward_dh(dYg, W2, H, se, off)                        # :223-231 + silu*mul backward
+        dW2, _ = _z.group_bwd_w(dYg, A, off, E)                                # :216-221 (W2)
+        dW1, _ = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)          # :213-221 (W1, x gathered)
+        dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False,
+                                 expert_offsets=off)                           # :223-231 (W1)
+        dx = _z.sum_k(dXe, k)                                                  # :236
+        return dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None
+
+
+class MLP(nn.Module):
+    """Reference scattermoe/mlp.py:6-49 (non-GLU expert MLP)."""
+
+    def __init__(self, input_size, hidden_size, num_experts, top_k, bias=False, activation=None):
+        super(MLP, self).__init__()
+        self.num_experts = num_experts
+        self.input_size = input_size
+        self.hidden_size = hidden_size
+        self.experts = ParallelExperts(num_experts, input_size, hidden_size, bias=bias)
+        self.output_experts = ParallelExperts(num_experts, hidden_size, input_size, bias=bias)
+        self.top_k = min(top_k, self.num_experts)
+        self.activation = activation
+
+    def extra_repr(self):
+        return "k={}".format(self.top_k)
+
+    def forward(self, x: torch.Tensor, expert_p: torch.Tensor, expert_idxs: torch.Tensor):
+        x_shape = x.size()
+        x = x.view(-1, x_shape[-1])
+        sorted_expert_idxs, sorted_scattered_idxs, expert_offsets = flatten_sort_count(
+            expert_idxs, num_experts=self.num_experts)
+        h = self.experts(x, self.top_k, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
+                         grouped_out=True)
+        h = self.activation(h)
+        y = self.output_experts(h, 1, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
+                                grouped_in=True, gates=expert_p)
+        y = y.view(*x_shape[:-1], y.size(-1))
+        return y
+
+
+class GLUMLP(nn.Module):
+    """Reference scattermoe/mlp.py:51-95 (SwiGLU expert MLP)."""
+
+    def __init__(self, input_size, hidden_size, num_experts, top_k, bias=False, activation=nn.SiLU(), fused=True):
+        super(GLUMLP, self).__init__()
+        self.num_experts = num_experts
+        self.input_size = input_size
+        self.hidden_size = hidden_size
+        self.experts = ParallelExperts(num_experts, input_size, 2 * hidden_size, bias=bias)
+        self.output_experts = ParallelExperts(num_experts, hidden_size, input_size, bias=bias)
+        self.top_k = min(top_k, self.num_experts)
+        self.activation = activation
+        # The fused kernels implement SiLU-gated units without expert biases.
+        self.fused = fused and not bias and isinstance(activation, nn.SiLU)
+
+    def extra_repr(self):
+        return "k={}".format(self.top_k)
+
+    def forward(self, x: torch.Tensor, expert_p: torch.Tensor, expert_idxs: torch.Tensor):
+        x_shape = x.size()
+        x = x.view(-1, x_shape[-1])
+        if self.fused:
+            dtype = _compute_dtype(x)
+            y = GLUExpertsFunction.apply(x.to(dtype), expert_p, expert_idxs,
+                                         self.experts.compute_weight(dtype),
+                                         self.output_experts.compute_weight(dtype), self.top_k, self.num_experts)
+            return y.view(*x_shape[:-1], y.size(-1))
+        sorted_expert_idxs, sorted_scattered_idxs, expert_offsets = flatten_sort_count(
+            expert_idxs, num_experts=self.num_experts)
+        h, gates = self.experts(x, self.top_k, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
+                                grouped_out=True).chunk(2, dim=-1)
+        h = self.activation(gates) * h
+        y = self.output_experts(h, 1, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
+                                grouped_in=True, gates=expert_p)
+        y = y.view(*x_shape[:-1], y.size(-1))
+        return y

@@ -1,0 +1,360 @@
+"""torch-facing wrappers of the libzmoe_hip C ABI.
+
+Every function checks devices, dtypes and shapes, allocates its outputs with
+torch on the input's device (torch owns all memory), and enqueues the HIP work on
+torch's current stream. Nothing here synchronises or falls back to another
+implementation: unsupported inputs raise.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+from . import profiling
+
+_DT = {torch.float32: L.DTYPE_F32, torch.bfloat16: L.DTYPE_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _require_cuda(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("zmoe ops need tensors on a HIP device")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("zmoe ops need all tensors on one device")
+    return dev
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """2-D tensor with unit column stride (row stride may be anything)."""
+    if t.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(t.shape)}")
+    return t if t.stride(1) == 1 else t.contiguous()
+
+
+def _idx64(t: torch.Tensor) -> torch.Tensor:
+    t = t.reshape(-1)
+    if t.dtype != torch.int64:
+        t = t.to(torch.int64)
+    return t.contiguous()
+
+
+# --------------------------------------------------------------------- routing
+def route_topk(logits: torch.Tensor, expert_biases: torch.Tensor, k: int, round_probs_bf16: bool = False):
+    """modeling/moe_gate.py:27-34 on given logits [T, E] -> (idx, weight, prob) [T, k]."""
+    dev = _require_cuda(logits, expert_biases)
+    logits = logits.contiguous()
+    T, E = logits.shape
+    bias = expert_biases.to(torch.float32).contiguous()
+    if bias.numel() != E:
+        raise ValueError("expert_biases must have E entries")
+    idx = torch.empty((T, k), dtype=torch.int64, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    p = torch.empty((T, k), dtype=torch.float32, device=dev)
+    with profiling.region("route_topk", dev):
+        L.call("zmoe_route_topk", _ptr(logits), _dtype_code(logits), T, E, k, _ptr(bias), int(round_probs_bf16),
+               _ptr(idx), _ptr(w), _ptr(p), _stream(dev))
+    return idx, w, p
+
+
+def route_topk_backward(d_weight: torch.Tensor, topk_prob: torch.Tensor, topk_idx: torch.Tensor, E: int,
+                        dtype: torch.dtype) -> torch.Tensor:
+    dev = _require_cuda(d_weight, topk_prob, topk_idx)
+    T, k = topk_idx.shape
+    dw = d_weight.to(torch.float32).contiguous()
+    out = torch.empty((T, E), dtype=dtype, device=dev)
+    L.call("zmoe_route_topk_backward", _ptr(dw), _ptr(topk_prob.contiguous()), _ptr(topk_idx.contiguous()), T, E,
+           k, _ptr(out), _DT[dtype], _stream(dev))
+    return out
+
+
+# --------------------------------------------------------------------- sort
+def bincount(expert_idxs: torch.Tensor, num_experts: int) -> torch.Tensor:
+    dev = _require_cuda(expert_idxs)
+    flat = _idx64(expert_idxs)
+    counts = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    L.call("zmoe_bincount", _ptr(flat), flat.numel(), num_experts, _ptr(counts), _stream(dev))
+    return counts
+
+
+def flatten_sort_count(expert_idxs: torch.Tensor, num_experts: int, return_workspace: bool = False):
+    """scattermoe/parallel_experts.py:21-28 plus the inverse permutation.
+
+    Returns (sorted_expert_idxs, sorted_scattered_idxs, expert_offsets, inverse)
+    [+ workspace, whose first int32 is 1 when an index was outside [0, E)].
+    """
+    dev = _require_cuda(expert_idxs)
+    flat = _idx64(expert_idxs)
+    R = flat.numel()
+    se = torch.empty(R, dtype=torch.int64, device=dev)
+    ss = torch.empty(R, dtype=torch.int64, device=dev)
+    off = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    inv = torch.empty(R, dtype=torch.int32, device=dev)
+    nbytes = L.load().zmoe_sort_workspace_bytes(R, num_experts)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with profiling.region("flatten_sort_count", dev):
+        L.call("zmoe_flatten_sort_count", _ptr(flat), R, num_experts, _ptr(se), _ptr(ss), _ptr(off), _ptr(inv),
+               _ptr(ws), nbytes, _stream(dev))
+    if return_workspace:
+        return se, ss, off, inv, ws
+    return se, ss, off, inv
+
+
+def sort_out_of_range(workspace: torch.Tensor) -> bool:
+    """Host check (synchronises) of the sort's out-of-range flag."""
+    return bool(workspace[:4].view(torch.int32)[0].item())
+
+
+def offsets_from_sorted(sorted_expert_idxs: torch.Tensor, num_experts: int) -> torch.Tensor:
+    dev = _require_cuda(sorted_expert_idxs)
+    se = _idx64(sorted_expert_idxs)
+    off = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    L.call("zmoe_offsets_from_sorted", _ptr(se), se.numel(), num_experts, _ptr(off), _stream(dev))
+    return off
+
+
+# --------------------------------------------------------------------- group
+def group(A: torch.Tensor, sorted_idxs: torch.Tensor, coeff: Optional[torch.Tensor] = None, fan_out: int = 1,
+          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """scattermoe/kernels/ops.py:449-458: Y[n] = A[idx[n] // fan_out] * coeff[idx[n]]."""
+    dev = _require_cuda(A, sorted_idxs, coeff, out)
+    A = _rows(A)
+    idx = _idx64(sorted_idxs)
+    N, K = idx.numel(), A.shape[1]
+    if A.shape[0] * fan_out != N:
+        raise ValueError("group: A.size(0) * fan_out must equal len(sorted_idxs)")
+    Y = torch.empty((N, K), dtype=A.dtype, device=dev) if out is None else out
+    if Y.shape != (N, K) or Y.dtype != A.dtype or Y.stride(1) != 1:
+        raise ValueError("group: bad out tensor")
+    c = None
+    if coeff is not None:
+        c = coeff.reshape(-1)
+        if c.dtype not in _DT:
+            c = c.float()
+        c = c.contiguous()
+    with profiling.region("group", dev):
+        L.call("zmoe_group", _ptr(A), A.stride(0), K, _dtype_code(A), _ptr(idx), N, fan_out, _ptr(c),
+               _DT[c.dtype] if c is not None else L.DTYPE_F32, _ptr(Y), Y.stride(0), _stream(dev))
+    return Y
+
+
+# --------------------------------------------------------------------- grouped GEMMs
+def scatter2scatter(X: torch.Tensor, W: torch.Tensor, sorted_expert_idxs: torch.Tensor,
+                    sorted_scattered_idxs: torch.Tensor, k: int, b: Optional[torch.Tensor] = None,
+                    x_grouped: bool = False, y_grouped: bool = False, out: Optional[torch.Tensor] = None,
+                    expert_offsets: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """scattermoe/kernels/ops.py:192-209. W is the logical [E, K, N] operand."""
+    dev = _require_cuda(X, W, sorted_expert_idxs, sorted_scattered_idxs, b, out, expert_offsets)
+    X = _rows(X)
+    if W.dim() != 3:
+        raise ValueError("scatter2scatter: W must be [E, K, N]")
+    E, K, N = W.shape
+    if W.stride(1) != 1 and W.stride(2) != 1:
+        W = W.contiguous()
+    if W.dtype != X.dtype:
+        raise ValueError("scatter2scatter: X and W dtypes differ")
+    se = _idx64(sorted_expert_idxs)
+    ss = _idx64(sorted_scattered_idxs)
+    R = se.numel()
+    if ss.numel() != R or R != X.shape[0] * k:
+        raise ValueError("scatter2scatter: sorted index lengths must equal X.size(0) * k")
+    if X.shape[1] != K:
+        raise ValueError("scatter2scatter: X.size(1) != W.size(1)")
+    if out is None:
+        out = torch.empty((R, N), dtype=X.dtype, device=dev)
+    elif out.shape != (R, N) or out.dtype != X.dtype or out.stride(1) != 1:
+        raise ValueError("scatter2scatter: bad out tensor")
+    off = offsets_from_sorted(se, E) if expert_offsets is None else _idx64(expert_offsets)
+    if b is not None:
+        b = b.to(X.dtype).contiguous()
+    M = X.shape[0]
+    with profiling.region("scatter2scatter", dev):
+        L.call("zmoe_scatter2scatter", _ptr(X), X.stride(0), _ptr(W), W.stride(0), W.stride(1), W.stride(2),
+               _ptr(b), b.stride(0) if b is not None else 0, _ptr(se), _ptr(ss), _ptr(off), M, K, N, E, k,
+               int(x_grouped), int(y_grouped), _dtype_code(X), _ptr(out), out.stride(0), _stream(dev))
+    return out
+
+
+def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor, E: int, has_bias: bool = False,
+                x_gather: Optional[torch.Tensor] = None, x_div: int = 1, out: Optional[torch.Tensor] = None,
+                out_bias: Optional[torch.Tensor] = None):
+    """scattermoe/kernels/ops.py:263-271 -> (DWt [E, N, K] contiguous, Db [E, N] or None).
+
+    ``x_gather`` makes row i of X read X[x_gather[i] // x_div] (no grouped copy).
+    ``out`` / ``out_bias`` may supply the contiguous result buffers.
+    """
+    dev = _require_cuda(DY, X, expert_offsets, x_gather)
+    DY = _rows(DY)
+    X = _rows(X)
+    if DY.dtype != X.dtype:
+        raise ValueError("group_bwd_w: DY and X dtypes differ")
+    M, N = DY.shape
+    K = X.shape[1]
+    g = None
+    if x_gather is not None:
+        g = _idx64(x_gather)
+        if g.numel() != M:
+            raise ValueError("group_bwd_w: x_gather must have DY.size(0) entries")
+    elif X.shape[0] != M:
+        raise ValueError("group_bwd_w: X and DY row counts differ")
+    DWt = torch.empty((E, N, K), dtype=DY.dtype, device=dev) if out is None else out
+    if DWt.shape != (E, N, K) or DWt.dtype != DY.dtype or not DWt.is_contiguous():
+        raise ValueError("group_bwd_w: bad out tensor")
+    Db = None
+    if has_bias:
+        Db = torch.empty((E, N), dtype=DY.dtype, device=dev) if out_bias is None else out_bias
+        if Db.shape != (E, N) or Db.dtype != DY.dtype or not Db.is_contiguous():
+            raise ValueError("group_bwd_w: bad out_bias tensor")
+    off = _idx64(expert_offsets)
+    with profiling.region("group_bwd_w", dev):
+        L.call("zmoe_group_bwd_w", _ptr(DY), DY.stride(0), _ptr(X), X.stride(0), _ptr(g), x_div, _ptr(off), M, N, K,
+               E, _dtype_code(DY), _ptr(DWt), _ptr(Db), _stream(dev))
+    return DWt, Db
+
+
+def glu_w1_forward(x: torch.Tensor, W1: torch.Tensor, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
+                   k: int):
+    """W1 grouped GEMM with fused SwiGLU: returns H [R, 2f] and A [R, f] in sorted order."""
+    dev = _require_cuda(x, W1)
+    x = _rows(x)
+    W1 = W1.contiguous()
+    E, two_f, d = W1.shape
+    f = two_f // 2
+    T = x.shape[0]
+    R = T * k
+    H = torch.empty((R, two_f), dtype=x.dtype, device=dev)
+    A = torch.empty((R, f), dtype=x.dtype, device=dev)
+    with profiling.region("glu_w1_forward", dev):
+        L.call("zmoe_glu_w1_forward", _ptr(x), x.stride(0), _ptr(W1), _ptr(sorted_expert_idxs),
+               _ptr(sorted_scattered_idxs), _ptr(expert_offsets), T, d, f, E, k, _dtype_code(x), _ptr(H), _ptr(A),
+               _stream(dev))
+    return H, A
+
+
+def glu_w2_backward_dh(dYg: torch.Tensor, W2: torch.Tensor, H: torch.Tensor, sorted_expert_idxs, expert_offsets):
+    """dA = dYg @ W2[e] fused with the SwiGLU backward: returns dH [R, 2f]."""
+    dev = _require_cuda(dYg, W2, H)
+    dYg = dYg.contiguous()
+    W2 = W2.contiguous()
+    E, d, f = W2.shape
+    R = dYg.shape[0]
+    dH = torch.empty((R, 2 * f), dtype=dYg.dtype, device=dev)
+    with profiling.region("glu_w2_backward_dh", dev):
+        L.call("zmoe_glu_w2_backward_dh", _ptr(dYg), _ptr(W2), _ptr(H), _ptr(sorted_expert_idxs),
+               _ptr(expert_offsets), R, d, f, E, _dtype_code(dYg), _ptr(dH), _stream(dev))
+    return dH
+
+
+# --------------------------------------------------------------------- combine / reductions
+def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[t] = addend[t] + sum_j gates[t, j] * Y[t*k + j]."""
+    dev = _require_cuda(Y, gates, addend)
+    Y = Y.contiguous()
+    d = Y.shape[-1]
+    T = Y.numel() // (d * k)
+    g = gates.reshape(T, k).to(torch.float32).contiguous()
+    if addend is not None:
+        addend = addend.reshape(T, d).to(Y.dtype).contiguous()
+    out = torch.empty((T, d), dtype=Y.dtype, device=dev)
+    with profiling.region("combine", dev):
+        L.call("zmoe_combine", _ptr(Y), _ptr(g), _ptr(addend), T, k, d, _dtype_code(Y), _ptr(out), _stream(dev))
+    return out
+
+
+def combine_backward(Y: torch.Tensor, grad_out: torch.Tensor, gates: torch.Tensor, inverse: torch.Tensor):
+    """(d_gates [T, k] f32, grouped_grad_out [T*k, d] in sorted order)."""
+    dev = _require_cuda(Y, grad_out, gates, inverse)
+    Y = Y.contiguous()
+    d = Y.shape[-1]
+    T, k = gates.shape
+    g = gates.to(torch.float32).contiguous()
+    go = grad_out.reshape(T, d).to(Y.dtype).contiguous()
+    d_gates = torch.empty((T, k), dtype=torch.float32, device=dev)
+    grouped = torch.empty((T * k, d), dtype=Y.dtype, device=dev)
+    with profiling.region("combine_backward", dev):
+        L.call("zmoe_combine_backward", _ptr(Y), _ptr(go), _ptr(g), _ptr(inverse), T, k, d, _dtype_code(Y),
+               _ptr(d_gates), _ptr(grouped), _stream(dev))
+    return d_gates, grouped
+
+
+def sum_k(Xe: torch.Tensor, k: int, add0: Optional[torch.Tensor] = None,
+          add1: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[t] = sum_j Xe[t*k + j] (+ add0[t] + add1[t])."""
+    dev = _require_cuda(Xe, add0, add1)
+    Xe = Xe.contiguous()
+    d = Xe.shape[-1]
+    T = Xe.numel() // (d * k)
+    a0 = None if add0 is None else add0.reshape(T, d).to(Xe.dtype).contiguous()
+    a1 = None if add1 is None else add1.reshape(T, d).to(Xe.dtype).contiguous()
+    out = torch.empty((T, d), dtype=Xe.dtype, device=dev)
+    with profiling.region("sum_k", dev):
+        L.call("zmoe_sum_k", _ptr(Xe), T, k, d, _dtype_code(Xe), _ptr(a0), _ptr(a1), _ptr(out), _stream(dev))
+    return out
+
+
+def rowwise_sum_product(A: torch.Tensor, B: torch.Tensor, dtype: Optional[torch.dtype] = None,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """scattermoe/kernels/ops.py:9-18: out[t, j] = sum_h A[t, j, h] * B[t, h]."""
+    dev = _require_cuda(A, B, out)
+    if A.dim() != 3 or B.dim() != 2 or A.shape[0] != B.shape[0] or A.shape[2] != B.shape[1]:
+        raise ValueError("rowwise_sum_product: expected A [T, F, H] and B [T, H]")
+    A = A.contiguous()
+    B = B.contiguous()
+    T, F, H = A.shape
+    if out is None:
+        out = torch.empty((T, F), dtype=dtype or A.dtype, device=dev)
+    with profiling.region("rowwise_sum_product", dev):
+        L.call("zmoe_rowwise_sum_product", _ptr(A), _dtype_code(A), _ptr(B), _dtype_code(B), T, F, H, _ptr(out),
+               _dtype_code(out), _stream(dev))
+    return out
+
+
+def swiglu(H: torch.Tensor) -> torch.Tensor:
+    dev = _require_cuda(H)
+    H = H.contiguous()
+    R, two_f = H.shape
+    A = torch.empty((R, two_f // 2), dtype=H.dtype, device=dev)
+    L.call("zmoe_swiglu", _ptr(H), R, two_f // 2, _dtype_code(H), _ptr(A), _stream(dev))
+    return A
+
+
+def swiglu_backward(dA: torch.Tensor, H: torch.Tensor) -> torch.Tensor:
+    dev = _require_cuda(dA, H)
+    H = H.contiguous()
+    dA = dA.to(H.dtype).contiguous()
+    R, two_f = H.shape
+    dH = torch.empty_like(H)
+    L.call("zmoe_swiglu_backward", _ptr(dA), _ptr(H), R, two_f // 2, _dtype_code(H), _ptr(dH), _stream(dev))
+    return dH
+
+
+def bias_update_(expert_biases: torch.Tensor, expert_offsets: torch.Tensor, update_rate: float) -> torch.Tensor:
+    """main.py:161-175 in place on expert_biases (f32 [E]) from the sort's offsets."""
+    dev = _require_cuda(expert_biases, expert_offsets)
+    if expert_biases.dtype != torch.float32 or not expert_biases.is_contiguous():
+        raise ValueError("bias_update_: expert_biases must be a contiguous float32 tensor")
+    off = _idx64(expert_offsets)
+    L.call("zmoe_bias_update", _ptr(off), off.numel(), float(update_rate), _ptr(expert_biases), _stream(dev))
+    return expert_biases

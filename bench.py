@@ -1,0 +1,259 @@
+"""MoE-layer fwd+bwd throughput on one MI355X (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3]
+                    [--no-cpu-baseline]
+
+Workload (default): the full MoE layer training step
+at T=32768 tokens, d=2048, E=128 routed experts, top-8, SwiGLU f=768, plus a
+shared SwiGLU expert of width 1536, bf16 parameters and activations, synthetic
+seeded inputs (x ~ N(0,1), upstream grad ~ N(0,1), random-init weights). A step
+is one forward and one full backward of the layer (gate, shared expert, routed
+experts, combine; dX, grouped dW, gate grads). Inputs are resident in HBM before
+the timed region.
+
+Prints ONE JSON line. ``roofline`` covers the dominant grouped-GEMM launch,
+timed live with HIP events on the stream it runs on; ``cpu_baseline`` times the
+numpy oracle (float32) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.join(ROOT, "architecture-zarelga-superposition_amd")
+for _p in (ROOT, PKG_ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE-layer tokens/s fwd+bwd on 1 MI355X; grouped-GEMM MFMA util %"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (T, d, E, k, f, shared_width, backward)
+    "c2": (16384, 1024, 64, 8, 512, 0, False),
+    "c3": (32768, 2048, 128, 8, 768, 1536, True),
+    "c4": (8192, 7168, 256, 8, 2048, 2048, True),
+    "c5": (512, 2048, 128, 8, 768, 0, False),
+}
+
+GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bwd_w")
+ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "sum_k")
+
+
+def gemm_flops(name: str, launch: int, T, d, k, f) -> float:
+    """Algorithmic flops of the n-th launch of ``name`` within one step."""
+    R = T * k
+    big, small = 2.0 * R * d * 2 * f, 2.0 * R * d * f
+    if name == "glu_w1_forward":
+        return big
+    if name == "glu_w2_backward_dh":
+        return small
+    # scatter2scatter: W2 forward then W1 input grad; group_bwd_w: dW2 then dW1
+    return small if launch % 2 == 0 else big
+
+
+def row_bytes(name: str, T, d, E, k) -> float:
+    """Algorithmic HBM bytes of one launch (bf16 rows, fp32 gates, int64 ids)."""
+    R = T * k
+    return {
+        "route_topk": T * E * 2 + E * 4 + R * (8 + 4 + 4),
+        "flatten_sort_count": R * 8 * 2 + R * 8 * 2 + R * 4,
+        "combine": R * d * 2 + R * 4 + T * d * 2,
+        "combine_backward": R * d * 2 + T * d * 2 + R * (4 + 4 + 4) + R * d * 2,
+        "sum_k": R * d * 2 + T * d * 2,
+    }[name]
+
+
+def build_layer(T, d, E, k, f, fs, dev, seed=0):
+    import torch
+
+    from modeling.model_config import ModelConfig
+    from modeling.moe_layer import MoELayer
+
+    ns = fs // f if fs else 0
+    if ns * f != fs:
+        raise ValueError("shared width must be a multiple of f")
+    torch.manual_seed(seed)
+    cfg = ModelConfig(hidden_size=d, intermediate_size=f, n_experts=E + ns, n_shared_experts=ns,
+                      n_experts_per_token=k)
+    layer = MoELayer(cfg).to(dev).to(torch.bfloat16)
+    layer.gate.expert_biases.data = layer.gate.expert_biases.data.float()
+    return layer
+
+
+def cpu_baseline(T, d, E, k, f, fs, budget_s=20.0, sample_T=1024):
+    """Time the numpy oracle (float32) fwd+bwd on ``sample_T`` tokens of the workload."""
+    import numpy as np
+
+    import oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover - informational only
+        threads = len(os.sched_getaffinity(0))
+    O.set_precision(np.float32)
+    rng = np.random.default_rng(0)
+    std = np.float32(1.0 / np.sqrt(d))
+    x = rng.standard_normal((sample_T, d), dtype=np.float32)
+    dout = rng.standard_normal((sample_T, d), dtype=np.float32)
+    Wg = rng.standard_normal((E, d), dtype=np.float32) * std
+    W1 = rng.standard_normal((E, 2 * f, d), dtype=np.float32) * std
+    W2 = rng.standard_normal((E, d, f), dtype=np.float32) * std
+    shared = None
+    if fs:
+        shared = tuple(rng.standard_normal(s, dtype=np.float32) * std for s in ((fs, d), (fs, d), (d, fs)))
+    orc = O.MoELayerOracle(Wg, np.zeros(E, np.float32), W1, W2, k, shared=shared)
+    times = []
+    t_start = time.perf_counter()
+    for i in range(6):
+        t0 = time.perf_counter()
+        orc.forward(x)
+        orc.backward(dout)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s and i >= 1:
+            break
+    O.set_precision(np.float64)
+    timed = times[1:] if len(times) > 1 else times
+    sec = sum(timed) / len(timed)
+    return {
+        "value": sample_T / sec,
+        "unit": "tokens/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"numpy oracle (float32) MoE layer fwd+bwd on {sample_T} tokens of the same shape "
+                   f"(d={d}, E={E}, k={k}, f={f}, shared={fs}); mean of {len(timed)} steps after 1 warmup, "
+                   f"{sec:.2f} s/step"),
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the MoE layer would shard experts across GPUs; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from zmoe import profiling
+
+    dev = torch.device("cuda:0")
+    T, d, E, k, f, fs, backward = WORKLOADS[args.workload]
+    layer = build_layer(T, d, E, k, f, fs, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    x = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16).requires_grad_(backward)
+    dout = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16)
+    params = list(layer.parameters())
+
+    def step():
+        if backward:
+            for p in params:
+                p.grad = None
+            x.grad = None
+            out, _ = layer(x)
+            out.backward(dout)
+        else:
+            with torch.no_grad():
+                layer(x)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    profiling.reset()
+    profiling.enable(*GEMM_OPS, *ROW_OPS)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    profiling.disable()
+    ms_per_step = 1000.0 * elapsed / args.steps
+    tokens_per_s = T / (ms_per_step / 1000.0)
+
+    # per-launch kernel times from HIP events recorded on the launch stream
+    kernels = {}
+    for name in GEMM_OPS:
+        durs = profiling.durations_ms(name)
+        if not durs:
+            continue
+        per_step = len(durs) // args.steps
+        for j in range(per_step):
+            ds = durs[j::per_step]
+            fl = gemm_flops(name, j, T, d, k, f)
+            avg = sum(ds) / len(ds)
+            kernels[f"{name}#{j}"] = dict(avg_ms=avg, tflops=fl / (avg * 1e-3) / 1e12, flops=fl)
+    for name in ROW_OPS:
+        durs = profiling.durations_ms(name)
+        if not durs:
+            continue
+        avg = sum(durs) / len(durs)
+        by = row_bytes(name, T, d, E, k)
+        kernels[name] = dict(avg_ms=avg, gbs=by / (avg * 1e-3) / 1e9, bytes=by)
+    gemm = {n: v for n, v in kernels.items() if "tflops" in v}
+    dom_name = max(gemm, key=lambda n: gemm[n]["avg_ms"])
+    dom = gemm[dom_name]
+    gemm_ms = sum(v["avg_ms"] for v in gemm.values())
+    gemm_flops_total = sum(v["flops"] for v in gemm.values())
+    util = gemm_flops_total / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(T, d, E, k, f, fs)
+
+    line = {
+        "metric": METRIC,
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs and upstream grads; random-init weights)",
+        "config": {
+            "workload": (f"{args.workload}: MoE layer {'fwd+bwd' if backward else 'fwd'} T={T} d={d} E={E} "
+                         f"k={k} SwiGLU f={f}" + (f" + shared SwiGLU {fs}" if fs else "")),
+            "tokens": T, "d_model": d, "experts": E, "top_k": k, "ffn": f, "shared_ffn": fs,
+            "parallelism": "single GPU",
+        },
+        "grouped_gemm_mfma_util_pct": 100.0 * util,
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "mfma",
+            "achieved": dom["tflops"],
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": dom["tflops"] / PEAK_BF16_TFLOPS,
+            "avg_ms": dom["avg_ms"],
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    if args.verbose:
+        line["kernels"] = kernels
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,217 @@
+/*
+ * zmoe.h — C ABI of the MI355X (gfx950) MoE-layer hot path.
+ *
+ * One shared library, libzmoe_hip.so, behind the reference's ScatterMoE op
+ * layer and its aux-loss-free gate. Every entry point:
+ *   - takes caller-owned device pointers, element counts/strides (in elements),
+ *     and a hipStream_t passed as void* (NULL = the legacy default stream);
+ *   - never allocates device memory (scratch comes in through `workspace`);
+ *   - enqueues work on `stream` and returns without synchronising;
+ *   - returns ZMOE_OK or a ZMOE_ERR_* code; zmoe_last_error() gives a message
+ *     (thread-local) for the most recent failure on the calling thread.
+ * Index arrays are int64 like the reference's torch.long tensors.
+ *
+ * Reference paths (file:line) are relative to the reference repository root.
+ */
+#ifndef ZMOE_H_
+#define ZMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZMOE_ABI_VERSION 1
+
+/* element types */
+enum { ZMOE_DTYPE_F32 = 0, ZMOE_DTYPE_BF16 = 1 };
+
+/* status codes */
+enum {
+  ZMOE_OK = 0,
+  ZMOE_ERR_NULL = 1,      /* a required pointer is NULL                        */
+  ZMOE_ERR_SHAPE = 2,     /* sizes inconsistent, out of range or unsupported    */
+  ZMOE_ERR_DTYPE = 3,     /* element type not supported by this entry point     */
+  ZMOE_ERR_ALIGN = 4,     /* pointer/stride not aligned for 16-byte accesses    */
+  ZMOE_ERR_WORKSPACE = 5, /* workspace missing or smaller than required         */
+  ZMOE_ERR_HIP = 6        /* HIP runtime or launch error                        */
+};
+
+int zmoe_abi_version(void);
+const char* zmoe_status_string(int status);
+const char* zmoe_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Routing — replaces the post-projection part of MoEGate.forward,
+ * modeling/moe_gate.py:27-34 (sigmoid, +expert_biases, topk, gather,
+ * F.normalize(p=1)).
+ *   logits [T, E] (row stride E), dtype F32 or BF16; expert_biases [E] f32.
+ *   p = fp32(sigmoid_f64(logit)); if round_probs_bf16, p = bf16(p) (the
+ *   reference under bf16 autocast). s = p + bias. Slots ordered by
+ *   (s desc, expert asc); NaN ranks above all numbers.
+ *   Outputs: topk_idx [T, k] int64, topk_weight [T, k] f32 =
+ *   p_sel / max(sum p_sel, 1e-12), topk_prob [T, k] f32 = p_sel (may be NULL).
+ *   1 <= k <= E <= 1024.
+ * ------------------------------------------------------------------------- */
+int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, int E, int k,
+                    const float* expert_biases, int round_probs_bf16,
+                    int64_t* topk_idx, float* topk_weight, float* topk_prob,
+                    void* stream);
+
+/* Autograd of modeling/moe_gate.py:27,33-34: d_weight [T, k] f32 ->
+ * d_logits [T, E] (dense, zeros off the selected experts), dtype F32/BF16. */
+int zmoe_route_topk_backward(const float* d_weight, const float* topk_prob,
+                             const int64_t* topk_idx, int64_t T, int E, int k,
+                             void* d_logits, int d_logits_dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Counting and sorting — scattermoe/parallel_experts.py:6-28.
+ * ------------------------------------------------------------------------- */
+/* compileable_bincount (parallel_experts.py:6-15): counts [E] int64. Indices
+ * outside [0, E) are not counted; the workspace-free call cannot report them. */
+int zmoe_bincount(const int64_t* expert_idxs, int64_t R, int E, int64_t* counts,
+                  void* stream);
+
+/* Bytes of device workspace zmoe_flatten_sort_count needs for (R, E). */
+size_t zmoe_sort_workspace_bytes(int64_t R, int E);
+
+/* flatten_sort_count (parallel_experts.py:21-28), a stable counting sort:
+ *   sorted_expert_idxs [R], sorted_scattered_idxs [R] (flat slot ids, equal
+ *   experts in slot order), expert_offsets [E] (inclusive cumsum of counts),
+ *   all int64; inverse [R] int32 (inverse[slot] = sorted position, may be NULL).
+ * Indices outside [0, E) set the int32 flag at workspace offset 0 to 1 and are
+ * dropped (not written); read it with zmoe_sort_error_flag.                   */
+int zmoe_flatten_sort_count(const int64_t* expert_idxs, int64_t R, int E,
+                            int64_t* sorted_expert_idxs,
+                            int64_t* sorted_scattered_idxs,
+                            int64_t* expert_offsets, int32_t* inverse,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device address of the out-of-range flag inside a sort workspace. */
+const int32_t* zmoe_sort_error_flag(const void* workspace);
+
+/* expert_offsets [E] (inclusive) from an already sorted expert list; used by
+ * scatter2scatter callers that do not carry offsets (ops.py:192 signature). */
+int zmoe_offsets_from_sorted(const int64_t* sorted_expert_idxs, int64_t R, int E,
+                             int64_t* expert_offsets, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * group — scattermoe/kernels/ops.py:449-529:
+ *   Y[n, :] = A[idx[n] / fan_out, :] * coeff[idx[n]]   (coeff may be NULL)
+ * A [*, K] row stride lda; Y [N, K] row stride ldy; dtype F32/BF16 for A and Y;
+ * coeff f32 or bf16 (coeff_dtype).
+ * ------------------------------------------------------------------------- */
+int zmoe_group(const void* A, int64_t lda, int64_t K, int dtype,
+               const int64_t* sorted_idxs, int64_t N, int fan_out,
+               const void* coeff, int coeff_dtype, void* Y, int64_t ldy,
+               void* stream);
+
+/* ---------------------------------------------------------------------------
+ * scatter2scatter — scattermoe/kernels/ops.py:192-255 (grouped GEMM):
+ *   sorted row i, expert e = sorted_expert_idxs[i]:
+ *   in  = X[i] if x_grouped else X[sorted_scattered_idxs[i] / k]
+ *   out = Y[i] if y_grouped else Y[sorted_scattered_idxs[i]]
+ *   out[:] = in[:] @ W[e] (+ b[e])   with W the logical [E, K, N] operand.
+ * W strides (w_stride_k, w_stride_n): one must be 1 (the reference passes the
+ * parameter [E, N, K] as a permuted view, or its transpose in backward).
+ * expert_offsets is required (see zmoe_offsets_from_sorted).
+ * R = rows of the sorted list = (x_grouped ? M : M * k).
+ * ------------------------------------------------------------------------- */
+int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const void* W,
+                         int64_t w_stride_e, int64_t w_stride_k, int64_t w_stride_n,
+                         const void* b, int64_t b_stride_e,
+                         const int64_t* sorted_expert_idxs,
+                         const int64_t* sorted_scattered_idxs,
+                         const int64_t* expert_offsets, int64_t M, int64_t K,
+                         int64_t N, int E, int k, int x_grouped, int y_grouped,
+                         int dtype, void* Y, int64_t y_stride_m, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * group_bwd_W — scattermoe/kernels/ops.py:263-438 (grouped weight gradient):
+ *   DWt[e, n, c] = sum_{i in expert e} DY[i, n] * Xrow(i)[c]
+ *   Xrow(i) = X[i] if x_gather_idxs == NULL else X[x_gather_idxs[i] / x_gather_div]
+ *   (the gather replaces the reference's group() copy, parallel_experts.py:102).
+ * DWt [E, N, K] contiguous = the reference's DWt (its DW is DWt.permute(0,2,1));
+ * experts with no rows get exact zeros. Db [E, N] (may be NULL) = row sums.
+ * ------------------------------------------------------------------------- */
+int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X,
+                     int64_t x_stride_m, const int64_t* x_gather_idxs,
+                     int x_gather_div, const int64_t* expert_offsets, int64_t M,
+                     int64_t N, int64_t K, int E, int dtype, void* DWt, void* Db,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------
+ * rowwise_sum_product — scattermoe/kernels/ops.py:9-80:
+ *   out[t, j] = sum_h A[t, j, h] * B[t, h] (fp32 accumulation)
+ * A [T, F, H], B [T, H] contiguous; each F32 or BF16; out F32 or BF16.
+ * ------------------------------------------------------------------------- */
+int zmoe_rowwise_sum_product(const void* A, int a_dtype, const void* B, int b_dtype,
+                             int64_t T, int F, int64_t H, void* out, int out_dtype,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused GLU-expert pieces. Each replaces a sequence of reference calls.
+ * ------------------------------------------------------------------------- */
+
+/* scattermoe/mlp.py:96-102 — W1 scatter2scatter (grouped_out=True) fused with
+ * chunk(2) and silu(gates) * h:
+ *   H[i, :] = X[sorted_scattered_idxs[i] / k] @ W1[e]^T   ([R, 2f], sorted rows)
+ *   A[i, j] = silu(H[i, f + j]) * H[i, j]                 ([R, f])
+ * W1 [E, 2f, d] contiguous (ParallelExperts.weight). */
+int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
+                        const int64_t* sorted_expert_idxs,
+                        const int64_t* sorted_scattered_idxs,
+                        const int64_t* expert_offsets, int64_t T, int64_t d,
+                        int64_t f, int E, int k, int dtype, void* H, void* A,
+                        void* stream);
+
+/* scattermoe/parallel_experts.py:112-120 (W2 input grad, x_grouped and
+ * y_grouped) fused with the backward of silu(gates) * h (mlp.py:102):
+ *   dA[i, :] = dYg[i, :] @ W2[e]                 (W2 [E, d, f] contiguous)
+ *   dH[i, j]     = dA[i, j] * silu(g)             (g = H[i, f + j], h = H[i, j])
+ *   dH[i, f + j] = dA[i, j] * h * s * (1 + g (1 - s)),  s = sigmoid(g)        */
+int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const void* H,
+                            const int64_t* sorted_expert_idxs,
+                            const int64_t* expert_offsets, int64_t R, int64_t d,
+                            int64_t f, int E, int dtype, void* dH, void* stream);
+
+/* scattermoe/parallel_experts.py:161-163 (gates @ output_expanded) plus the
+ * residual sum of modeling/moe_layer.py:53:
+ *   out[t, :] = addend[t, :] + sum_j gates[t, j] * Y[t * k + j, :]
+ * Y [T*k, d] in slot order; addend may be NULL; fp32 accumulation in j order. */
+int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t T,
+                 int k, int64_t d, int dtype, void* out, void* stream);
+
+/* scattermoe/parallel_experts.py:191-208 (rowwise_sum_product + group with
+ * coeff=gates) in one pass over grad_out:
+ *   d_gates[t, j] = sum_h Y[t*k+j, h] * grad_out[t, h]
+ *   grouped_grad_out[inverse[t*k+j], :] = gates[t, j] * grad_out[t, :]       */
+int zmoe_combine_backward(const void* Y, const void* grad_out, const float* gates,
+                          const int32_t* inverse, int64_t T, int k, int64_t d,
+                          int dtype, float* d_gates, void* grouped_grad_out,
+                          void* stream);
+
+/* scattermoe/parallel_experts.py:236 (d_expanded_input.view(T,k,d).sum(-2))
+ * plus up to two addends (gate and shared-expert input grads):
+ *   out[t, :] = sum_j Xe[t*k + j, :] + add0[t, :] + add1[t, :]               */
+int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype,
+               const void* add0, const void* add1, void* out, void* stream);
+
+/* scattermoe/mlp.py:101-102 stand-alone (shapes the fused kernels reject):
+ * A = silu(H[:, f:]) * H[:, :f]; and its backward dH from (dA, H). */
+int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void* A, void* stream);
+int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f,
+                         int dtype, void* dH, void* stream);
+
+/* main.py:161-175 (aux-loss-free bias update) from the sort's offsets:
+ *   counts = diff(expert_offsets); b += rate * sign(mean(counts) - counts)    */
+int zmoe_bias_update(const int64_t* expert_offsets, int E, float update_rate,
+                     float* expert_biases, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZMOE_H_ */

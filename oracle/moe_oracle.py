@@ -34,7 +34,21 @@ from __future__ import annotations
 
 import numpy as np
 
+_PREC = {"float": np.float64}
+
+
+def set_precision(dtype) -> None:
+    """Float type of the GEMM/elementwise restatements (float64 for parity
+    checks, float32 for the timed CPU baseline). Routing math stays float64."""
+    _PREC["float"] = np.dtype(dtype).type
+
+
+def _f():
+    return _PREC["float"]
+
+
 __all__ = [
+    "set_precision",
     "bf16_round",
     "sigmoid_f32",
     "route_topk",
@@ -185,11 +199,11 @@ def inverse_permutation(sorted_scattered_idxs):
 # --------------------------------------------------------------------------- #
 def group(A, sorted_idxs, coeff=None, fan_out=1):
     """Y[n] = A[idx[n] // fan_out] * coeff[idx[n]]  (ops.py:504-519)."""
-    A = np.asarray(A, dtype=np.float64)
+    A = np.asarray(A, dtype=_f())
     idx = np.asarray(sorted_idxs, dtype=np.int64)
     Y = A[idx // fan_out]
     if coeff is not None:
-        c = np.asarray(coeff, dtype=np.float64).reshape(-1)
+        c = np.asarray(coeff, dtype=_f()).reshape(-1)
         Y = Y * c[idx][:, None]
     return Y
 
@@ -214,15 +228,15 @@ def scatter2scatter(X, W, sorted_expert_idxs, sorted_scattered_idxs, k, b=None,
     ``W`` is the logical [E, K, N] operand (the reference passes
     ``weight.permute(0, 2, 1)``); optional bias ``b`` [E, N] (:181-183).
     """
-    X = np.asarray(X, dtype=np.float64)
-    W = np.asarray(W, dtype=np.float64)
+    X = np.asarray(X, dtype=_f())
+    W = np.asarray(W, dtype=_f())
     se = np.asarray(sorted_expert_idxs, dtype=np.int64)
     ss = np.asarray(sorted_scattered_idxs, dtype=np.int64)
     R = se.size
     E, _, N = W.shape
     rows_in = np.arange(R) if x_grouped else ss // k
     rows_out = np.arange(R) if y_grouped else ss
-    Y = np.zeros((R, N), dtype=np.float64)
+    Y = np.zeros((R, N), dtype=_f())
     starts, ends = _expert_ranges(se, E)
     for e in range(E):
         s, t = starts[e], ends[e]
@@ -230,7 +244,7 @@ def scatter2scatter(X, W, sorted_expert_idxs, sorted_scattered_idxs, k, b=None,
             continue
         blk = X[rows_in[s:t]] @ W[e]
         if b is not None:
-            blk = blk + np.asarray(b, dtype=np.float64)[e][None, :]
+            blk = blk + np.asarray(b, dtype=_f())[e][None, :]
         Y[rows_out[s:t]] = blk
     return Y
 
@@ -245,12 +259,12 @@ def group_bwd_w(DY, X, expert_offsets, E, has_bias=False):
     (pre-zeroed, so an empty expert gets exactly 0). Returns DW [E, K, N] (the
     logical view the reference returns) and Db [E, N] or None (:430-438).
     """
-    DY = np.asarray(DY, dtype=np.float64)
-    X = np.asarray(X, dtype=np.float64)
+    DY = np.asarray(DY, dtype=_f())
+    X = np.asarray(X, dtype=_f())
     off = np.asarray(expert_offsets, dtype=np.int64)
     K, N = X.shape[1], DY.shape[1]
-    DW = np.zeros((E, K, N), dtype=np.float64)
-    Db = np.zeros((E, N), dtype=np.float64) if has_bias else None
+    DW = np.zeros((E, K, N), dtype=_f())
+    Db = np.zeros((E, N), dtype=_f()) if has_bias else None
     start = 0
     for e in range(E):
         end = int(off[e])
@@ -267,7 +281,7 @@ def group_bwd_w(DY, X, expert_offsets, E, has_bias=False):
 # --------------------------------------------------------------------------- #
 def rowwise_sum_product(A, B):
     """out[t, j] = sum_h A[t, j, h] * B[t, h]  (ops.py:79)."""
-    return np.einsum("tjh,th->tj", np.asarray(A, dtype=np.float64), np.asarray(B, dtype=np.float64))
+    return np.einsum("tjh,th->tj", np.asarray(A, dtype=_f()), np.asarray(B, dtype=_f()))
 
 
 # --------------------------------------------------------------------------- #
@@ -285,7 +299,7 @@ def parallel_linear_forward(x, W, k, sorted_expert_idxs, sorted_scattered_idxs,
                           x_grouped=grouped_in, y_grouped=grouped_out)
     if gates is None:
         return out, None
-    g = np.asarray(gates, dtype=np.float64)
+    g = np.asarray(gates, dtype=_f())
     T, kk = g.shape
     expanded = out.reshape(T, kk, out.shape[-1])
     return np.einsum("tj,tjn->tn", g, expanded), expanded
@@ -298,11 +312,11 @@ def parallel_linear_backward(grad_out, x, W, k, sorted_expert_idxs, sorted_scatt
 
     Returns (d_input, d_weights [E, K, N], d_biases or None, d_gates or None).
     """
-    grad_out = np.asarray(grad_out, dtype=np.float64)
+    grad_out = np.asarray(grad_out, dtype=_f())
     E = np.asarray(W).shape[0]
     if gates is not None:
         d_gates = rowwise_sum_product(output_expanded, grad_out)             # :82
-        gates_flat = np.asarray(gates, dtype=np.float64).reshape(-1)
+        gates_flat = np.asarray(gates, dtype=_f()).reshape(-1)
         gate_fan = np.asarray(gates).shape[1]
     else:
         d_gates, gates_flat, gate_fan = None, None, 1
@@ -314,7 +328,7 @@ def parallel_linear_backward(grad_out, x, W, k, sorted_expert_idxs, sorted_scatt
     grouped_x = x if grouped_in else group(x, sorted_scattered_idxs, fan_out=k)  # :98-103
     d_w, d_b = group_bwd_w(grouped_grad_out, grouped_x, expert_offsets, E,       # :105-110
                            has_bias=b is not None)
-    Wt = np.transpose(np.asarray(W, dtype=np.float64), (0, 2, 1))
+    Wt = np.transpose(np.asarray(W, dtype=_f()), (0, 2, 1))
     d_exp = scatter2scatter(grouped_grad_out, Wt, sorted_expert_idxs,            # :112-120
                             sorted_scattered_idxs, 1, x_grouped=True, y_grouped=grouped_in)
     if k == 1:
@@ -355,18 +369,18 @@ def glu_mlp_forward(x, expert_p, expert_idxs, W1, W2):
     ``nn.Parameter`` storage (the reference permutes them to [E, in, out]).
     Returns (y [T, d], cache) with the tensors the reference saves.
     """
-    x = np.asarray(x, dtype=np.float64)
+    x = np.asarray(x, dtype=_f())
     T, k = np.asarray(expert_idxs).shape
     E = np.asarray(W1).shape[0]
     se, ss, off = flatten_sort_count(expert_idxs, E)                          # :77-78
-    W1l = np.transpose(np.asarray(W1, dtype=np.float64), (0, 2, 1))
-    W2l = np.transpose(np.asarray(W2, dtype=np.float64), (0, 2, 1))
+    W1l = np.transpose(np.asarray(W1, dtype=_f()), (0, 2, 1))
+    W2l = np.transpose(np.asarray(W2, dtype=_f()), (0, 2, 1))
     H, _ = parallel_linear_forward(x, W1l, k, se, ss, off, grouped_out=True)  # :79-84
     A = swiglu(H)                                                             # :85-87
     y, y_exp = parallel_linear_forward(A, W2l, 1, se, ss, off, gates=expert_p,  # :88-93
                                        grouped_in=True)
     cache = dict(x=x, se=se, ss=ss, off=off, H=H, A=A, y_exp=y_exp,
-                 gates=np.asarray(expert_p, dtype=np.float64), k=k, W1l=W1l, W2l=W2l)
+                 gates=np.asarray(expert_p, dtype=_f()), k=k, W1l=W1l, W2l=W2l)
     return y, cache
 
 
@@ -387,19 +401,19 @@ def glu_mlp_backward(dy, cache):
 # --------------------------------------------------------------------------- #
 def shared_expert_forward(x, Wg, Wu, Wd):
     """down(silu(gate(x)) * up(x)) with nn.Linear weights [out, in]."""
-    x = np.asarray(x, dtype=np.float64)
-    g = x @ np.asarray(Wg, dtype=np.float64).T
-    u = x @ np.asarray(Wu, dtype=np.float64).T
+    x = np.asarray(x, dtype=_f())
+    g = x @ np.asarray(Wg, dtype=_f()).T
+    u = x @ np.asarray(Wu, dtype=_f()).T
     a = _silu(g) * u
-    return a @ np.asarray(Wd, dtype=np.float64).T, (x, g, u, a)
+    return a @ np.asarray(Wd, dtype=_f()).T, (x, g, u, a)
 
 
 def shared_expert_backward(dy, cache, Wg, Wu, Wd):
     x, g, u, a = cache
-    dy = np.asarray(dy, dtype=np.float64)
-    Wg = np.asarray(Wg, dtype=np.float64)
-    Wu = np.asarray(Wu, dtype=np.float64)
-    Wd = np.asarray(Wd, dtype=np.float64)
+    dy = np.asarray(dy, dtype=_f())
+    Wg = np.asarray(Wg, dtype=_f())
+    Wu = np.asarray(Wu, dtype=_f())
+    Wd = np.asarray(Wd, dtype=_f())
     dWd = dy.T @ a
     da = dy @ Wd
     s = 1.0 / (1.0 + np.exp(-g))
@@ -426,16 +440,16 @@ class MoELayerOracle:
     """
 
     def __init__(self, Wgate, expert_biases, W1, W2, k, shared=None, round_probs_bf16=False):
-        self.Wgate = np.asarray(Wgate, dtype=np.float64)
+        self.Wgate = np.asarray(Wgate, dtype=_f())
         self.bias = np.asarray(expert_biases, dtype=np.float32)
-        self.W1 = np.asarray(W1, dtype=np.float64)
-        self.W2 = np.asarray(W2, dtype=np.float64)
+        self.W1 = np.asarray(W1, dtype=_f())
+        self.W2 = np.asarray(W2, dtype=_f())
         self.k = int(k)
-        self.shared = None if shared is None else tuple(np.asarray(w, dtype=np.float64) for w in shared)
+        self.shared = None if shared is None else tuple(np.asarray(w, dtype=_f()) for w in shared)
         self.round_probs_bf16 = round_probs_bf16
 
     def forward(self, x, logits=None):
-        x = np.asarray(x, dtype=np.float64)
+        x = np.asarray(x, dtype=_f())
         if logits is None:
             logits = (x @ self.Wgate.T).astype(np.float32)                    # moe_gate.py:26
         idx, w, p_sel = route_topk(logits, self.bias, self.k, self.round_probs_bf16)
@@ -451,7 +465,7 @@ class MoELayerOracle:
     def backward(self, dout):
         """Returns dict of float64 grads: x, gate_weight, W1, W2 (+ shared_*)."""
         c = self._cache
-        dout = np.asarray(dout, dtype=np.float64)
+        dout = np.asarray(dout, dtype=_f())
         dx, dW1, dW2, d_gates = glu_mlp_backward(dout, c["mcache"])
         E = self.Wgate.shape[0]
         dz = route_topk_backward(d_gates, c["p_sel"], c["idx"], E)

@@ -1,0 +1,150 @@
+"""GPU parity of the whole MoE layer (gate -> sort -> GLU experts -> combine,
+plus the shared expert) forward and backward against the float64 oracle.
+
+Routing is compared bit-exactly from the logits the device's gate projection
+produced (the projection itself is checked with the float tolerance); outputs
+and gradients use the north-star tolerances.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+from helpers import TOL, assert_close, gen, layer_inputs, np64
+
+pytestmark = pytest.mark.gpu
+
+
+def build_layer(P, d, E, k, f, n_shared, dtype, dev, fused=True):
+    from modeling.model_config import ModelConfig
+    from modeling.moe_layer import MoELayer
+
+    cfg = ModelConfig(hidden_size=d, intermediate_size=f, n_experts=E + n_shared, n_shared_experts=n_shared,
+                      n_experts_per_token=k)
+    layer = MoELayer(cfg)
+    layer.routed_experts.fused = fused
+    with torch.no_grad():
+        layer.gate.weight.copy_(P["Wg"])
+        layer.gate.expert_biases.copy_(P["bias"])
+        layer.routed_experts.experts.weight.copy_(P["W1"])
+        layer.routed_experts.output_experts.weight.copy_(P["W2"])
+        if n_shared:
+            layer.shared_experts.gate_proj.weight.copy_(P["shared"][0])
+            layer.shared_experts.up_proj.weight.copy_(P["shared"][1])
+            layer.shared_experts.down_proj.weight.copy_(P["shared"][2])
+    layer = layer.to(dev)
+    if dtype != torch.float32:
+        layer = layer.to(dtype)
+        # .to(dtype) also rounds the fp32 buffer; restore the exact fp32 biases
+        layer.gate.expert_biases.data = P["bias"].float().to(dev)
+    return layer
+
+
+def run_and_compare(T, d, E, k, f, n_shared, dtype, dev, fused=True, bias_std=0.1, seed=0):
+    fs = f * n_shared
+    P = layer_inputs(T, d, E, k, f, fs, seed=seed, dtype=dtype, bias_std=bias_std)
+    layer = build_layer(P, d, E, k, f, n_shared, dtype, dev, fused=fused)
+    x = P["x"].to(dtype).to(dev).view(1, T, d).requires_grad_(True)
+    out, idx = layer(x)
+    out.backward(P["dout"].to(dtype).to(dev).view(1, T, d))
+
+    # the gate projection the device computed, re-run with the same call
+    with torch.no_grad():
+        logits = F.linear(x.detach().view(T, d), layer.gate.weight).float().cpu().numpy()
+    ref_logits = (np64(P["x"]) @ np64(P["Wg"]).T)
+    assert_close(logits, ref_logits, **TOL[dtype], what="gate logits")
+
+    orc = O.MoELayerOracle(np64(P["Wg"]), P["bias"].numpy(), np64(P["W1"]), np64(P["W2"]), k,
+                           shared=None if not n_shared else tuple(np64(w) for w in P["shared"]),
+                           round_probs_bf16=dtype == torch.bfloat16)
+    rout, ridx, _ = orc.forward(np64(P["x"]), logits=logits)
+    np.testing.assert_array_equal(idx.view(T, k).cpu().numpy(), ridx)
+    tol = TOL[dtype]
+    assert_close(np64(out.view(T, d)), rout, **tol, what="out")
+    g = orc.backward(np64(P["dout"]))
+    assert_close(np64(x.grad.view(T, d)), g["x"], **tol, what="dx")
+    assert_close(np64(layer.gate.weight.grad), g["gate_weight"], **tol, what="d gate.weight")
+    assert_close(np64(layer.routed_experts.experts.weight.grad), g["W1"], **tol, what="dW1")
+    assert_close(np64(layer.routed_experts.output_experts.weight.grad), g["W2"], **tol, what="dW2")
+    if n_shared:
+        se = layer.shared_experts
+        assert_close(np64(se.gate_proj.weight.grad), g["shared_gate"], **tol, what="d shared gate")
+        assert_close(np64(se.up_proj.weight.grad), g["shared_up"], **tol, what="d shared up")
+        assert_close(np64(se.down_proj.weight.grad), g["shared_down"], **tol, what="d shared down")
+    return layer
+
+
+def test_layer_c1_fp32(hip_device):
+    """BASELINE config 1 (T=2048 d=256 E=8 k=2 f=512, no shared expert) in fp32."""
+    run_and_compare(2048, 256, 8, 2, 512, 0, torch.float32, hip_device, bias_std=0.0)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_layer_small_c3_bf16(hip_device, fused):
+    """C3's structure (shared expert, k=8) at a size the oracle finishes quickly."""
+    run_and_compare(512, 512, 32, 8, 256, 2, torch.bfloat16, hip_device, fused=fused)
+
+
+def test_layer_fused_matches_composition_fp32(hip_device):
+    run_and_compare(700, 128, 16, 4, 96, 1, torch.float32, hip_device, fused=False, seed=3)
+
+
+def test_layer_unpad_indices(hip_device):
+    from modeling.model_config import ModelConfig
+    from modeling.moe_layer import MoELayer
+
+    torch.manual_seed(0)
+    cfg = ModelConfig(hidden_size=128, intermediate_size=64, n_experts=10, n_shared_experts=2, n_experts_per_token=2)
+    layer = MoELayer(cfg).to(hip_device)
+    B, S = 3, 40
+    h = torch.randn(B, S, 128, device=hip_device)
+    valid = torch.tensor([i for i in range(B * S) if (i % 7) != 3], device=hip_device)
+    out, idx = layer(h, unpad_indices=valid)
+    ref_out, ref_idx = layer(h.view(1, B * S, 128)[:, valid])
+    flat = out.view(B * S, 128)
+    assert torch.equal(flat[valid], ref_out.view(-1, 128))
+    pad = torch.ones(B * S, dtype=torch.bool, device=hip_device)
+    pad[valid] = False
+    assert (flat[pad] == 0).all() and (idx.view(B * S, -1)[pad] == 0).all()
+    assert torch.equal(idx.view(B * S, -1)[valid], ref_idx.view(-1, 2))
+
+
+def test_c3_full_size_properties(hip_device):
+    """BASELINE config 3 at full size (T=32768 d=2048 E=128 k=8 f=768, shared 1536):
+    sort invariants, linearity of the routed combine in the gates (exact for a
+    power-of-two scale), and sampled tokens against the oracle."""
+    from zmoe import ops
+    from scattermoe.mlp import GLUExpertsFunction
+
+    T, d, E, k, f = 32768, 2048, 128, 8, 768
+    g = torch.Generator(device=hip_device)
+    g.manual_seed(1)
+    x = torch.randn(T, d, device=hip_device, generator=g).to(torch.bfloat16)
+    W1 = (torch.randn(E, 2 * f, d, device=hip_device, generator=g) / d ** 0.5).to(torch.bfloat16)
+    W2 = (torch.randn(E, d, f, device=hip_device, generator=g) / d ** 0.5).to(torch.bfloat16)
+    Wg = (torch.randn(E, d, device=hip_device, generator=g) / d ** 0.5).to(torch.bfloat16)
+    bias = torch.randn(E, device=hip_device, generator=g) * 0.1
+    logits = F.linear(x, Wg)
+    idx, w, _ = ops.route_topk(logits, bias, k, round_probs_bf16=True)
+    se, ss, off, inv = ops.flatten_sort_count(idx, E)
+    assert int(off[-1]) == T * k
+    assert torch.equal(torch.sort(ss).values, torch.arange(T * k, device=hip_device))
+    assert torch.equal(se, idx.view(-1)[ss])
+    assert bool((se[1:] >= se[:-1]).all())
+    y1 = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
+    y2 = GLUExpertsFunction.apply(x, w * 2, idx, W1, W2, k, E)
+    assert torch.equal(y2.float(), (y1.float() * 2))
+    # sampled tokens vs the oracle (each token depends only on its own row)
+    rows = torch.randperm(T, generator=gen(2))[:48].to(hip_device)
+    sel_idx = idx[rows].cpu().numpy()
+    xr, wr = np64(x[rows]), w[rows].double().cpu().numpy()
+    ref = np.zeros((rows.numel(), d))
+    for e in np.unique(sel_idx):
+        W1e, W2e = np64(W1[int(e)]), np64(W2[int(e)])
+        for t, j in zip(*np.nonzero(sel_idx == e)):
+            hg = W1e @ xr[t]
+            a = O.swiglu(hg[None, :])[0]
+            ref[t] += wr[t, j] * (W2e @ a)
+    assert_close(np64(y1[rows]), ref, **TOL[torch.bfloat16], what="C3 sampled tokens")

@@ -1,0 +1,113 @@
+"""GPU parity: routing (bit-exact given logits), the stable expert sort, counts."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, gen, random_topk
+
+pytestmark = pytest.mark.gpu
+
+
+def _route_case(T, E, k, seed, dtype, bias_std, ties=False, nan=False):
+    g = gen(seed)
+    logits = torch.randn(T, E, generator=g) * 2
+    if ties:
+        logits[: T // 2] = torch.round(logits[: T // 2] * 2) / 2  # many equal logits per row
+    if nan:
+        logits[3, E // 2] = float("nan")
+    logits = logits.to(dtype)
+    bias = torch.randn(E, generator=g) * bias_std
+    if ties:
+        bias[: E // 2] = 0.0
+    return logits, bias
+
+
+@pytest.mark.parametrize("T,E,k", [(2048, 8, 2), (1000, 64, 8), (777, 128, 8), (300, 256, 8), (64, 1024, 16),
+                                   (33, 5, 5), (16, 70, 1)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_route_topk_bit_exact(hip_device, T, E, k, dtype):
+    logits, bias = _route_case(T, E, k, seed=T + E, dtype=dtype, bias_std=0.1, ties=True, nan=T > 3)
+    from zmoe import ops
+
+    rb = dtype == torch.bfloat16
+    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), k, round_probs_bf16=rb)
+    ridx, rw, rp = O.route_topk(logits.float().numpy(), bias.numpy(), k, round_probs_bf16=rb)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)  # sigmoid evaluated identically (f64, one rounding)
+    ok = ~np.isnan(rw).any(axis=1)
+    assert_close(w.cpu().numpy()[ok], rw[ok], rtol=1e-6, atol=1e-7, what="topk_weight")
+
+
+def test_route_equal_scores_and_forced_bias(hip_device):
+    from zmoe import ops
+
+    T, E, k = 128, 32, 4
+    logits = torch.zeros(T, E, device=hip_device)
+    bias = torch.zeros(E, device=hip_device)
+    idx, w, _ = ops.route_topk(logits, bias, k)
+    assert (idx.cpu() == torch.arange(k)).all()
+    assert torch.allclose(w.cpu(), torch.full((T, k), 0.25))
+    bias[17] = 50.0
+    idx, w, p = ops.route_topk(torch.randn(T, E, device=hip_device), bias, k)
+    assert (idx[:, 0] == 17).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_route_backward(hip_device, dtype):
+    from zmoe import ops
+
+    T, E, k = 500, 64, 8
+    logits, bias = _route_case(T, E, k, seed=5, dtype=dtype, bias_std=0.1)
+    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), k,
+                               round_probs_bf16=dtype == torch.bfloat16)
+    dw = torch.randn(T, k, generator=gen(6))
+    dz = ops.route_topk_backward(dw.to(hip_device), p, idx, E, torch.float32)
+    ref = O.route_topk_backward(dw.numpy(), p.cpu().numpy(), idx.cpu().numpy(), E)
+    assert_close(dz.cpu().numpy(), ref, rtol=1e-5, atol=1e-6, what="d_logits")
+
+
+@pytest.mark.parametrize("T,E,k,skew", [(2048, 8, 2, 0.0), (16384, 64, 8, 0.0), (32768, 128, 8, 0.0),
+                                        (8192, 256, 8, 1.1), (32, 128, 8, 0.0), (1, 1, 1, 0.0),
+                                        (5000, 1024, 3, 1.5)])
+def test_flatten_sort_count_bit_exact(hip_device, T, E, k, skew):
+    from zmoe import ops
+
+    idx = random_topk(T, E, k, seed=T + E, skew=skew)
+    se, ss, off, inv, ws = ops.flatten_sort_count(idx.to(hip_device), E, return_workspace=True)
+    rse, rss, roff = O.flatten_sort_count(idx.numpy(), E)
+    np.testing.assert_array_equal(se.cpu().numpy(), rse)
+    np.testing.assert_array_equal(ss.cpu().numpy(), rss)
+    np.testing.assert_array_equal(off.cpu().numpy(), roff)
+    np.testing.assert_array_equal(inv.cpu().numpy(), O.inverse_permutation(rss))
+    assert not ops.sort_out_of_range(ws)
+    np.testing.assert_array_equal(ops.bincount(idx.to(hip_device), E).cpu().numpy(), O.expert_counts(idx.numpy(), E))
+    np.testing.assert_array_equal(ops.offsets_from_sorted(se, E).cpu().numpy(), roff)
+
+
+def test_sort_empty_and_out_of_range(hip_device):
+    from zmoe import ops
+
+    empty = torch.empty(0, 8, dtype=torch.int64, device=hip_device)
+    se, ss, off, inv = ops.flatten_sort_count(empty, 16)
+    assert se.numel() == 0 and (off.cpu() == 0).all()
+    bad = torch.tensor([[0, 3], [7, 1], [2, -1]], device=hip_device)
+    se, ss, off, inv, ws = ops.flatten_sort_count(bad, 4, return_workspace=True)
+    assert ops.sort_out_of_range(ws)
+    # valid slots sorted first, the out-of-range ones after them; still a permutation
+    assert off.cpu().tolist() == [1, 2, 3, 4]
+    assert sorted(ss.cpu().tolist()) == list(range(6))
+    assert se.cpu().tolist()[:4] == [0, 1, 2, 3]
+
+
+def test_bias_update_matches_reference_rule(hip_device):
+    from zmoe import ops
+
+    T, E, k = 4096, 64, 8
+    idx = random_topk(T, E, k, seed=3, skew=0.7)
+    _, _, off, _ = ops.flatten_sort_count(idx.to(hip_device), E)
+    b0 = (torch.randn(E, generator=gen(4)) * 0.01).float()
+    b = b0.to(hip_device).clone()
+    ops.bias_update_(b, off, 1e-3)
+    np.testing.assert_array_equal(b.cpu().numpy(), O.bias_update(b0.numpy(), idx.numpy(), E, 1e-3))

@@ -1,0 +1,87 @@
+"""GPU parity: dispatch gather (group), combine, combine backward, k-sum,
+rowwise_sum_product and SwiGLU against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import TOL, assert_close, gen, np64, random_topk
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T,d,k,coeff", [(300, 256, 2, False), (300, 2048, 8, True), (77, 64, 1, True),
+                                         (1024, 7168, 8, True)])
+def test_group(hip_device, dtype, T, d, k, coeff):
+    from zmoe import ops
+
+    g = gen(T + d)
+    A = torch.randn(T, d, generator=g).to(dtype)
+    idx = torch.randperm(T * k, generator=g)
+    c = torch.randn(T * k, generator=g) if coeff else None
+    Y = ops.group(A.to(hip_device), idx.to(hip_device), coeff=None if c is None else c.to(hip_device), fan_out=k)
+    ref = O.group(np64(A), idx.numpy(), coeff=None if c is None else c.numpy(), fan_out=k)
+    if coeff:
+        # one multiply, then rounding to the storage type
+        assert_close(np64(Y), ref, rtol=2 ** -7 if dtype == torch.bfloat16 else 1e-6, atol=0, what="group")
+    else:
+        np.testing.assert_array_equal(np64(Y), ref)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T,d,k", [(513, 256, 2), (300, 2048, 8), (64, 7168, 8), (5, 96, 3)])
+def test_combine_and_backward(hip_device, dtype, T, d, k):
+    from zmoe import ops
+
+    g = gen(T * d + k)
+    Y = torch.randn(T * k, d, generator=g).to(dtype)
+    gates = torch.rand(T, k, generator=g)
+    add = torch.randn(T, d, generator=g).to(dtype)
+    dout = torch.randn(T, d, generator=g).to(dtype)
+    idx = random_topk(T, 4 * k, k, seed=1)
+    _, ss, _, inv = ops.flatten_sort_count(idx.to(hip_device), 4 * k)
+    out = ops.combine(Y.to(hip_device), gates.to(hip_device), k, addend=add.to(hip_device))
+    ref = np.einsum("tj,tjd->td", gates.double().numpy(), np64(Y).reshape(T, k, d)) + np64(add)
+    tol = TOL[dtype]
+    assert_close(np64(out), ref, **tol, what="combine")
+
+    d_gates, grouped = ops.combine_backward(Y.to(hip_device), dout.to(hip_device), gates.to(hip_device), inv)
+    ref_dg = O.rowwise_sum_product(np64(Y).reshape(T, k, d), np64(dout))
+    assert_close(d_gates.cpu().numpy(), ref_dg, rtol=1e-5, atol=1e-4, what="d_gates")
+    ref_grouped = O.group(np64(dout), ss.cpu().numpy(), coeff=gates.double().numpy().reshape(-1), fan_out=k)
+    assert_close(np64(grouped), ref_grouped, **tol, what="grouped_grad_out")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_sum_k_and_rowwise(hip_device, dtype):
+    from zmoe import ops
+
+    T, d, k = 257, 1024, 8
+    g = gen(9)
+    Xe = torch.randn(T * k, d, generator=g).to(dtype)
+    a0 = torch.randn(T, d, generator=g).to(dtype)
+    a1 = torch.randn(T, d, generator=g).to(dtype)
+    out = ops.sum_k(Xe.to(hip_device), k, a0.to(hip_device), a1.to(hip_device))
+    ref = np64(Xe).reshape(T, k, d).sum(1) + np64(a0) + np64(a1)
+    assert_close(np64(out), ref, **TOL[dtype], what="sum_k")
+    A = torch.randn(T, k, 100, generator=g).to(dtype)
+    B = torch.randn(T, 100, generator=g)
+    rs = ops.rowwise_sum_product(A.to(hip_device), B.to(hip_device), dtype=torch.float32)
+    assert_close(rs.cpu().numpy(), O.rowwise_sum_product(np64(A), np64(B)), rtol=1e-5, atol=1e-5, what="rowwise")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_swiglu(hip_device, dtype):
+    from zmoe import ops
+
+    g = gen(10)
+    H = torch.randn(333, 2 * 768, generator=g).to(dtype)
+    dA = torch.randn(333, 768, generator=g).to(dtype)
+    A = ops.swiglu(H.to(hip_device))
+    assert_close(np64(A), O.swiglu(np64(H)), **TOL[dtype], what="swiglu")
+    dH = ops.swiglu_backward(dA.to(hip_device), H.to(hip_device))
+    assert_close(np64(dH), O.swiglu_backward(np64(dA), np64(H)), **TOL[dtype], what="swiglu_backward")
