@@ -284,6 +284,8 @@ struct RowsParams {
   int K, N, E;
   int half;               // SwiGLU pair width f
   int n_tiles;
+  uint32_t a_bytes;       // addressable bytes from p.a (buffer-resource range)
+  uint32_t b_bytes;       // addressable bytes of one expert's weights
 };
 
 struct WgradParams {
@@ -297,7 +299,37 @@ struct WgradParams {
   const int64_t* offsets;
   int Ndy, Kx, E;
   int m_tiles, n_tiles;
+  uint32_t dy_bytes, x_bytes;  // addressable bytes from p.dy / p.x
 };
+
+struct RowsTile {
+  int e, nt, rows;
+  int64_t row0;
+};
+
+// Map this workgroup to (expert, m-tile, n-tile) of a rows launch; false if it has no tile.
+template <int BM>
+__device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem, RowsTile& t) {
+  int* tstart = reinterpret_cast<int*>(smem);
+  int* tmp = tstart + kGemmMaxE + 4;
+  const int mtiles = build_tile_starts<BM>(p.offsets, p.E, tstart, tmp);
+  const int logical = xcd_logical_tile(mtiles * p.n_tiles);
+  if (logical < 0) return false;
+  const int mt = logical / p.n_tiles;
+  t.nt = logical % p.n_tiles;
+  int lo = 0, hi = p.E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tstart[mid] <= mt) lo = mid;
+    else hi = mid - 1;
+  }
+  t.e = lo;
+  const int64_t e_begin = lo ? p.offsets[lo - 1] : 0;
+  t.row0 = e_begin + (int64_t)(mt - tstart[lo]) * BM;
+  t.rows = (int)min((int64_t)BM, p.offsets[lo] - t.row0);
+  __syncthreads();  // tstart is dead; LDS becomes operand stages
+  return true;
+}
 
 // ------------------------------------------------------------------ epilogue helpers
 template <typename T, int WM, int WN>
@@ -338,6 +370,89 @@ __device__ __forceinline__ void stage_acc(char* st, int pitch, const f32x16_t (&
       }
 }
 
+// Stage the accumulators through LDS and write the rows kernel's outputs.
+template <typename T, int BM, int BN, int EPI, int MI, int NI>
+__device__ __forceinline__ void rows_epilogue(const RowsParams& p, char* smem, const f32x16_t (&acc)[MI][NI],
+                                              int e, int64_t row0, int rows, int nt) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int WM = BM / 2, WN = BN / 2;
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  const int ncol0 = nt * BN;
+  using S = Stage<T, WM, WN>;
+  char* st = smem + wave * S::BYTES;
+  const T* bias_row = (EPI == EPI_STORE && p.bias) ? reinterpret_cast<const T*>(p.bias) + e * p.bias_estride : nullptr;
+  stage_acc<T, MI, NI>(st, S::PITCH, acc, bias_row, ncol0 + wn0, p.N);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  T* C = reinterpret_cast<T*>(p.c);
+  if constexpr (EPI == EPI_STORE) {
+    constexpr int CPR = WN / VEC;  // chunks per staged row
+    for (int idx = lane; idx < WM * CPR; idx += 64) {
+      const int rr = idx / CPR, cc = idx % CPR;
+      const int r = wm0 + rr;
+      const int col = ncol0 + wn0 + cc * VEC;
+      if (r < rows && col < p.N) {
+        const int64_t i = row0 + r;
+        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) =
+            *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    // staged cols: per 64-col pair block pb: [h 32 | g 32] for pair columns jj0 + pb*32 + 0..31
+    constexpr int PB = WN / 64;
+    constexpr int CPP = 32 / VEC;  // chunks per 32 columns
+    T* A2 = reinterpret_cast<T*>(p.c2);
+    for (int idx = lane; idx < WM * PB * CPP; idx += 64) {
+      const int rr = idx / (PB * CPP);
+      const int rem = idx % (PB * CPP);
+      const int pb = rem / CPP, cc = rem % CPP;
+      const int r = wm0 + rr;
+      const int jj = nt * (BN / 2) + (wn0 / 64 + pb) * 32 + cc * VEC;
+      if (r < rows && jj < p.half) {
+        const int64_t i = row0 + r;
+        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
+        const uint4 hv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + cc * VEC) * (int)sizeof(T));
+        const uint4 gv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + 32 + cc * VEC) * (int)sizeof(T));
+        float h[VEC], g[VEC], a[VEC];
+        unpack_chunk(hv, h, T{});
+        unpack_chunk(gv, g, T{});
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) a[q] = silu_f(g[q]) * h[q];
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + jj) = hv;
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + jj) = gv;
+        *reinterpret_cast<uint4*>(A2 + orow * p.ldc2 + jj) = pack_chunk(a, T{});
+      }
+    }
+  } else {  // EPI_SWIGLU_BWD: staged dA for columns ncol0 + wn0 + ...
+    constexpr int CPR = WN / VEC;
+    const T* Hs = reinterpret_cast<const T*>(p.aux);
+    for (int idx = lane; idx < WM * CPR; idx += 64) {
+      const int rr = idx / CPR, cc = idx % CPR;
+      const int r = wm0 + rr;
+      const int col = ncol0 + wn0 + cc * VEC;
+      if (r < rows && col < p.N) {
+        const int64_t i = row0 + r;
+        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
+        float da[VEC], h[VEC], g[VEC], dh[VEC], dg[VEC];
+        unpack_chunk(*reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16), da, T{});
+        unpack_chunk(ldg16(Hs + i * p.ld_aux + col), h, T{});
+        unpack_chunk(ldg16(Hs + i * p.ld_aux + p.half + col), g, T{});
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const float s = sigmoid_fast(g[q]);
+          dh[q] = da[q] * g[q] * s;
+          dg[q] = da[q] * h[q] * s * (1.f + g[q] * (1.f - s));
+        }
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = pack_chunk(dh, T{});
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + col) = pack_chunk(dg, T{});
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ rows kernel
 template <typename T, int BM, int BN, bool B_KN, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void grouped_rows_kernel(RowsParams p) {
@@ -348,24 +463,10 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_rows_kernel(RowsParams p
   constexpr int MI = WM / 32, NI = WN / 32;
   static_assert(EPI != EPI_SWIGLU || WN % 64 == 0, "SwiGLU pairs 32-column blocks inside a wave");
 
-  // ---- tile decode
-  int* tstart = reinterpret_cast<int*>(smem);
-  int* tmp = tstart + kGemmMaxE + 4;
-  const int mtiles = build_tile_starts<BM>(p.offsets, p.E, tstart, tmp);
-  const int logical = xcd_logical_tile(mtiles * p.n_tiles);
-  if (logical < 0) return;  // uniform per workgroup
-  const int mt = logical / p.n_tiles, nt = logical % p.n_tiles;
-  int lo = 0, hi = p.E - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tstart[mid] <= mt) lo = mid;
-    else hi = mid - 1;
-  }
-  const int e = lo;
-  const int64_t e_begin = e ? p.offsets[e - 1] : 0;
-  const int64_t row0 = e_begin + (int64_t)(mt - tstart[e]) * BM;
-  const int rows = (int)min((int64_t)BM, p.offsets[e] - row0);
-  __syncthreads();  // tstart is dead; LDS becomes operand stages
+  RowsTile tile;
+  if (!decode_rows_tile<BM>(p, smem, tile)) return;  // uniform per workgroup
+  const int e = tile.e, nt = tile.nt, rows = tile.rows;
+  const int64_t row0 = tile.row0;
 
   constexpr int kStage = (BM + BN) * kRowBytes;
   auto stage_a = [&](int st) { return smem + st * kStage; };
@@ -455,78 +556,30 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_rows_kernel(RowsParams p
     __syncthreads();
   }
 
-  // ---- epilogue
+  rows_epilogue<T, BM, BN, EPI>(p, smem, acc, e, row0, rows, nt);
+}
+
+template <typename T, int BM, int BN, int MI, int NI>
+__device__ __forceinline__ void wgrad_epilogue(const WgradParams& p, char* smem, const f32x16_t (&acc)[MI][NI], int e,
+                                               int m0, int n0) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int WM = BM / 2, WN = BN / 2;
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
   using S = Stage<T, WM, WN>;
   char* st = smem + wave * S::BYTES;
-  const T* bias_row = (EPI == EPI_STORE && p.bias) ? reinterpret_cast<const T*>(p.bias) + e * p.bias_estride : nullptr;
-  stage_acc<T, MI, NI>(st, S::PITCH, acc, bias_row, ncol0 + wn0, p.N);
+  stage_acc<T, MI, NI>(st, S::PITCH, acc, nullptr, 0, 0);
   __syncthreads();
-
   const int lane = threadIdx.x & 63;
-  T* C = reinterpret_cast<T*>(p.c);
-  if constexpr (EPI == EPI_STORE) {
-    constexpr int CPR = WN / VEC;  // chunks per staged row
-    for (int idx = lane; idx < WM * CPR; idx += 64) {
-      const int rr = idx / CPR, cc = idx % CPR;
-      const int r = wm0 + rr;
-      const int col = ncol0 + wn0 + cc * VEC;
-      if (r < rows && col < p.N) {
-        const int64_t i = row0 + r;
-        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) =
-            *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
-      }
-    }
-  } else if constexpr (EPI == EPI_SWIGLU) {
-    // staged cols: per 64-col pair block pb: [h 32 | g 32] for pair columns jj0 + pb*32 + 0..31
-    constexpr int PB = WN / 64;
-    constexpr int CPP = 32 / VEC;  // chunks per 32 columns
-    T* A2 = reinterpret_cast<T*>(p.c2);
-    for (int idx = lane; idx < WM * PB * CPP; idx += 64) {
-      const int rr = idx / (PB * CPP);
-      const int rem = idx % (PB * CPP);
-      const int pb = rem / CPP, cc = rem % CPP;
-      const int r = wm0 + rr;
-      const int jj = nt * (BN / 2) + (wn0 / 64 + pb) * 32 + cc * VEC;
-      if (r < rows && jj < p.half) {
-        const int64_t i = row0 + r;
-        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
-        const uint4 hv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + cc * VEC) * (int)sizeof(T));
-        const uint4 gv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + 32 + cc * VEC) * (int)sizeof(T));
-        float h[VEC], g[VEC], a[VEC];
-        unpack_chunk(hv, h, T{});
-        unpack_chunk(gv, g, T{});
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) a[q] = silu_f(g[q]) * h[q];
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + jj) = hv;
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + jj) = gv;
-        *reinterpret_cast<uint4*>(A2 + orow * p.ldc2 + jj) = pack_chunk(a, T{});
-      }
-    }
-  } else {  // EPI_SWIGLU_BWD: staged dA for columns ncol0 + wn0 + ...
-    constexpr int CPR = WN / VEC;
-    const T* Hs = reinterpret_cast<const T*>(p.aux);
-    for (int idx = lane; idx < WM * CPR; idx += 64) {
-      const int rr = idx / CPR, cc = idx % CPR;
-      const int r = wm0 + rr;
-      const int col = ncol0 + wn0 + cc * VEC;
-      if (r < rows && col < p.N) {
-        const int64_t i = row0 + r;
-        const int64_t orow = p.c_rows ? p.c_rows[i] : i;
-        float da[VEC], h[VEC], g[VEC], dh[VEC], dg[VEC];
-        unpack_chunk(*reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16), da, T{});
-        unpack_chunk(ldg16(Hs + i * p.ld_aux + col), h, T{});
-        unpack_chunk(ldg16(Hs + i * p.ld_aux + p.half + col), g, T{});
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          const float s = sigmoid_fast(g[q]);
-          dh[q] = da[q] * g[q] * s;
-          dg[q] = da[q] * h[q] * s * (1.f + g[q] * (1.f - s));
-        }
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = pack_chunk(dh, T{});
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + col) = pack_chunk(dg, T{});
-      }
-    }
+  T* DW = reinterpret_cast<T*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
+  constexpr int CPR = WN / VEC;
+  for (int idx = lane; idx < WM * CPR; idx += 64) {
+    const int rr = idx / CPR, cc = idx % CPR;
+    const int m = m0 + wm0 + rr;
+    const int n = n0 + wn0 + cc * VEC;
+    if (m < p.Ndy && n < p.Kx)
+      *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) =
+          *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
   }
 }
 
@@ -608,21 +661,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_wgrad_kernel(WgradParams
     }
   }
 
-  using S = Stage<T, WM, WN>;
-  char* st = smem + wave * S::BYTES;
-  stage_acc<T, MI, NI>(st, S::PITCH, acc, nullptr, 0, 0);
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  T* DW = reinterpret_cast<T*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
-  constexpr int CPR = WN / VEC;
-  for (int idx = lane; idx < WM * CPR; idx += 64) {
-    const int rr = idx / CPR, cc = idx % CPR;
-    const int m = m0 + wm0 + rr;
-    const int n = n0 + wn0 + cc * VEC;
-    if (m < p.Ndy && n < p.Kx)
-      *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) =
-          *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
-  }
+  wgrad_epilogue<T, BM, BN>(p, smem, acc, e, m0, n0);
 }
 
 // Db[e, n] = sum over the expert's rows of DY[i, n] (bias grad, off the GLU path).
@@ -636,6 +675,315 @@ __global__ void bias_grad_kernel(const T* __restrict__ DY, int64_t lddy, const i
   float s = 0.f;
   for (int64_t i = a; i < b; ++i) s += to_f32(DY[i * lddy + n]);
   Db[(int64_t)e * N + n] = from_f32<T>(s);
+}
+
+
+// ==================================================================== bf16 path
+// HBM -> LDS with buffer loads that write LDS directly (no staging registers,
+// no ds_write; rows past an operand's range read as zero through the buffer
+// resource's num_records), reduction-strided operands kept K-major in LDS and
+// read with ds_read_b64_tr_b16, MFMA fragments double-buffered across the four
+// 16-deep steps of each 64-deep K tile.
+typedef __attribute__((address_space(3))) char lds_char;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef short v8i16_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16;
+typedef __attribute__((address_space(3))) uint4 lds_uint4;
+
+constexpr uint32_t kOOB = 0x80000000u;  // any offset >= num_records reads zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_to_lds(__amdgpu_buffer_rsrc_t r, lds_char* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
+// K-major ("transposed") tile: [64 k-rows][COLS], 16-byte chunks XOR (row & 3) * 4:
+// the four k-rows one transpose-read touches land in four different 64-byte bank groups.
+__device__ __forceinline__ uint32_t t_off(int krow, int col, int row_bytes) {
+  return (uint32_t)(krow * row_bytes + ((((col >> 3) ^ ((krow & 3) << 2))) << 4) + ((col & 7) << 1));
+}
+
+// MFMA fragment: lane (r = lane % 32, g = lane / 32) gets k = 16 s + 8 g + 0..7 of row mn0 + r.
+template <bool TR, int BMN>
+__device__ __forceinline__ bf16x8_t frag(const lds_char* base, int mn0, int s) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (!TR) {
+    return __builtin_bit_cast(bf16x8_t,
+                              *reinterpret_cast<const lds_uint4*>(base + lds_off(mn0 + (lane & 31), 2 * s + (lane >> 5))));
+  } else {
+    // ds_read_b64_tr_b16: in each 16-lane group, lane 4a+b receives element b of the
+    // 8-byte rows addressed by lanes a, a+4, a+8, a+12. Lane s16 of group G addresses
+    // k-row (16 s + 8 g + 4 q + s16 / 4), columns mn0 + 16 (G & 1) + 4 (s16 % 4) .. +3.
+    const int G = lane >> 4, g = lane >> 5, s16 = lane & 15;
+    const int krow = 16 * s + 8 * g + (s16 >> 2);
+    const int col = mn0 + 16 * (G & 1) + 4 * (s16 & 3);
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<lds_v4i16*>(const_cast<lds_char*>(base) + t_off(krow, col, BMN * 2)));
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<lds_v4i16*>(const_cast<lds_char*>(base) + t_off(krow + 4, col, BMN * 2)));
+    const v8i16_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+template <int MI, int NI, bool A_T, bool B_T, int BM, int BN>
+__device__ __forceinline__ void mma_tile_bf16(const lds_char* la, const lds_char* lb, int wm0, int wn0,
+                                              f32x16_t (&acc)[MI][NI]) {
+  // All fragment reads of the 64-deep tile go out first (they only depend on the
+  // stage being complete); the 4 x MI x NI MFMAs then wait on them progressively.
+  // sched_barrier(0) on both sides keeps the block between the caller's global-load
+  // issue and its end-of-tile wait + barrier (MFMAs touch only registers, so the
+  // scheduler would otherwise hoist that wait above them and serialise HBM with math).
+  __builtin_amdgcn_sched_barrier(0);
+  bf16x8_t a[4][MI], b[4][NI];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) a[s][mi] = frag<A_T, BM>(la, wm0 + mi * 32, s);
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) b[s][ni] = frag<B_T, BN>(lb, wn0 + ni * 32, s);
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[s][ni], a[s][mi], acc[mi][ni], 0, 0, 0);
+  constexpr int kReads = 4 * ((A_T ? 2 : 1) * MI + (B_T ? 2 : 1) * NI);
+  __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);    // every DS read
+  __builtin_amdgcn_sched_group_barrier(0x008, 4 * MI * NI, 0);  // then every MFMA
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Rows-major tile [ROWS][64 bf16]: each wave instruction fills 8 LDS rows (1 KB);
+// lane i takes physical chunk i % 8 of row i / 8, i.e. logical chunk (i % 8) ^ swizzle(row).
+template <int ROWS>
+struct NtLoad {
+  static constexpr int NQ = ROWS / 32;  // instructions per wave per tile
+  uint32_t roff[NQ];                    // byte offset of this lane's chunk at k = 0, or kOOB
+  int kc[NQ];                           // first k element of this lane's chunk within a tile
+
+  __device__ __forceinline__ static int row_of(int q) { return 8 * ((threadIdx.x >> 6) * NQ + q) + ((threadIdx.x & 63) >> 3); }
+  __device__ __forceinline__ static int chunk_of(int q) {
+    const int r = row_of(q);
+    return (threadIdx.x & 7) ^ (((r >> 1) ^ (r >> 3)) & 7);
+  }
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, lds_char* stage, int k0, int K) const {
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const uint32_t v = (roff[q] != kOOB && k0 + kc[q] < K) ? roff[q] + (uint32_t)k0 * 2u : kOOB;
+      buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
+    }
+  }
+};
+
+// K-major tile [64][COLS]: each wave instruction fills 1 KB = 512 / COLS k-rows.
+template <int COLS>
+struct TLoad {
+  static constexpr int CPR = COLS / 8;  // chunks per k-row
+  static constexpr int NQ = CPR / 4;    // instructions per wave per tile
+  int kr[NQ];                           // k-row within the tile
+  uint32_t coff[NQ];                    // column byte offset, or kOOB past the operand's width
+
+  __device__ __forceinline__ void init(int mn0, int ncols) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int f = (w * NQ + q) * 64 + lane;
+      kr[q] = f / CPR;
+      const int c = (f % CPR) ^ ((kr[q] & 3) << 2);
+      const int col = mn0 + 8 * c;
+      coff[q] = col < ncols ? (uint32_t)col * 2u : kOOB;
+    }
+  }
+  // row_off(k) -> byte offset of k-row k (absolute within the operand's tile range) or kOOB
+  template <typename RowOff>
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, lds_char* stage, RowOff row_off) const {
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const uint32_t ro = row_off(q, kr[q]);
+      const uint32_t v = (ro == kOOB || coff[q] == kOOB) ? kOOB : ro + coff[q];
+      buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
+    }
+  }
+};
+
+template <int BM, int BN, bool B_T, int EPI>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_bf16_kernel(RowsParams p) {
+  extern __shared__ __align__(16) char smem[];
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MI = WM / 32, NI = WN / 32;
+  constexpr int kStage = (BM + BN) * kRowBytes;
+  static_assert(EPI != EPI_SWIGLU || WN % 64 == 0, "SwiGLU pairs 32-column blocks inside a wave");
+
+  RowsTile tile;
+  if (!decode_rows_tile<BM>(p, smem, tile)) return;  // uniform per workgroup
+  const int e = tile.e, nt = tile.nt, rows = tile.rows;
+  const int64_t row0 = tile.row0;
+  lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb =
+      make_rsrc(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride, p.b_bytes);
+
+  NtLoad<BM> la;
+#pragma unroll
+  for (int q = 0; q < NtLoad<BM>::NQ; ++q) {
+    const int r = NtLoad<BM>::row_of(q), c = NtLoad<BM>::chunk_of(q);
+    la.kc[q] = 8 * c;
+    if (r < rows) {
+      const int64_t i = row0 + r;
+      const int64_t src = p.a_rows ? (int64_t)((int)p.a_rows[i] / p.a_div) : i;
+      la.roff[q] = (uint32_t)(src * p.lda * 2) + 16u * c;
+    } else {
+      la.roff[q] = kOOB;
+    }
+  }
+  const int ncol0 = nt * BN;
+  NtLoad<B_T ? 32 : BN> lbn;
+  TLoad<B_T ? BN : 128> lbt;
+  if constexpr (!B_T) {
+#pragma unroll
+    for (int q = 0; q < NtLoad<BN>::NQ; ++q) {
+      const int r = NtLoad<BN>::row_of(q), c = NtLoad<BN>::chunk_of(q);
+      lbn.kc[q] = 8 * c;
+      int n;
+      bool ok;
+      if constexpr (EPI == EPI_SWIGLU) {
+        const int jj = nt * (BN / 2) + (r >> 6) * 32 + (r & 31);
+        ok = jj < p.half;
+        n = (r & 32) ? p.half + jj : jj;
+      } else {
+        n = ncol0 + r;
+        ok = n < p.N;
+      }
+      lbn.roff[q] = ok ? (uint32_t)((int64_t)n * p.ldb * 2) + 16u * c : kOOB;
+    }
+  } else {
+    lbt.init(ncol0, p.N);
+  }
+  auto issue = [&](int stage, int k0) {
+    lds_char* sa = lds + stage * kStage;
+    lds_char* sb = sa + BM * kRowBytes;
+    la.issue(ra, sa, k0, p.K);
+    if constexpr (!B_T) {
+      lbn.issue(rb, sb, k0, p.K);
+    } else {
+      lbt.issue(rb, sb, [&](int, int kr) -> uint32_t {
+        const int kk = k0 + kr;
+        return kk < p.K ? (uint32_t)((int64_t)kk * p.ldb * 2) : kOOB;
+      });
+    }
+  };
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+
+  const int nk = (p.K + 63) / 64;
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * 64);
+    const lds_char* sa = lds + cur * kStage;
+    mma_tile_bf16<MI, NI, false, B_T, BM, BN>(sa, sa + BM * kRowBytes, wm0, wn0, acc);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  rows_epilogue<uint16_t, BM, BN, EPI>(p, smem, acc, e, row0, rows, nt);
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p) {
+  extern __shared__ __align__(16) char smem[];
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MI = WM / 32, NI = WN / 32;
+  constexpr int kStage = (BM + BN) * kRowBytes;
+
+  const int per_e = p.m_tiles * p.n_tiles;
+  const int logical = xcd_logical_tile(p.E * per_e);
+  if (logical < 0) return;
+  const int e = logical / per_e;
+  const int rem = logical % per_e;
+  const int mt = rem / p.n_tiles, nt = rem % p.n_tiles;
+  const int64_t r_begin = e ? p.offsets[e - 1] : 0;
+  const int64_t r_end = p.offsets[e];
+  const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
+  const int m0 = mt * BM, n0 = nt * BN;
+  lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
+
+  const __amdgpu_buffer_rsrc_t rdy = make_rsrc(p.dy, p.dy_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.x_bytes);
+  TLoad<BM> la;
+  TLoad<BN> lb;
+  la.init(m0, p.Ndy);
+  lb.init(n0, p.Kx);
+  // gathered X rows: source row of each of this lane's k-rows, fetched one tile ahead
+  int64_t src_next[TLoad<BN>::NQ];
+  auto fetch_src = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < TLoad<BN>::NQ; ++q) {
+      const int rr = k0 + lb.kr[q];
+      const int64_t i = r_begin + (rr < nrows ? rr : 0);
+      src_next[q] = p.x_rows ? (int64_t)((int)p.x_rows[i] / p.x_div) : i;
+    }
+  };
+  auto issue = [&](int stage, int k0) {
+    lds_char* sa = lds + stage * kStage;
+    lds_char* sb = sa + BM * kRowBytes;
+    la.issue(rdy, sa, [&](int, int kr) -> uint32_t {
+      const int rr = k0 + kr;
+      return rr < nrows ? (uint32_t)((r_begin + rr) * p.lddy * 2) : kOOB;
+    });
+    lb.issue(rx, sb, [&](int q, int kr) -> uint32_t {
+      const int rr = k0 + kr;
+      return rr < nrows ? (uint32_t)(src_next[q] * p.ldx * 2) : kOOB;
+    });
+  };
+
+  const int wave = threadIdx.x >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+
+  const int nk = (nrows + 63) / 64;
+  if (nk > 0) {
+    fetch_src(0);
+    issue(0, 0);
+    if (nk > 1) fetch_src(64);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) {
+        issue(cur ^ 1, (kt + 1) * 64);
+        if (kt + 2 < nk) fetch_src((kt + 2) * 64);
+      }
+      const lds_char* sa = lds + cur * kStage;
+      mma_tile_bf16<MI, NI, true, true, BM, BN>(sa, sa + BM * kRowBytes, wm0, wn0, acc);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  wgrad_epilogue<uint16_t, BM, BN>(p, smem, acc, e, m0, n0);
 }
 
 // ------------------------------------------------------------------ host side
@@ -660,10 +1008,8 @@ int prepare(K kernel, int lds_bytes) {
   return ZMOE_OK;
 }
 
-template <typename T, int BM, int BN, bool B_KN, int EPI>
-int launch_rows(const RowsParams& p, int64_t R, hipStream_t s) {
-  constexpr int lds = rows_lds_bytes<T, BM, BN>();
-  auto kern = grouped_rows_kernel<T, BM, BN, B_KN, EPI>;
+template <typename K>
+int launch_rows_kernel(K kern, int lds, int BM, const RowsParams& p, int64_t R, hipStream_t s) {
   int rc = prepare(kern, lds);
   if (rc) return rc;
   const int64_t mt_bound = cdiv(R, BM) + (R < p.E ? R : p.E);
@@ -671,13 +1017,22 @@ int launch_rows(const RowsParams& p, int64_t R, hipStream_t s) {
   total = cdiv(total, kXcds) * kXcds;
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "grouped gemm: too many tiles");
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(kGemmThreads), lds, s, p);
-  return check_launch("grouped_rows_kernel");
+  return check_launch("grouped rows kernel");
 }
 
-template <typename T, int BM, int BN>
-int launch_wgrad(WgradParams p, hipStream_t s) {
-  constexpr int lds = rows_lds_bytes<T, BM, BN>();
-  auto kern = grouped_wgrad_kernel<T, BM, BN>;
+template <int BM, int BN, bool B_KN, int EPI>
+int launch_rows_f32(const RowsParams& p, int64_t R, hipStream_t s) {
+  return launch_rows_kernel(grouped_rows_kernel<float, BM, BN, B_KN, EPI>, rows_lds_bytes<float, BM, BN>(), BM, p,
+                            R, s);
+}
+
+template <int BM, int BN, bool B_KN, int EPI>
+int launch_rows_bf16(const RowsParams& p, int64_t R, hipStream_t s) {
+  return launch_rows_kernel(rows_bf16_kernel<BM, BN, B_KN, EPI>, rows_lds_bytes<uint16_t, BM, BN>(), BM, p, R, s);
+}
+
+template <typename K>
+int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStream_t s) {
   int rc = prepare(kern, lds);
   if (rc) return rc;
   p.m_tiles = (int)cdiv(p.Ndy, BM);
@@ -686,7 +1041,7 @@ int launch_wgrad(WgradParams p, hipStream_t s) {
   total = cdiv(total, kXcds) * kXcds;
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(kGemmThreads), lds, s, p);
-  return check_launch("grouped_wgrad_kernel");
+  return check_launch("grouped wgrad kernel");
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
@@ -698,13 +1053,13 @@ int dispatch_rows(int dtype, RowsParams p, int64_t R, int bn_for_tiles_div, hipS
   if (dtype == ZMOE_DTYPE_BF16) {
     if (use_big_tiles(R, p.E, p.N)) {
       p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 128 : 256);
-      return launch_rows<uint16_t, 256, 256, B_KN, EPI>(p, R, s);
+      return launch_rows_bf16<256, 256, B_KN, EPI>(p, R, s);
     }
     p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 64 : 128);
-    return launch_rows<uint16_t, 128, 128, B_KN, EPI>(p, R, s);
+    return launch_rows_bf16<128, 128, B_KN, EPI>(p, R, s);
   }
   p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 64 : 128);
-  return launch_rows<float, 128, 128, B_KN, EPI>(p, R, s);
+  return launch_rows_f32<128, 128, B_KN, EPI>(p, R, s);
 }
 
 }  // namespace zmoe
@@ -714,6 +1069,12 @@ using namespace zmoe;
 namespace {
 
 int vec_elems(int dtype) { return dtype == ZMOE_DTYPE_BF16 ? 8 : 4; }
+
+// Bytes addressable from a matrix base: (rows - 1) * ld + cols elements.
+int64_t span_bytes(int64_t rows, int64_t ld, int64_t cols, int dtype) {
+  return rows <= 0 ? 0 : ((rows - 1) * ld + cols) * dtype_size(dtype);
+}
+constexpr int64_t kMaxSpan = 0x7fffffffLL;  // buffer-resource ranges (offsets stay below 2^31)
 bool ok_rows(int dtype, const void* ptr, int64_t ld) {
   return aligned16(ptr) && (ld % vec_elems(dtype)) == 0;
 }
@@ -757,15 +1118,24 @@ extern "C" int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const voi
   p.K = (int)K;
   p.N = (int)N;
   p.E = E;
+  const int64_t a_span = span_bytes(M, x_stride_m, K, dtype);
+  ZMOE_REQUIRE(a_span <= kMaxSpan, ZMOE_ERR_SHAPE, "scatter2scatter: X spans more than 2 GiB");
+  p.a_bytes = (uint32_t)a_span;
   hipStream_t s = as_stream(stream);
   if (w_stride_k == 1) {  // W[e] stored [N][K]
     ZMOE_REQUIRE(w_stride_n % v == 0, ZMOE_ERR_ALIGN, "scatter2scatter: weight row stride");
     p.ldb = w_stride_n;
+    const int64_t b_span = span_bytes(N, w_stride_n, K, dtype);
+    ZMOE_REQUIRE(b_span <= kMaxSpan, ZMOE_ERR_SHAPE, "scatter2scatter: one expert's W spans more than 2 GiB");
+    p.b_bytes = (uint32_t)b_span;
     return dispatch_rows<false, EPI_STORE>(dtype, p, R, (int)N, s);
   }
   ZMOE_REQUIRE(w_stride_n == 1, ZMOE_ERR_SHAPE, "scatter2scatter: W needs unit stride along K or N");
   ZMOE_REQUIRE(w_stride_k % v == 0, ZMOE_ERR_ALIGN, "scatter2scatter: weight row stride");
   p.ldb = w_stride_k;
+  const int64_t b_span = span_bytes(K, w_stride_k, N, dtype);
+  ZMOE_REQUIRE(b_span <= kMaxSpan, ZMOE_ERR_SHAPE, "scatter2scatter: one expert's W spans more than 2 GiB");
+  p.b_bytes = (uint32_t)b_span;
   return dispatch_rows<true, EPI_STORE>(dtype, p, R, (int)N, s);
 }
 
@@ -803,6 +1173,11 @@ extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void
   p.N = (int)(2 * f);
   p.E = E;
   p.half = (int)f;
+  const int64_t a_span = span_bytes(T, x_stride_m, d, dtype), b_span = span_bytes(2 * f, d, d, dtype);
+  ZMOE_REQUIRE(a_span <= kMaxSpan && b_span <= kMaxSpan, ZMOE_ERR_SHAPE,
+               "glu_w1_forward: X or one expert's W1 spans more than 2 GiB");
+  p.a_bytes = (uint32_t)a_span;
+  p.b_bytes = (uint32_t)b_span;
   return dispatch_rows<false, EPI_SWIGLU>(dtype, p, R, (int)f, as_stream(stream));
 }
 
@@ -836,6 +1211,11 @@ extern "C" int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const vo
   p.N = (int)f;
   p.E = E;
   p.half = (int)f;
+  const int64_t a_span = span_bytes(R, d, d, dtype), b_span = span_bytes(d, f, f, dtype);
+  ZMOE_REQUIRE(a_span <= kMaxSpan && b_span <= kMaxSpan, ZMOE_ERR_SHAPE,
+               "glu_w2_backward_dh: dYg or one expert's W2 spans more than 2 GiB");
+  p.a_bytes = (uint32_t)a_span;
+  p.b_bytes = (uint32_t)b_span;
   return dispatch_rows<true, EPI_SWIGLU_BWD>(dtype, p, R, (int)f, as_stream(stream));
 }
 
@@ -865,13 +1245,21 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   p.Ndy = (int)N;
   p.Kx = (int)K;
   p.E = E;
+  const int64_t x_rows_n = x_gather_idxs ? cdiv(M, x_gather_div) : M;
+  const int64_t dy_span = span_bytes(M, dy_stride_m, N, dtype), x_span = span_bytes(x_rows_n, x_stride_m, K, dtype);
+  ZMOE_REQUIRE(dy_span <= kMaxSpan && x_span <= kMaxSpan, ZMOE_ERR_SHAPE, "group_bwd_w: DY or X spans more than 2 GiB");
+  p.dy_bytes = (uint32_t)dy_span;
+  p.x_bytes = (uint32_t)x_span;
   hipStream_t s = as_stream(stream);
   int rc;
   if (dtype == ZMOE_DTYPE_BF16) {
-    if (use_big_tiles(M, E, N) && K >= 256) rc = launch_wgrad<uint16_t, 256, 256>(p, s);
-    else rc = launch_wgrad<uint16_t, 128, 128>(p, s);
+    if (use_big_tiles(M, E, N) && K >= 256)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256>, rows_lds_bytes<uint16_t, 256, 256>(), 256, 256, p, s);
+    else
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128>, rows_lds_bytes<uint16_t, 128, 128>(), 128, 128, p, s);
   } else {
-    rc = launch_wgrad<float, 128, 128>(p, s);
+    rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
+                             s);
   }
   if (rc || Db == nullptr) return rc;
   const dim3 grid((unsigned)cdiv(N, 256), (unsigned)E), block(256);
