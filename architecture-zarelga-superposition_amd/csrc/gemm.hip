@@ -28,6 +28,8 @@
 //   * Workgroup -> tile: XCD-aware. Workgroup b runs on XCD b % 8; each XCD takes
 //     a contiguous range of the (expert, m-tile, n-tile) sequence so that tiles
 //     sharing an expert's weights and rows run on one XCD and share its L2.
+#include <cstdlib>
+
 #include "zmoe_internal.h"
 
 namespace zmoe {
@@ -367,6 +369,10 @@ __device__ __forceinline__ void stage_acc(char* st, int pitch, const f32x16_t (&
         } else {
           *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
         }
+        // One 32x32 block at a time: hoisting every accumulator read into VGPRs at
+        // once exhausts the register file and spills (scratch traffic counts on
+        // vmcnt, which would also drain in-flight operand loads).
+        if (q == 3) __builtin_amdgcn_sched_barrier(0);
       }
 }
 
@@ -682,8 +688,9 @@ __global__ void bias_grad_kernel(const T* __restrict__ DY, int64_t lddy, const i
 // HBM -> LDS with buffer loads that write LDS directly (no staging registers,
 // no ds_write; rows past an operand's range read as zero through the buffer
 // resource's num_records), reduction-strided operands kept K-major in LDS and
-// read with ds_read_b64_tr_b16, MFMA fragments double-buffered across the four
-// 16-deep steps of each 64-deep K tile.
+// read with ds_read_b64_tr_b16. The K loop runs over NS LDS stages of KS
+// reduction elements each, with NS - 1 stages of HBM loads in flight: the loop is
+// bound by load latency unless several tiles are outstanding per CU.
 typedef __attribute__((address_space(3))) char lds_char;
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef short v8i16_t __attribute__((ext_vector_type(8)));
@@ -699,95 +706,176 @@ __device__ __forceinline__ void buf_to_lds(__amdgpu_buffer_rsrc_t r, lds_char* d
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
 }
 
-// K-major ("transposed") tile: [64 k-rows][COLS], 16-byte chunks XOR (row & 3) * 4:
+// s_waitcnt immediate that waits until at most n vector-memory ops are outstanding.
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Rows-major ("non-transposed") tile: [ROWS][KS bf16], KS*2 bytes per row, 16-byte
+// chunks XOR-swizzled by row so MFMA fragment reads are bank-conflict free.
+template <int KS>
+__device__ __forceinline__ uint32_t nt_off(int row, int chunk) {
+  if constexpr (KS == 64) return (uint32_t)(row * 128 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 7)) << 4));
+  else return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+}
+template <int KS>
+__device__ __forceinline__ int nt_swz(int row) {
+  if constexpr (KS == 64) return ((row >> 1) ^ (row >> 3)) & 7;
+  else return (row >> 2) & 3;
+}
+
+// K-major ("transposed") tile: [KS k-rows][COLS], 16-byte chunks XOR (row & 3) * 4:
 // the four k-rows one transpose-read touches land in four different 64-byte bank groups.
 __device__ __forceinline__ uint32_t t_off(int krow, int col, int row_bytes) {
   return (uint32_t)(krow * row_bytes + ((((col >> 3) ^ ((krow & 3) << 2))) << 4) + ((col & 7) << 1));
 }
 
-// MFMA fragment: lane (r = lane % 32, g = lane / 32) gets k = 16 s + 8 g + 0..7 of row mn0 + r.
-template <bool TR, int BMN>
-__device__ __forceinline__ bf16x8_t frag(const lds_char* base, int mn0, int s) {
-  const int lane = threadIdx.x & 63;
-  if constexpr (!TR) {
-    return __builtin_bit_cast(bf16x8_t,
-                              *reinterpret_cast<const lds_uint4*>(base + lds_off(mn0 + (lane & 31), 2 * s + (lane >> 5))));
-  } else {
-    // ds_read_b64_tr_b16: in each 16-lane group, lane 4a+b receives element b of the
-    // 8-byte rows addressed by lanes a, a+4, a+8, a+12. Lane s16 of group G addresses
-    // k-row (16 s + 8 g + 4 q + s16 / 4), columns mn0 + 16 (G & 1) + 4 (s16 % 4) .. +3.
-    const int G = lane >> 4, g = lane >> 5, s16 = lane & 15;
-    const int krow = 16 * s + 8 * g + (s16 >> 2);
-    const int col = mn0 + 16 * (G & 1) + 4 * (s16 & 3);
-    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4i16*>(const_cast<lds_char*>(base) + t_off(krow, col, BMN * 2)));
-    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4i16*>(const_cast<lds_char*>(base) + t_off(krow + 4, col, BMN * 2)));
-    const v8i16_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(bf16x8_t, v);
-  }
-}
+// Fragment reads are inline asm: LLVM's waitcnt pass makes any LDS read it cannot
+// disambiguate (the ds_read_tr intrinsic carries no alias info) wait for every
+// in-flight LDS-DMA load, which would serialise the stage pipeline. Being asm,
+// these reads are invisible to that pass, so mma_stage_bf16 issues its own
+// lgkmcnt waits and ties the fragment registers to them with empty asm (data
+// dependencies keep every MFMA after the wait that covers its operands).
+typedef int v4i32_t __attribute__((ext_vector_type(4)));
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
 
-template <int MI, int NI, bool A_T, bool B_T, int BM, int BN>
-__device__ __forceinline__ void mma_tile_bf16(const lds_char* la, const lds_char* lb, int wm0, int wn0,
-                                              f32x16_t (&acc)[MI][NI]) {
-  // All fragment reads of the 64-deep tile go out first (they only depend on the
-  // stage being complete); the 4 x MI x NI MFMAs then wait on them progressively.
-  // sched_barrier(0) on both sides keeps the block between the caller's global-load
-  // issue and its end-of-tile wait + barrier (MFMAs touch only registers, so the
-  // scheduler would otherwise hoist that wait above them and serialise HBM with math).
-  __builtin_amdgcn_sched_barrier(0);
-  bf16x8_t a[4][MI], b[4][NI];
+__device__ __forceinline__ uint32_t lds_addr(const lds_char* p) { return (uint32_t)(uintptr_t)p; }
+
+__device__ __forceinline__ v4i32_t asm_ds_read_b128(uint32_t addr) {
+  v4i32_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ v2i32_t asm_ds_read_tr16(uint32_t addr) {
+  v2i32_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void asm_wait_lgkm() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N < 15 ? N : 15));
+}
+__device__ __forceinline__ void asm_tie(v4i32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void asm_tie(v2i32_t& v) { asm volatile("" : "+v"(v)); }
+
+// One MFMA operand fragment: lane (r = lane % 32, g = lane / 32) gets k = 16 s + 8 g + 0..7
+// of row mn0 + r, as one 16-byte register (non-transposed) or two 8-byte halves.
+template <bool TR>
+struct Frag {
+  v4i32_t w;
+  v2i32_t lo, hi;
+  static constexpr int kReads = TR ? 2 : 1;
+  template <int BMN, int KS>
+  __device__ __forceinline__ void read(const lds_char* base, int mn0, int s) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (!TR) {
+      w = asm_ds_read_b128(lds_addr(base) + nt_off<KS>(mn0 + (lane & 31), 2 * s + (lane >> 5)));
+    } else {
+      // ds_read_b64_tr_b16: in each 16-lane group, lane 4a+b receives element b of the
+      // 8-byte rows addressed by lanes a, a+4, a+8, a+12. Lane s16 of group G addresses
+      // k-row (16 s + 8 g + 4 q + s16 / 4), columns mn0 + 16 (G & 1) + 4 (s16 % 4) .. +3.
+      const int G = lane >> 4, g = lane >> 5, s16 = lane & 15;
+      const int krow = 16 * s + 8 * g + (s16 >> 2);
+      const int col = mn0 + 16 * (G & 1) + 4 * (s16 & 3);
+      lo = asm_ds_read_tr16(lds_addr(base) + t_off(krow, col, BMN * 2));
+      hi = asm_ds_read_tr16(lds_addr(base) + t_off(krow + 4, col, BMN * 2));
+    }
+  }
+  // piece h (0 .. kReads-1) of read(): lets callers spread reads between MFMAs
+  template <int BMN, int KS>
+  __device__ __forceinline__ void read_piece(const lds_char* base, int mn0, int s, int h) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (!TR) {
+      w = asm_ds_read_b128(lds_addr(base) + nt_off<KS>(mn0 + (lane & 31), 2 * s + (lane >> 5)));
+    } else {
+      const int G = lane >> 4, g = lane >> 5, s16 = lane & 15;
+      const int krow = 16 * s + 8 * g + (s16 >> 2) + 4 * h;
+      const int col = mn0 + 16 * (G & 1) + 4 * (s16 & 3);
+      const v2i32_t v = asm_ds_read_tr16(lds_addr(base) + t_off(krow, col, BMN * 2));
+      if (h == 0) lo = v;
+      else hi = v;
+    }
+  }
+  __device__ __forceinline__ void tie() {
+    if constexpr (!TR) {
+      asm_tie(w);
+    } else {
+      asm_tie(lo);
+      asm_tie(hi);
+    }
+  }
+  __device__ __forceinline__ bf16x8_t value() const {
+    if constexpr (!TR) return __builtin_bit_cast(bf16x8_t, w);
+    else return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
+  }
+};
+
+template <int MI, int NI, bool A_T, bool B_T, int BM, int BN, int KS>
+__device__ __forceinline__ void mma_stage_bf16(const lds_char* la, const lds_char* lb, int wm0, int wn0,
+                                               f32x16_t (&acc)[MI][NI]) {
+  // Every fragment read of the stage is issued first (in step order); step s then
+  // waits until only the reads of later steps are outstanding and runs its MFMAs.
+  constexpr int S = KS / 16;
+  constexpr int kPerStep = MI * Frag<A_T>::kReads + NI * Frag<B_T>::kReads;
+  Frag<A_T> a[S][MI];
+  Frag<B_T> b[S][NI];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < S; ++s) {
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) a[s][mi] = frag<A_T, BM>(la, wm0 + mi * 32, s);
+    for (int mi = 0; mi < MI; ++mi) a[s][mi].template read<BM, KS>(la, wm0 + mi * 32, s);
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) b[s][ni] = frag<B_T, BN>(lb, wn0 + ni * 32, s);
+    for (int ni = 0; ni < NI; ++ni) b[s][ni].template read<BN, KS>(lb, wn0 + ni * 32, s);
   }
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < S; ++s) {
+    if (s == 0) asm_wait_lgkm<(S - 1) * kPerStep>();
+    else if (s == 1) asm_wait_lgkm<(S - 2 > 0 ? S - 2 : 0) * kPerStep>();
+    else if (s == 2) asm_wait_lgkm<(S - 3 > 0 ? S - 3 : 0) * kPerStep>();
+    else asm_wait_lgkm<0>();
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) a[s][mi].tie();
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) b[s][ni].tie();
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[s][ni], a[s][mi], acc[mi][ni], 0, 0, 0);
-  constexpr int kReads = 4 * ((A_T ? 2 : 1) * MI + (B_T ? 2 : 1) * NI);
-  __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);    // every DS read
-  __builtin_amdgcn_sched_group_barrier(0x008, 4 * MI * NI, 0);  // then every MFMA
-  __builtin_amdgcn_sched_barrier(0);
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[s][ni].value(), a[s][mi].value(), acc[mi][ni], 0,
+                                                              0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // this step's MFMAs stay ahead of the next step's wait
+  }
 }
 
-// Rows-major tile [ROWS][64 bf16]: each wave instruction fills 8 LDS rows (1 KB);
-// lane i takes physical chunk i % 8 of row i / 8, i.e. logical chunk (i % 8) ^ swizzle(row).
-template <int ROWS>
+// Rows-major tile loader: each wave instruction fills 1 KB = 1024 / (2 KS) LDS rows;
+// lane i takes physical chunk i % (KS/8) of its row, i.e. logical chunk p ^ swizzle(row).
+template <int ROWS, int KS>
 struct NtLoad {
-  static constexpr int NQ = ROWS / 32;  // instructions per wave per tile
-  uint32_t roff[NQ];                    // byte offset of this lane's chunk at k = 0, or kOOB
-  int kc[NQ];                           // first k element of this lane's chunk within a tile
+  static constexpr int CPR = KS / 8;               // chunks per row
+  static constexpr int RPI = 64 / CPR;             // rows per instruction
+  static constexpr int NQ = ROWS / (RPI * 4);      // instructions per wave per stage
+  uint32_t roff[NQ];                               // byte offset of this lane's chunk at k = 0, or kOOB
+  int kc[NQ];                                      // first k element of the chunk within a stage
 
-  __device__ __forceinline__ static int row_of(int q) { return 8 * ((threadIdx.x >> 6) * NQ + q) + ((threadIdx.x & 63) >> 3); }
-  __device__ __forceinline__ static int chunk_of(int q) {
-    const int r = row_of(q);
-    return (threadIdx.x & 7) ^ (((r >> 1) ^ (r >> 3)) & 7);
+  __device__ __forceinline__ static int row_of(int q) {
+    return RPI * ((threadIdx.x >> 6) * NQ + q) + ((threadIdx.x & 63) / CPR);
   }
+  __device__ __forceinline__ static int chunk_of(int q) { return ((threadIdx.x & 63) % CPR) ^ nt_swz<KS>(row_of(q)); }
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, lds_char* stage, int k0, int K) const {
-    const int w = threadIdx.x >> 6;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const uint32_t v = (roff[q] != kOOB && k0 + kc[q] < K) ? roff[q] + (uint32_t)k0 * 2u : kOOB;
-      buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
-    }
+    for (int q = 0; q < NQ; ++q) issue_one(q, rs, stage, k0, K);
+  }
+  __device__ __forceinline__ void issue_one(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, int k0, int K) const {
+    const int w = threadIdx.x >> 6;
+    const uint32_t v = (roff[q] != kOOB && k0 + kc[q] < K) ? roff[q] + (uint32_t)k0 * 2u : kOOB;
+    buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
   }
 };
 
-// K-major tile [64][COLS]: each wave instruction fills 1 KB = 512 / COLS k-rows.
-template <int COLS>
+// K-major tile loader: [KS k-rows][COLS], each wave instruction fills 1 KB.
+template <int COLS, int KS>
 struct TLoad {
-  static constexpr int CPR = COLS / 8;  // chunks per k-row
-  static constexpr int NQ = CPR / 4;    // instructions per wave per tile
-  int kr[NQ];                           // k-row within the tile
-  uint32_t coff[NQ];                    // column byte offset, or kOOB past the operand's width
+  static constexpr int CPR = COLS / 8;       // chunks per k-row
+  static constexpr int NQ = KS * CPR / 256;  // instructions per wave per stage
+  int kr[NQ];                                // k-row within the stage
+  uint32_t coff[NQ];                         // column byte offset, or kOOB past the operand's width
 
   __device__ __forceinline__ void init(int mn0, int ncols) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -800,25 +888,134 @@ struct TLoad {
       coff[q] = col < ncols ? (uint32_t)col * 2u : kOOB;
     }
   }
-  // row_off(k) -> byte offset of k-row k (absolute within the operand's tile range) or kOOB
+  // row_off(q, kr) -> byte offset of k-row kr of this stage, or kOOB
   template <typename RowOff>
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, lds_char* stage, RowOff row_off) const {
-    const int w = threadIdx.x >> 6;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const uint32_t ro = row_off(q, kr[q]);
-      const uint32_t v = (ro == kOOB || coff[q] == kOOB) ? kOOB : ro + coff[q];
-      buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
-    }
+    for (int q = 0; q < NQ; ++q) issue_one(q, rs, stage, row_off);
+  }
+  template <typename RowOff>
+  __device__ __forceinline__ void issue_one(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, RowOff row_off) const {
+    const int w = threadIdx.x >> 6;
+    const uint32_t ro = row_off(q, kr[q]);
+    const uint32_t v = (ro == kOOB || coff[q] == kOOB) ? kOOB : ro + coff[q];
+    buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
   }
 };
 
+// Wait until at most `ahead` whole stages of LPS loads per wave are outstanding.
+template <int LPS>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(2 * LPS));
+  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vm_wait(LPS));
+  else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+}
+
+// The software-pipelined K loop shared by both bf16 kernels. NS LDS stages of KS = 32
+// reduction elements (two 16-deep MFMA steps each), NS - 1 stages of loads in flight.
+// The instruction order is pinned (sched_barrier(0) after every MFMA slot) so that:
+//   step 0 of stage kt: each MFMA is followed by one DMA instruction of stage
+//     kt + NS - 1 and one fragment read of step 1 of stage kt;
+//   then the stage barrier that publishes stage kt + 1 (a bare s_barrier: a
+//     __syncthreads() fence would drain every in-flight load);
+//   step 1: each MFMA is followed by one fragment read of step 0 of stage kt + 1.
+// With one wave per SIMD this keeps the matrix unit fed while loads, LDS reads and
+// the barrier are in flight. dma(q, stage, k0) issues load instruction q (0..LPS-1)
+// of a stage; prefetch(k0) readies inputs of the dma for k0 (gather indices).
+template <int NS, int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch>
+__device__ __forceinline__ void kloop_interleaved(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI],
+                                                  Dma dma, Prefetch prefetch) {
+  constexpr int KS = 32;
+  constexpr int kStage = (BM + BN) * KS * 2;
+  constexpr int AR = Frag<A_T>::kReads, BR = Frag<B_T>::kReads;
+  constexpr int NREAD = MI * AR + NI * BR;  // fragment reads per step
+  constexpr int NMMA = MI * NI;             // MFMAs per step
+  constexpr int RPS = (NREAD + NMMA - 1) / NMMA;  // reads per MFMA slot
+  constexpr int DPS = (LPS + NMMA - 1) / NMMA;    // DMA instructions per MFMA slot
+  Frag<A_T> fa[2][MI];
+  Frag<B_T> fb[2][NI];
+  auto read_piece = [&](int buf, const lds_char* st, int s, int i) {
+    if (i < MI * AR) {
+      fa[buf][i / AR].template read_piece<BM, KS>(st, wm0 + (i / AR) * 32, s, i % AR);
+    } else {
+      const int j = i - MI * AR;
+      fb[buf][j / BR].template read_piece<BN, KS>(st + BM * KS * 2, wn0 + (j / BR) * 32, s, j % BR);
+    }
+  };
+  auto tie = [&](int buf) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) fa[buf][mi].tie();
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) fb[buf][ni].tie();
+  };
+  if (nk <= 0) return;
+  prefetch(0);
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j) {
+    if (j < nk) {
+#pragma unroll
+      for (int q = 0; q < LPS; ++q) dma(q, j, j * KS);
+      if (j + 1 < nk) prefetch((j + 1) * KS);
+    }
+  }
+  wait_stages<LPS>(min(nk - 1, NS - 2));
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < NREAD; ++i) read_piece(0, lds, 0, i);
+  asm_wait_lgkm<0>();
+  tie(0);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const lds_char* st = lds + (kt % NS) * kStage;
+    const bool dma_next = kt + NS - 1 < nk;
+    lds_char* dst = lds + ((kt + NS - 1) % NS) * kStage;
+    const int dk0 = (kt + NS - 1) * KS;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NMMA; ++i) {
+      acc[i / NI][i % NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][i % NI].value(), fa[0][i / NI].value(),
+                                                                    acc[i / NI][i % NI], 0, 0, 0);
+#pragma unroll
+      for (int d = 0; d < DPS; ++d)
+        if (i * DPS + d < LPS && dma_next) dma(i * DPS + d, (int)((dst - lds) / kStage), dk0);
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+        if (i * RPS + r < NREAD) read_piece(1, st, 1, i * RPS + r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm_wait_lgkm<0>();
+    tie(1);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      wait_stages<LPS>(min(nk - 2 - kt, NS - 2));
+      asm volatile("s_barrier" ::: "memory");
+    }
+    if (kt + NS < nk) prefetch((kt + NS) * KS);
+    const lds_char* st1 = lds + ((kt + 1) % NS) * kStage;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NMMA; ++i) {
+      acc[i / NI][i % NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][i % NI].value(), fa[1][i / NI].value(),
+                                                                    acc[i / NI][i % NI], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+        if (i * RPS + r < NREAD && more) read_piece(0, st1, 0, i * RPS + r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (more) {
+      asm_wait_lgkm<0>();
+      tie(0);
+    }
+  }
+}
+
 template <int BM, int BN, bool B_T, int EPI>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_bf16_kernel(RowsParams p) {
+__global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   extern __shared__ __align__(16) char smem[];
+  constexpr int KS = 32, NS = 4;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MI = WM / 32, NI = WN / 32;
-  constexpr int kStage = (BM + BN) * kRowBytes;
+  constexpr int kStage = (BM + BN) * KS * 2;
   static_assert(EPI != EPI_SWIGLU || WN % 64 == 0, "SwiGLU pairs 32-column blocks inside a wave");
 
   RowsTile tile;
@@ -831,10 +1028,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1,
   const __amdgpu_buffer_rsrc_t rb =
       make_rsrc(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride, p.b_bytes);
 
-  NtLoad<BM> la;
+  using LA = NtLoad<BM, KS>;
+  LA la;
 #pragma unroll
-  for (int q = 0; q < NtLoad<BM>::NQ; ++q) {
-    const int r = NtLoad<BM>::row_of(q), c = NtLoad<BM>::chunk_of(q);
+  for (int q = 0; q < LA::NQ; ++q) {
+    const int r = LA::row_of(q), c = LA::chunk_of(q);
     la.kc[q] = 8 * c;
     if (r < rows) {
       const int64_t i = row0 + r;
@@ -845,12 +1043,14 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1,
     }
   }
   const int ncol0 = nt * BN;
-  NtLoad<B_T ? 32 : BN> lbn;
-  TLoad<B_T ? BN : 128> lbt;
+  using LBN = NtLoad<B_T ? 64 : BN, KS>;
+  using LBT = TLoad<B_T ? BN : 128, KS>;
+  LBN lbn;
+  LBT lbt;
   if constexpr (!B_T) {
 #pragma unroll
-    for (int q = 0; q < NtLoad<BN>::NQ; ++q) {
-      const int r = NtLoad<BN>::row_of(q), c = NtLoad<BN>::chunk_of(q);
+    for (int q = 0; q < LBN::NQ; ++q) {
+      const int r = LBN::row_of(q), c = LBN::chunk_of(q);
       lbn.kc[q] = 8 * c;
       int n;
       bool ok;
@@ -867,14 +1067,16 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1,
   } else {
     lbt.init(ncol0, p.N);
   }
-  auto issue = [&](int stage, int k0) {
+  constexpr int LPS = LA::NQ + (B_T ? LBT::NQ : LBN::NQ);
+  auto dma = [&](int q, int stage, int k0) {
     lds_char* sa = lds + stage * kStage;
-    lds_char* sb = sa + BM * kRowBytes;
-    la.issue(ra, sa, k0, p.K);
-    if constexpr (!B_T) {
-      lbn.issue(rb, sb, k0, p.K);
+    lds_char* sb = sa + BM * KS * 2;
+    if (q < LA::NQ) {
+      la.issue_one(q, ra, sa, k0, p.K);
+    } else if constexpr (!B_T) {
+      lbn.issue_one(q - LA::NQ, rb, sb, k0, p.K);
     } else {
-      lbt.issue(rb, sb, [&](int, int kr) -> uint32_t {
+      lbt.issue_one(q - LA::NQ, rb, sb, [&](int, int kr) -> uint32_t {
         const int kk = k0 + kr;
         return kk < p.K ? (uint32_t)((int64_t)kk * p.ldb * 2) : kOOB;
       });
@@ -891,27 +1093,18 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1,
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
 
-  const int nk = (p.K + 63) / 64;
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * 64);
-    const lds_char* sa = lds + cur * kStage;
-    mma_tile_bf16<MI, NI, false, B_T, BM, BN>(sa, sa + BM * kRowBytes, wm0, wn0, acc);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
+  kloop_interleaved<NS, LPS, MI, NI, false, B_T, BM, BN>((p.K + KS - 1) / KS, lds, wm0, wn0, acc, dma, [](int) {});
+  __syncthreads();  // every wave done with the stages before LDS is reused
   rows_epilogue<uint16_t, BM, BN, EPI>(p, smem, acc, e, row0, rows, nt);
 }
 
 template <int BM, int BN>
 __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
+  constexpr int KS = 32, NS = 4;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MI = WM / 32, NI = WN / 32;
-  constexpr int kStage = (BM + BN) * kRowBytes;
+  constexpr int kStage = (BM + BN) * KS * 2;
 
   const int per_e = p.m_tiles * p.n_tiles;
   const int logical = xcd_logical_tile(p.E * per_e);
@@ -927,31 +1120,64 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
 
   const __amdgpu_buffer_rsrc_t rdy = make_rsrc(p.dy, p.dy_bytes);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.x_bytes);
-  TLoad<BM> la;
-  TLoad<BN> lb;
+  using LA = TLoad<BM, KS>;
+  using LB = TLoad<BN, KS>;
+  LA la;
+  LB lb;
   la.init(m0, p.Ndy);
   lb.init(n0, p.Kx);
-  // gathered X rows: source row of each of this lane's k-rows, fetched one tile ahead
-  int64_t src_next[TLoad<BN>::NQ];
+  constexpr int LPS = LA::NQ + LB::NQ;
+  // Each wave owns k-rows 8 w .. 8 w + 7 of every stage (KS = 32 over 4 waves). The
+  // gather indices of those rows come through scalar loads one stage ahead: they
+  // count on lgkmcnt, so waiting for them never drains the in-flight LDS loads.
+  static_assert(KS == 32 && LB::NQ * 64 / LB::CPR == 8, "8 k-rows per wave per stage");
+  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  typedef const __attribute__((address_space(4))) int64_t cidx_t;
+  cidx_t* xr = (cidx_t*)(p.x_rows);  // global -> constant address space (scalar loads)
+  int src_rows[8];  // gather indices (< 2^31) of the wave's 8 k-rows of the next stage
   auto fetch_src = [&](int k0) {
 #pragma unroll
-    for (int q = 0; q < TLoad<BN>::NQ; ++q) {
-      const int rr = k0 + lb.kr[q];
-      const int64_t i = r_begin + (rr < nrows ? rr : 0);
-      src_next[q] = p.x_rows ? (int64_t)((int)p.x_rows[i] / p.x_div) : i;
+    for (int j = 0; j < 8; ++j) {
+      int rr = k0 + 8 * wu + j;
+      rr = rr < nrows ? rr : nrows - 1;
+      src_rows[j] = (int)xr[r_begin + rr];
     }
   };
-  auto issue = [&](int stage, int k0) {
-    lds_char* sa = lds + stage * kStage;
-    lds_char* sb = sa + BM * kRowBytes;
-    la.issue(rdy, sa, [&](int, int kr) -> uint32_t {
+  auto a_row = [&](int k0) {
+    return [=](int, int kr) -> uint32_t {
       const int rr = k0 + kr;
       return rr < nrows ? (uint32_t)((r_begin + rr) * p.lddy * 2) : kOOB;
-    });
-    lb.issue(rx, sb, [&](int q, int kr) -> uint32_t {
-      const int rr = k0 + kr;
-      return rr < nrows ? (uint32_t)(src_next[q] * p.ldx * 2) : kOOB;
-    });
+    };
+  };
+  auto dma = [&](int q, int stage, int k0) {
+    lds_char* sa = lds + stage * kStage;
+    lds_char* sb = sa + BM * KS * 2;
+    if (q < LA::NQ) {
+      la.issue_one(q, rdy, sa, a_row(k0));
+    } else if (p.x_rows != nullptr) {
+      lb.issue_one(q - LA::NQ, rx, sb, [&](int qq, int kr) -> uint32_t {
+        const int rr = k0 + kr;
+        if (rr >= nrows) return kOOB;
+        // this lane's row is qq * RPI + sub of the wave's 8; qq is a compile-time constant
+        // here (unrolled), so the pick below uses constant indices (no scratch array)
+        constexpr int RPI = 64 / LB::CPR;
+        static_assert(RPI == 2 || RPI == 4, "2 or 4 k-rows per load instruction");
+        const int sub = (int)(threadIdx.x & 63) / LB::CPR;
+        // branch-free pick (a select chain gets turned back into a scratch-array index)
+        const int m1 = -(sub & 1);
+        int v = src_rows[qq * RPI] ^ ((src_rows[qq * RPI] ^ src_rows[qq * RPI + 1]) & m1);
+        if constexpr (RPI == 4) {
+          const int hi = src_rows[qq * RPI + 2] ^ ((src_rows[qq * RPI + 2] ^ src_rows[qq * RPI + 3]) & m1);
+          v = v ^ ((v ^ hi) & -((sub >> 1) & 1));
+        }
+        return (uint32_t)((int64_t)(v / p.x_div) * p.ldx * 2);
+      });
+    } else {
+      lb.issue_one(q - LA::NQ, rx, sb, [&](int, int kr) -> uint32_t {
+        const int rr = k0 + kr;
+        return rr < nrows ? (uint32_t)((r_begin + rr) * p.ldx * 2) : kOOB;
+      });
+    }
   };
 
   const int wave = threadIdx.x >> 6;
@@ -964,25 +1190,10 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
 
-  const int nk = (nrows + 63) / 64;
-  if (nk > 0) {
-    fetch_src(0);
-    issue(0, 0);
-    if (nk > 1) fetch_src(64);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) {
-        issue(cur ^ 1, (kt + 1) * 64);
-        if (kt + 2 < nk) fetch_src((kt + 2) * 64);
-      }
-      const lds_char* sa = lds + cur * kStage;
-      mma_tile_bf16<MI, NI, true, true, BM, BN>(sa, sa + BM * kRowBytes, wm0, wn0, acc);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-  }
+  kloop_interleaved<NS, LPS, MI, NI, true, true, BM, BN>((nrows + KS - 1) / KS, lds, wm0, wn0, acc, dma, [&](int k0) {
+    if (p.x_rows != nullptr) fetch_src(k0);
+  });
+  __syncthreads();  // every wave done with the stages before LDS is reused
   wgrad_epilogue<uint16_t, BM, BN>(p, smem, acc, e, m0, n0);
 }
 
@@ -1045,7 +1256,16 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
-inline bool use_big_tiles(int64_t R, int E, int64_t N) { return R >= (int64_t)E * 256 && N >= 256; }
+// ZMOE_GEMM_TILE=128|256 pins the choice (a tuning knob; unset = automatic).
+inline bool use_big_tiles(int64_t R, int E, int64_t N) {
+  static const int forced = [] {
+    const char* v = getenv("ZMOE_GEMM_TILE");
+    return v ? atoi(v) : 0;
+  }();
+  if (forced == 128) return false;
+  if (forced == 256) return N >= 256;
+  return R >= (int64_t)E * 256 && N >= 256;
+}
 
 template <bool B_KN, int EPI>
 int dispatch_rows(int dtype, RowsParams p, int64_t R, int bn_for_tiles_div, hipStream_t s) {
