@@ -297,6 +297,7 @@ struct WgradParams {
   int64_t ldx;
   const int64_t* x_rows;
   int x_div;
+  int x_div_shift;  // log2(x_div) when x_div is a power of two, else -1
   void* dw;  // [E, Ndy, Kx]
   const int64_t* offsets;
   int Ndy, Kx, E;
@@ -808,130 +809,104 @@ struct Frag {
   }
 };
 
-template <int MI, int NI, bool A_T, bool B_T, int BM, int BN, int KS>
-__device__ __forceinline__ void mma_stage_bf16(const lds_char* la, const lds_char* lb, int wm0, int wn0,
-                                               f32x16_t (&acc)[MI][NI]) {
-  // Every fragment read of the stage is issued first (in step order); step s then
-  // waits until only the reads of later steps are outstanding and runs its MFMAs.
-  constexpr int S = KS / 16;
-  constexpr int kPerStep = MI * Frag<A_T>::kReads + NI * Frag<B_T>::kReads;
-  Frag<A_T> a[S][MI];
-  Frag<B_T> b[S][NI];
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) a[s][mi].template read<BM, KS>(la, wm0 + mi * 32, s);
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) b[s][ni].template read<BN, KS>(lb, wn0 + ni * 32, s);
-  }
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    if (s == 0) asm_wait_lgkm<(S - 1) * kPerStep>();
-    else if (s == 1) asm_wait_lgkm<(S - 2 > 0 ? S - 2 : 0) * kPerStep>();
-    else if (s == 2) asm_wait_lgkm<(S - 3 > 0 ? S - 3 : 0) * kPerStep>();
-    else asm_wait_lgkm<0>();
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) a[s][mi].tie();
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) b[s][ni].tie();
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[s][ni].value(), a[s][mi].value(), acc[mi][ni], 0,
-                                                              0, 0);
-    __builtin_amdgcn_sched_barrier(0);  // this step's MFMAs stay ahead of the next step's wait
-  }
-}
-
-// Rows-major tile loader: each wave instruction fills 1 KB = 1024 / (2 KS) LDS rows;
-// lane i takes physical chunk i % (KS/8) of its row, i.e. logical chunk p ^ swizzle(row).
-template <int ROWS, int KS>
-struct NtLoad {
-  static constexpr int CPR = KS / 8;               // chunks per row
-  static constexpr int RPI = 64 / CPR;             // rows per instruction
-  static constexpr int NQ = ROWS / (RPI * 4);      // instructions per wave per stage
-  uint32_t roff[NQ];                               // byte offset of this lane's chunk at k = 0, or kOOB
-  int kc[NQ];                                      // first k element of the chunk within a stage
+// Rows-major tile loader: [ROWS][64 bf16] per stage, the reduction dim contiguous in
+// HBM. Each wave instruction fills 1 KB of LDS = 8 rows x one 128-byte line; lane i
+// takes physical chunk i % 8 of its row, i.e. logical chunk (i % 8) ^ swizzle(row).
+// Offsets are relative to the stage's buffer resource (based at k0), so issuing a
+// load costs no vector ALU work: the per-stage advance lives in the scalar resource.
+template <int ROWS>
+struct RowLoad {
+  static constexpr int NQ = ROWS / 32;  // instructions per wave per stage
+  uint32_t off[NQ];                     // byte offset of this lane's chunk at k0 = 0, or kOOB
+  uint32_t tail[NQ];                    // the same for the final partial stage (chunks past K: kOOB)
 
   __device__ __forceinline__ static int row_of(int q) {
-    return RPI * ((threadIdx.x >> 6) * NQ + q) + ((threadIdx.x & 63) / CPR);
+    return 8 * ((int)(threadIdx.x >> 6) * NQ + q) + (int)((threadIdx.x & 63) >> 3);
   }
-  __device__ __forceinline__ static int chunk_of(int q) { return ((threadIdx.x & 63) % CPR) ^ nt_swz<KS>(row_of(q)); }
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, lds_char* stage, int k0, int K) const {
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) issue_one(q, rs, stage, k0, K);
+  __device__ __forceinline__ static int chunk_of(int q) { return (int)(threadIdx.x & 7) ^ nt_swz<64>(row_of(q)); }
+  // row_off: byte offset of the row at k = 0, or kOOB; ktail = K % 64 (0: no partial stage)
+  __device__ __forceinline__ void set(int q, uint32_t row_off, int ktail) {
+    const int c = chunk_of(q);
+    off[q] = row_off == kOOB ? kOOB : row_off + 16u * (uint32_t)c;
+    tail[q] = (ktail == 0 || 8 * c < ktail) ? off[q] : kOOB;
   }
-  __device__ __forceinline__ void issue_one(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, int k0, int K) const {
-    const int w = threadIdx.x >> 6;
-    const uint32_t v = (roff[q] != kOOB && k0 + kc[q] < K) ? roff[q] + (uint32_t)k0 * 2u : kOOB;
-    buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
+  __device__ __forceinline__ void issue(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, int wu, bool last) const {
+    buf_to_lds(rs, stage + (wu * NQ + q) * 1024, last ? tail[q] : off[q]);
   }
 };
 
-// K-major tile loader: [KS k-rows][COLS], each wave instruction fills 1 KB.
-template <int COLS, int KS>
-struct TLoad {
+// K-major tile loader: [64 k-rows][COLS] per stage, COLS contiguous in HBM. Each
+// wave instruction fills 1 KB = RPI k-rows; wave w covers k-rows 16 w .. 16 w + 15.
+template <int COLS>
+struct KLoad {
   static constexpr int CPR = COLS / 8;       // chunks per k-row
-  static constexpr int NQ = KS * CPR / 256;  // instructions per wave per stage
-  int kr[NQ];                                // k-row within the stage
-  uint32_t coff[NQ];                         // column byte offset, or kOOB past the operand's width
+  static constexpr int NQ = 64 * CPR / 256;  // instructions per wave per stage
+  static constexpr int RPI = 64 / CPR;       // k-rows per instruction
+  static_assert(NQ * RPI == 16, "16 k-rows per wave per stage");
+  uint32_t coff[NQ];  // column byte offset of this lane's chunk, or kOOB past the operand's width
+  uint32_t voff[NQ];  // coff + (k-row within the stage) * row pitch, or kOOB
 
-  __device__ __forceinline__ void init(int mn0, int ncols) {
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __device__ __forceinline__ static int krow_of(int q) {
+    return (((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63)) / CPR;
+  }
+  // k-row of this lane within its wave's 16 for instruction q: q * RPI + sub()
+  __device__ __forceinline__ static int sub() { return (int)(threadIdx.x & 63) / CPR; }
+  __device__ __forceinline__ void init(int mn0, int ncols, int64_t pitch_bytes) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const int f = (w * NQ + q) * 64 + lane;
-      kr[q] = f / CPR;
-      const int c = (f % CPR) ^ ((kr[q] & 3) << 2);
+      const int f = ((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63);
+      const int kr = f / CPR;
+      const int c = (f % CPR) ^ ((kr & 3) << 2);
       const int col = mn0 + 8 * c;
       coff[q] = col < ncols ? (uint32_t)col * 2u : kOOB;
+      voff[q] = col < ncols ? (uint32_t)((int64_t)kr * pitch_bytes) + coff[q] : kOOB;
     }
   }
-  // row_off(q, kr) -> byte offset of k-row kr of this stage, or kOOB
-  template <typename RowOff>
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, lds_char* stage, RowOff row_off) const {
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) issue_one(q, rs, stage, row_off);
+  __device__ __forceinline__ void issue(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, int wu) const {
+    buf_to_lds(rs, stage + (wu * NQ + q) * 1024, voff[q]);
   }
-  template <typename RowOff>
-  __device__ __forceinline__ void issue_one(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, RowOff row_off) const {
-    const int w = threadIdx.x >> 6;
-    const uint32_t ro = row_off(q, kr[q]);
-    const uint32_t v = (ro == kOOB || coff[q] == kOOB) ? kOOB : ro + coff[q];
-    buf_to_lds(rs, stage + (w * NQ + q) * 1024, v);
+  __device__ __forceinline__ void issue_at(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, int wu,
+                                           uint32_t v) const {
+    buf_to_lds(rs, stage + (wu * NQ + q) * 1024, v);
   }
 };
 
-// Wait until at most `ahead` whole stages of LPS loads per wave are outstanding.
-template <int LPS>
-__device__ __forceinline__ void wait_stages(int ahead) {
-  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(2 * LPS));
-  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vm_wait(LPS));
-  else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+// Buffer resource for the rows [row0 + k0, rows_end) of a row-major operand whose
+// rows are `pitch` bytes apart: loads at or past rows_end read zero, and so does
+// every load when `on` is false (stages past the end of the loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const char* base, uint32_t span, int64_t first_byte,
+                                                           int64_t valid_bytes, bool on) {
+  const int64_t room = (int64_t)span - first_byte;
+  const int64_t n = valid_bytes < room ? valid_bytes : room;
+  return make_rsrc(base + first_byte, (on && n > 0) ? (uint32_t)n : 0u);
 }
 
-// The software-pipelined K loop shared by both bf16 kernels. NS LDS stages of KS = 32
-// reduction elements (two 16-deep MFMA steps each), NS - 1 stages of loads in flight.
-// The instruction order is pinned (sched_barrier(0) after every MFMA slot) so that:
-//   step 0 of stage kt: each MFMA is followed by one DMA instruction of stage
-//     kt + NS - 1 and one fragment read of step 1 of stage kt;
-//   then the stage barrier that publishes stage kt + 1 (a bare s_barrier: a
-//     __syncthreads() fence would drain every in-flight load);
-//   step 1: each MFMA is followed by one fragment read of step 0 of stage kt + 1.
-// With one wave per SIMD this keeps the matrix unit fed while loads, LDS reads and
-// the barrier are in flight. dma(q, stage, k0) issues load instruction q (0..LPS-1)
-// of a stage; prefetch(k0) readies inputs of the dma for k0 (gather indices).
-template <int NS, int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch>
-__device__ __forceinline__ void kloop_interleaved(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI],
-                                                  Dma dma, Prefetch prefetch) {
-  constexpr int KS = 32;
+// The software-pipelined K loop of both bf16 kernels: two LDS stages of 64 reduction
+// elements (four 16-deep MFMA steps each). Per stage kt (buffer kt & 1):
+//   steps 0..2: each MFMA slot issues the fragment reads of the next step;
+//   barrier (after step 2): this wave's loads of stage kt + 1 have landed and every
+//     wave has read all of stage kt, so stage kt + 1 is readable and buffer kt & 1
+//     is free;
+//   step 3: reads step 0 of stage kt + 1, and starts stage kt + 2's loads into
+//     buffer kt & 1; the rest of those loads go out during step 0 of stage kt + 1.
+// Stage kt + 2's loads thus have steps 1 and 2 of stage kt + 1 to land. Slots are
+// pinned with sched_barrier(0); one wave per SIMD keeps the matrix unit fed while
+// loads, LDS reads and the barrier are in flight.
+// dma(q, buf, kt, on) issues load instruction q (0..LPS-1) of stage kt into buffer
+// buf (reading zeros when !on); prefetch(kt) readies the gather indices of stage kt.
+template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch>
+__device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI], Dma dma,
+                                        Prefetch prefetch) {
+  constexpr int KS = 64;
   constexpr int kStage = (BM + BN) * KS * 2;
   constexpr int AR = Frag<A_T>::kReads, BR = Frag<B_T>::kReads;
-  constexpr int NREAD = MI * AR + NI * BR;  // fragment reads per step
-  constexpr int NMMA = MI * NI;             // MFMAs per step
+  constexpr int NREAD = MI * AR + NI * BR;        // fragment reads per step
+  constexpr int NMMA = MI * NI;                   // MFMAs per step
   constexpr int RPS = (NREAD + NMMA - 1) / NMMA;  // reads per MFMA slot
-  constexpr int DPS = (LPS + NMMA - 1) / NMMA;    // DMA instructions per MFMA slot
+  constexpr int WIN = 2 * NMMA;                   // load window: step 3 + step 0
+  // load j goes to window slot j * WIN / LPS (evenly spread); loads in slots < NMMA
+  // belong to step 3 of the previous stage
+  constexpr int kEarly = (NMMA * LPS + WIN - 1) / WIN;  // loads j with j * WIN / LPS < NMMA
   Frag<A_T> fa[2][MI];
   Frag<B_T> fb[2][NI];
   auto read_piece = [&](int buf, const lds_char* st, int s, int i) {
@@ -948,17 +923,36 @@ __device__ __forceinline__ void kloop_interleaved(int nk, lds_char* lds, int wm0
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) fb[buf][ni].tie();
   };
+  auto mma = [&](int buf, int i) {
+    acc[i / NI][i % NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[buf][i % NI].value(), fa[buf][i / NI].value(),
+                                                                  acc[i / NI][i % NI], 0, 0, 0);
+  };
+  // one compute step: MFMAs on fragment buffer `cur`, reads of (rst, rs) into the other
+  // buffer, and the loads of window slots [w0, w0 + NMMA) of stage lkt into buffer lbuf
+  auto step = [&](int cur, const lds_char* rst, int rs, int w0, int lbuf, int lkt, bool lon) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NMMA; ++i) {
+      mma(cur, i);
+#pragma unroll
+      for (int j = 0; j < LPS; ++j)
+        if (w0 >= 0 && j * WIN / LPS == w0 + i) dma(j, lbuf, lkt, lon);
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+        if (i * RPS + r < NREAD) read_piece(cur ^ 1, rst, rs, i * RPS + r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm_wait_lgkm<0>();
+    tie(cur ^ 1);
+  };
   if (nk <= 0) return;
   prefetch(0);
 #pragma unroll
-  for (int j = 0; j < NS - 1; ++j) {
-    if (j < nk) {
+  for (int j = 0; j < LPS; ++j) dma(j, 0, 0, true);
+  prefetch(1);
 #pragma unroll
-      for (int q = 0; q < LPS; ++q) dma(q, j, j * KS);
-      if (j + 1 < nk) prefetch((j + 1) * KS);
-    }
-  }
-  wait_stages<LPS>(min(nk - 1, NS - 2));
+  for (int j = 0; j < kEarly; ++j) dma(j, 1, 1, nk > 1);
+  __builtin_amdgcn_s_waitcnt(vm_wait(kEarly));  // stage 0 landed (stage 1's early loads may not have)
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
   for (int i = 0; i < NREAD; ++i) read_piece(0, lds, 0, i);
@@ -966,53 +960,24 @@ __device__ __forceinline__ void kloop_interleaved(int nk, lds_char* lds, int wm0
   tie(0);
 
   for (int kt = 0; kt < nk; ++kt) {
-    const lds_char* st = lds + (kt % NS) * kStage;
-    const bool dma_next = kt + NS - 1 < nk;
-    lds_char* dst = lds + ((kt + NS - 1) % NS) * kStage;
-    const int dk0 = (kt + NS - 1) * KS;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < NMMA; ++i) {
-      acc[i / NI][i % NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][i % NI].value(), fa[0][i / NI].value(),
-                                                                    acc[i / NI][i % NI], 0, 0, 0);
-#pragma unroll
-      for (int d = 0; d < DPS; ++d)
-        if (i * DPS + d < LPS && dma_next) dma(i * DPS + d, (int)((dst - lds) / kStage), dk0);
-#pragma unroll
-      for (int r = 0; r < RPS; ++r)
-        if (i * RPS + r < NREAD) read_piece(1, st, 1, i * RPS + r);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    asm_wait_lgkm<0>();
-    tie(1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      wait_stages<LPS>(min(nk - 2 - kt, NS - 2));
-      asm volatile("s_barrier" ::: "memory");
-    }
-    if (kt + NS < nk) prefetch((kt + NS) * KS);
-    const lds_char* st1 = lds + ((kt + 1) % NS) * kStage;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < NMMA; ++i) {
-      acc[i / NI][i % NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[1][i % NI].value(), fa[1][i / NI].value(),
-                                                                    acc[i / NI][i % NI], 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < RPS; ++r)
-        if (i * RPS + r < NREAD && more) read_piece(0, st1, 0, i * RPS + r);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (more) {
-      asm_wait_lgkm<0>();
-      tie(0);
-    }
+    const int buf = kt & 1;
+    const lds_char* st = lds + buf * kStage;
+    const lds_char* nst = lds + (buf ^ 1) * kStage;
+    step(0, st, 1, NMMA, buf ^ 1, kt + 1, kt + 1 < nk);  // rest of stage kt + 1's loads
+    prefetch(kt + 2);
+    step(1, st, 2, -1, 0, 0, false);
+    step(0, st, 3, -1, 0, 0, false);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    asm volatile("s_barrier" ::: "memory");
+    step(1, nst, 0, 0, buf, kt + 2, kt + 2 < nk);  // first part of stage kt + 2's loads
   }
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
 }
 
 template <int BM, int BN, bool B_T, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   extern __shared__ __align__(16) char smem[];
-  constexpr int KS = 32, NS = 4;
+  constexpr int KS = 64;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MI = WM / 32, NI = WN / 32;
   constexpr int kStage = (BM + BN) * KS * 2;
@@ -1020,38 +985,34 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
 
   RowsTile tile;
   if (!decode_rows_tile<BM>(p, smem, tile)) return;  // uniform per workgroup
-  const int e = tile.e, nt = tile.nt, rows = tile.rows;
+  const int e = __builtin_amdgcn_readfirstlane(tile.e);
+  const int nt = __builtin_amdgcn_readfirstlane(tile.nt);
+  const int rows = tile.rows;
   const int64_t row0 = tile.row0;
+  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
+  const int ktail = p.K % KS;
+  const int nk = (p.K + KS - 1) / KS;
 
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
-  const __amdgpu_buffer_rsrc_t rb =
-      make_rsrc(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride, p.b_bytes);
-
-  using LA = NtLoad<BM, KS>;
-  LA la;
+  RowLoad<BM> la;
 #pragma unroll
-  for (int q = 0; q < LA::NQ; ++q) {
-    const int r = LA::row_of(q), c = LA::chunk_of(q);
-    la.kc[q] = 8 * c;
+  for (int q = 0; q < RowLoad<BM>::NQ; ++q) {
+    const int r = RowLoad<BM>::row_of(q);
+    uint32_t ro = kOOB;
     if (r < rows) {
       const int64_t i = row0 + r;
       const int64_t src = p.a_rows ? (int64_t)((int)p.a_rows[i] / p.a_div) : i;
-      la.roff[q] = (uint32_t)(src * p.lda * 2) + 16u * c;
-    } else {
-      la.roff[q] = kOOB;
+      ro = (uint32_t)(src * p.lda * 2);
     }
+    la.set(q, ro, ktail);
   }
   const int ncol0 = nt * BN;
-  using LBN = NtLoad<B_T ? 64 : BN, KS>;
-  using LBT = TLoad<B_T ? BN : 128, KS>;
-  LBN lbn;
-  LBT lbt;
+  RowLoad<B_T ? 32 : BN> lbn;
+  KLoad<B_T ? BN : 128> lbt;
   if constexpr (!B_T) {
 #pragma unroll
-    for (int q = 0; q < LBN::NQ; ++q) {
-      const int r = LBN::row_of(q), c = LBN::chunk_of(q);
-      lbn.kc[q] = 8 * c;
+    for (int q = 0; q < RowLoad<BN>::NQ; ++q) {
+      const int r = RowLoad<BN>::row_of(q);
       int n;
       bool ok;
       if constexpr (EPI == EPI_SWIGLU) {
@@ -1062,24 +1023,27 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
         n = ncol0 + r;
         ok = n < p.N;
       }
-      lbn.roff[q] = ok ? (uint32_t)((int64_t)n * p.ldb * 2) + 16u * c : kOOB;
+      lbn.set(q, ok ? (uint32_t)((int64_t)n * p.ldb * 2) : kOOB, ktail);
     }
   } else {
-    lbt.init(ncol0, p.N);
+    lbt.init(ncol0, p.N, p.ldb * 2);
   }
-  constexpr int LPS = LA::NQ + (B_T ? LBT::NQ : LBN::NQ);
-  auto dma = [&](int q, int stage, int k0) {
-    lds_char* sa = lds + stage * kStage;
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  const char* b_base = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride);
+  constexpr int NQA = RowLoad<BM>::NQ;
+  constexpr int LPS = NQA + (B_T ? KLoad<BN>::NQ : RowLoad<BN>::NQ);
+  auto dma = [&](int q, int buf, int kt, bool on) {
+    lds_char* sa = lds + buf * kStage;
     lds_char* sb = sa + BM * KS * 2;
-    if (q < LA::NQ) {
-      la.issue_one(q, ra, sa, k0, p.K);
+    const int64_t k0 = (int64_t)kt * KS;
+    const bool last = kt == nk - 1;
+    if (q < NQA) {
+      la.issue(q, stage_rsrc(a_base, p.a_bytes, 2 * k0, (int64_t)p.a_bytes, on), sa, wu, last);
     } else if constexpr (!B_T) {
-      lbn.issue_one(q - LA::NQ, rb, sb, k0, p.K);
+      lbn.issue(q - NQA, stage_rsrc(b_base, p.b_bytes, 2 * k0, (int64_t)p.b_bytes, on), sb, wu, last);
     } else {
-      lbt.issue_one(q - LA::NQ, rb, sb, [&](int, int kr) -> uint32_t {
-        const int kk = k0 + kr;
-        return kk < p.K ? (uint32_t)((int64_t)kk * p.ldb * 2) : kOOB;
-      });
+      const int64_t pitch = p.ldb * 2;
+      lbt.issue(q - NQA, stage_rsrc(b_base, p.b_bytes, k0 * pitch, ((int64_t)p.K - k0) * pitch, on), sb, wu);
     }
   };
 
@@ -1093,15 +1057,15 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
 
-  kloop_interleaved<NS, LPS, MI, NI, false, B_T, BM, BN>((p.K + KS - 1) / KS, lds, wm0, wn0, acc, dma, [](int) {});
+  kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {});
   __syncthreads();  // every wave done with the stages before LDS is reused
   rows_epilogue<uint16_t, BM, BN, EPI>(p, smem, acc, e, row0, rows, nt);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool GATHER>
 __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
-  constexpr int KS = 32, NS = 4;
+  constexpr int KS = 64;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MI = WM / 32, NI = WN / 32;
   constexpr int kStage = (BM + BN) * KS * 2;
@@ -1116,67 +1080,79 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
   const int64_t r_end = p.offsets[e];
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   const int m0 = mt * BM, n0 = nt * BN;
+  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
+  const int nk = (nrows + KS - 1) / KS;
 
-  const __amdgpu_buffer_rsrc_t rdy = make_rsrc(p.dy, p.dy_bytes);
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.x_bytes);
-  using LA = TLoad<BM, KS>;
-  using LB = TLoad<BN, KS>;
+  using LA = KLoad<BM>;
+  using LB = KLoad<BN>;
   LA la;
   LB lb;
-  la.init(m0, p.Ndy);
-  lb.init(n0, p.Kx);
+  la.init(m0, p.Ndy, p.lddy * 2);
+  lb.init(n0, p.Kx, p.ldx * 2);
   constexpr int LPS = LA::NQ + LB::NQ;
-  // Each wave owns k-rows 8 w .. 8 w + 7 of every stage (KS = 32 over 4 waves). The
-  // gather indices of those rows come through scalar loads one stage ahead: they
-  // count on lgkmcnt, so waiting for them never drains the in-flight LDS loads.
-  static_assert(KS == 32 && LB::NQ * 64 / LB::CPR == 8, "8 k-rows per wave per stage");
-  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const char* dy_base = reinterpret_cast<const char*>(p.dy);
+  const char* x_base = reinterpret_cast<const char*>(p.x);
+
+  // Gathered x rows: the wave's 16 k-rows of a stage come as byte offsets in scalar
+  // registers, loaded one stage ahead with scalar loads (they count on lgkmcnt, so
+  // waiting for them never drains in-flight LDS loads). Rows past the expert's end
+  // get kOOBRow, which stays out of range after adding any column offset.
+  constexpr uint32_t kOOBRow = 0x7ffffff0u;
   typedef const __attribute__((address_space(4))) int64_t cidx_t;
   cidx_t* xr = (cidx_t*)(p.x_rows);  // global -> constant address space (scalar loads)
-  int src_rows[8];  // gather indices (< 2^31) of the wave's 8 k-rows of the next stage
-  auto fetch_src = [&](int k0) {
+  uint32_t src_off[16];
+  const int64_t ldx2 = p.ldx * 2;
+  auto fetch_src = [&](int kt) {
+    const int base = kt * KS + 16 * wu;
+    uint32_t v[16];  // gather indices are below 2^31 (R < 2^31)
+    if (base + 16 <= nrows) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int rr = k0 + 8 * wu + j;
-      rr = rr < nrows ? rr : nrows - 1;
-      src_rows[j] = (int)xr[r_begin + rr];
-    }
-  };
-  auto a_row = [&](int k0) {
-    return [=](int, int kr) -> uint32_t {
-      const int rr = k0 + kr;
-      return rr < nrows ? (uint32_t)((r_begin + rr) * p.lddy * 2) : kOOB;
-    };
-  };
-  auto dma = [&](int q, int stage, int k0) {
-    lds_char* sa = lds + stage * kStage;
-    lds_char* sb = sa + BM * KS * 2;
-    if (q < LA::NQ) {
-      la.issue_one(q, rdy, sa, a_row(k0));
-    } else if (p.x_rows != nullptr) {
-      lb.issue_one(q - LA::NQ, rx, sb, [&](int qq, int kr) -> uint32_t {
-        const int rr = k0 + kr;
-        if (rr >= nrows) return kOOB;
-        // this lane's row is qq * RPI + sub of the wave's 8; qq is a compile-time constant
-        // here (unrolled), so the pick below uses constant indices (no scratch array)
-        constexpr int RPI = 64 / LB::CPR;
-        static_assert(RPI == 2 || RPI == 4, "2 or 4 k-rows per load instruction");
-        const int sub = (int)(threadIdx.x & 63) / LB::CPR;
-        // branch-free pick (a select chain gets turned back into a scratch-array index)
-        const int m1 = -(sub & 1);
-        int v = src_rows[qq * RPI] ^ ((src_rows[qq * RPI] ^ src_rows[qq * RPI + 1]) & m1);
-        if constexpr (RPI == 4) {
-          const int hi = src_rows[qq * RPI + 2] ^ ((src_rows[qq * RPI + 2] ^ src_rows[qq * RPI + 3]) & m1);
-          v = v ^ ((v ^ hi) & -((sub >> 1) & 1));
-        }
-        return (uint32_t)((int64_t)(v / p.x_div) * p.ldx * 2);
-      });
+      for (int j = 0; j < 16; ++j) v[j] = (uint32_t)xr[r_begin + base + j];
     } else {
-      lb.issue_one(q - LA::NQ, rx, sb, [&](int, int kr) -> uint32_t {
-        const int rr = k0 + kr;
-        return rr < nrows ? (uint32_t)((r_begin + rr) * p.ldx * 2) : kOOB;
-      });
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = (uint32_t)xr[r_begin + min(base + j, nrows - 1)];
+    }
+    if (p.x_div_shift >= 0) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] >>= p.x_div_shift;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] /= (uint32_t)p.x_div;
+    }
+    // row byte offsets fit in 32 bits: x spans less than 2 GiB
+#pragma unroll
+    for (int j = 0; j < 16; ++j) src_off[j] = base + j < nrows ? v[j] * (uint32_t)ldx2 : kOOBRow;
+  };
+  auto dma = [&](int q, int buf, int kt, bool on) {
+    lds_char* sa = lds + buf * kStage;
+    lds_char* sb = sa + BM * KS * 2;
+    const int64_t k0 = (int64_t)kt * KS;
+    if (q < LA::NQ) {
+      const int64_t pitch = p.lddy * 2;
+      la.issue(q, stage_rsrc(dy_base, p.dy_bytes, (r_begin + k0) * pitch, ((int64_t)nrows - k0) * pitch, on), sa,
+               wu);
+    } else if constexpr (GATHER) {
+      const int qq = q - LA::NQ;
+      // this lane's k-row is qq * RPI + sub of the wave's 16; qq is a compile-time
+      // constant here (unrolled), so the pick indexes the array with constants only
+      // (a select between array elements is turned back into a dynamically indexed
+      // array, i.e. scratch memory; the masked XOR keeps every index constant)
+      const int sub = LB::sub();
+      const uint32_t m1 = 0u - (uint32_t)(sub & 1);
+      const uint32_t s0 = src_off[qq * LB::RPI], s1 = src_off[qq * LB::RPI + 1];
+      uint32_t v = s0 ^ ((s0 ^ s1) & m1);
+      if constexpr (LB::RPI == 4) {
+        const uint32_t s2 = src_off[qq * LB::RPI + 2], s3 = src_off[qq * LB::RPI + 3];
+        const uint32_t hi = s2 ^ ((s2 ^ s3) & m1);
+        v = v ^ ((v ^ hi) & (0u - (uint32_t)((sub >> 1) & 1)));
+      }
+      // kOOBRow + coff and v + kOOB both stay below 2^32 and at or above 2^31 - 16
+      lb.issue_at(qq, make_rsrc(x_base, on ? p.x_bytes : 0u), sb, wu, v + lb.coff[qq]);
+    } else {
+      const int64_t pitch = ldx2;
+      lb.issue(q - LA::NQ, stage_rsrc(x_base, p.x_bytes, (r_begin + k0) * pitch, ((int64_t)nrows - k0) * pitch, on),
+               sb, wu);
     }
   };
 
@@ -1190,8 +1166,8 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
 
-  kloop_interleaved<NS, LPS, MI, NI, true, true, BM, BN>((nrows + KS - 1) / KS, lds, wm0, wn0, acc, dma, [&](int k0) {
-    if (p.x_rows != nullptr) fetch_src(k0);
+  kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, [&](int kt) {
+    if (GATHER && kt < nk) fetch_src(kt);
   });
   __syncthreads();  // every wave done with the stages before LDS is reused
   wgrad_epilogue<uint16_t, BM, BN>(p, smem, acc, e, m0, n0);
@@ -1294,7 +1270,9 @@ int vec_elems(int dtype) { return dtype == ZMOE_DTYPE_BF16 ? 8 : 4; }
 int64_t span_bytes(int64_t rows, int64_t ld, int64_t cols, int dtype) {
   return rows <= 0 ? 0 : ((rows - 1) * ld + cols) * dtype_size(dtype);
 }
-constexpr int64_t kMaxSpan = 0x7fffffffLL;  // buffer-resource ranges (offsets stay below 2^31)
+// Buffer-resource ranges: every valid offset stays below this, and the out-of-range
+// markers (kOOB = 2^31, gathered-row marker 2^31 - 16, plus column offsets) stay above it.
+constexpr int64_t kMaxSpan = 0x7fff0000LL;
 bool ok_rows(int dtype, const void* ptr, int64_t ld) {
   return aligned16(ptr) && (ld % vec_elems(dtype)) == 0;
 }
@@ -1460,6 +1438,7 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   p.ldx = x_stride_m;
   p.x_rows = x_gather_idxs;
   p.x_div = x_gather_div;
+  p.x_div_shift = (x_gather_div > 0 && (x_gather_div & (x_gather_div - 1)) == 0) ? __builtin_ctz(x_gather_div) : -1;
   p.dw = DWt;
   p.offsets = expert_offsets;
   p.Ndy = (int)N;
@@ -1473,10 +1452,17 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   hipStream_t s = as_stream(stream);
   int rc;
   if (dtype == ZMOE_DTYPE_BF16) {
-    if (use_big_tiles(M, E, N) && K >= 256)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256>, rows_lds_bytes<uint16_t, 256, 256>(), 256, 256, p, s);
+    const bool big = use_big_tiles(M, E, N) && K >= 256;
+    if (big && p.x_rows)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, true>, rows_lds_bytes<uint16_t, 256, 256>(), 256, 256, p, s);
+    else if (big)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, false>, rows_lds_bytes<uint16_t, 256, 256>(), 256, 256, p,
+                               s);
+    else if (p.x_rows)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, true>, rows_lds_bytes<uint16_t, 128, 128>(), 128, 128, p, s);
     else
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128>, rows_lds_bytes<uint16_t, 128, 128>(), 128, 128, p, s);
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, false>, rows_lds_bytes<uint16_t, 128, 128>(), 128, 128, p,
+                               s);
   } else {
     rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
                              s);
