@@ -39,7 +39,9 @@ constexpr int kRowBytes = 128;
 constexpr int kGemmMaxE = 1024;
 constexpr int kXcds = 8;
 
-enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2 };
+// EPI_STORE_BIAS: EPI_STORE plus a per-expert bias row (a separate instantiation keeps
+// the bias loads out of the common kernel's register budget).
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2, EPI_STORE_BIAS = 3 };
 
 __device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
   return (uint32_t)(row * kRowBytes + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 7)) << 4));
@@ -388,13 +390,14 @@ __device__ __forceinline__ void rows_epilogue(const RowsParams& p, char* smem, c
   const int ncol0 = nt * BN;
   using S = Stage<T, WM, WN>;
   char* st = smem + wave * S::BYTES;
-  const T* bias_row = (EPI == EPI_STORE && p.bias) ? reinterpret_cast<const T*>(p.bias) + e * p.bias_estride : nullptr;
+  const T* bias_row =
+      (EPI == EPI_STORE_BIAS && p.bias) ? reinterpret_cast<const T*>(p.bias) + e * p.bias_estride : nullptr;
   stage_acc<T, MI, NI>(st, S::PITCH, acc, bias_row, ncol0 + wn0, p.N);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
   T* C = reinterpret_cast<T*>(p.c);
-  if constexpr (EPI == EPI_STORE) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_BIAS) {
     constexpr int CPR = WN / VEC;  // chunks per staged row
     for (int idx = lane; idx < WM * CPR; idx += 64) {
       const int rr = idx / CPR, cc = idx % CPR;
@@ -893,10 +896,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const char* base, u
 // pinned with sched_barrier(0); one wave per SIMD keeps the matrix unit fed while
 // loads, LDS reads and the barrier are in flight.
 // dma(q, buf, kt, on) issues load instruction q (0..LPS-1) of stage kt into buffer
-// buf (reading zeros when !on); prefetch(kt) readies the gather indices of stage kt.
-template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch>
+// buf (reading zeros when !on); prefetch(kt) readies the gather indices of stage kt;
+// after_prologue_loads() runs once the first loads are in flight.
+template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch,
+          typename Hook>
 __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI], Dma dma,
-                                        Prefetch prefetch) {
+                                        Prefetch prefetch, Hook after_prologue_loads) {
   constexpr int KS = 64;
   constexpr int kStage = (BM + BN) * KS * 2;
   constexpr int AR = Frag<A_T>::kReads, BR = Frag<B_T>::kReads;
@@ -945,13 +950,17 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
     asm_wait_lgkm<0>();
     tie(cur ^ 1);
   };
-  if (nk <= 0) return;
+  if (nk <= 0) {
+    after_prologue_loads();
+    return;
+  }
   prefetch(0);
 #pragma unroll
   for (int j = 0; j < LPS; ++j) dma(j, 0, 0, true);
   prefetch(1);
 #pragma unroll
   for (int j = 0; j < kEarly; ++j) dma(j, 1, 1, nk > 1);
+  after_prologue_loads();
   __builtin_amdgcn_s_waitcnt(vm_wait(kEarly));  // stage 0 landed (stage 1's early loads may not have)
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
@@ -974,6 +983,160 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
   __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
 }
 
+// Epilogues: each wave stages its own WM x WN accumulator block in its own LDS area
+// (bf16, rows of WN * 2 + 16 bytes) and writes it out row-contiguously, 16 bytes
+// per lane, so every store instruction covers whole 128-byte lines. The MFMA layout
+// itself would give 8-byte pieces of 32 different rows per store instruction; such
+// partial-line writes cost more than the staging. Staging is wave-local: once every
+// wave is past the K loop (one barrier) no further workgroup sync is needed.
+// In the MFMA layout lane (r = lane % 32, g = lane / 32) holds, for row 32 mi + r,
+// the columns 32 ni + 8 q + 4 g + 0..3 in acc[mi][ni][4 q .. 4 q + 3].
+template <int WN>
+struct WaveStage {
+  static constexpr int PITCH = WN * 2 + 16;  // bytes per staged row
+  static constexpr int CPR = WN / 8;          // 16-byte chunks per row
+};
+
+__device__ __forceinline__ uint2 pack4_bf16(const float (&v)[4]) {
+  return make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+__device__ __forceinline__ void unpack4_bf16(uint2 w, float (&v)[4]) {
+  v[0] = __uint_as_float(w.x << 16);
+  v[1] = __uint_as_float(w.x & 0xffff0000u);
+  v[2] = __uint_as_float(w.y << 16);
+  v[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+
+// rows 32 mi0 .. 32 mi1 - 1 of the wave's block -> staged rows 0 .. 32 (mi1 - mi0) - 1,
+// rounded to bf16 (plus the bias row first, if any: one rounding, as an unfused add would not do)
+template <int MI, int NI>
+__device__ __forceinline__ void wave_stage_bf16(char* st, const f32x16_t (&acc)[MI][NI], int mi0, int mi1,
+                                                const uint16_t* bias_cols = nullptr, int bias_ncols = 0) {
+  constexpr int PITCH = WaveStage<NI * 32>::PITCH;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    if (mi < mi0 || mi >= mi1) continue;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = 32 * ni + 8 * q + 4 * g;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = acc[mi][ni][4 * q + u];
+        if (bias_cols != nullptr && col < bias_ncols) {  // (columns past N are never stored)
+          float bv[4];
+          unpack4_bf16(*reinterpret_cast<const uint2*>(bias_cols + col), bv);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] += bv[u];
+        }
+        *reinterpret_cast<uint2*>(st + (32 * (mi - mi0) + r) * PITCH + col * 2) = pack4_bf16(v);
+      }
+  }
+}
+
+template <int BM, int BN, int EPI, int MI, int NI>
+__device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st, const int* row_table,
+                                                   const f32x16_t (&acc)[MI][NI], int e, int64_t row0, int rows,
+                                                   int nt, int wm0, int wn0) {
+  using S = WaveStage<NI * 32>;
+  constexpr int VEC = 8;
+  const int lane = threadIdx.x & 63;
+  uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+  const int ncol0 = nt * BN + wn0;
+  if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_BIAS) {
+    const uint16_t* bias = nullptr;
+    if constexpr (EPI == EPI_STORE_BIAS)
+      bias = reinterpret_cast<const uint16_t*>(p.bias) + (int64_t)e * p.bias_estride + ncol0;
+    wave_stage_bf16(st, acc, 0, MI, bias, p.N - ncol0);
+    for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
+      const int rr = idx / S::CPR, cc = idx % S::CPR;
+      const int rl = wm0 + rr, col = ncol0 + cc * VEC;
+      if (rl < rows && col < p.N)
+        *reinterpret_cast<uint4*>(C + (int64_t)row_table[rl] * p.ldc + col) =
+            *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    // staged columns per 64: [h 32 | gate 32] for pair columns jj0 + 32 pb + 0..31;
+    // A = silu(gate) * h from the bf16-rounded h and gate, as stored in H
+    constexpr int PB = NI / 2, CPP = 32 / VEC;  // pair blocks, chunks per 32 columns
+    uint16_t* A2 = reinterpret_cast<uint16_t*>(p.c2);
+    const int jj0 = nt * (BN / 2) + (wn0 / 64) * 32;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {  // two halves of the rows: 3 outputs per pair need room
+      wave_stage_bf16(st, acc, half * MI / 2, (half + 1) * MI / 2, nullptr);
+      for (int idx = lane; idx < 16 * MI * PB * CPP; idx += 64) {
+        const int rr = idx / (PB * CPP), rem = idx % (PB * CPP);
+        const int pb = rem / CPP, cc = rem % CPP;
+        const int rl = wm0 + half * 16 * MI + rr;
+        const int jj = jj0 + pb * 32 + cc * VEC;
+        if (rl < rows && jj < p.half) {
+          const int64_t orow = row_table[rl];
+          const uint4 hv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + cc * VEC) * 2);
+          const uint4 gv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + 32 + cc * VEC) * 2);
+          float h[VEC], gt[VEC], a[VEC];
+          unpack_chunk(hv, h, uint16_t{});
+          unpack_chunk(gv, gt, uint16_t{});
+#pragma unroll
+          for (int u = 0; u < VEC; ++u) a[u] = silu_f(gt[u]) * h[u];
+          *reinterpret_cast<uint4*>(C + orow * p.ldc + jj) = hv;
+          *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + jj) = gv;
+          *reinterpret_cast<uint4*>(A2 + orow * p.ldc2 + jj) = pack_chunk(a, uint16_t{});
+        }
+      }
+    }
+  } else {  // EPI_SWIGLU_BWD: staged dA (bf16, as the unfused path stores it); H rows in sorted order
+    const uint16_t* Hs = reinterpret_cast<const uint16_t*>(p.aux);
+    wave_stage_bf16(st, acc, 0, MI, nullptr);
+    for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
+      const int rr = idx / S::CPR, cc = idx % S::CPR;
+      const int rl = wm0 + rr, col = ncol0 + cc * VEC;
+      if (rl < rows && col < p.N) {
+        const int64_t i = row0 + rl;
+        const int64_t orow = row_table[rl];
+        float da[VEC], h[VEC], gt[VEC], dh[VEC], dg[VEC];
+        unpack_chunk(*reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16), da, uint16_t{});
+        unpack_chunk(ldg16(Hs + i * p.ld_aux + col), h, uint16_t{});
+        unpack_chunk(ldg16(Hs + i * p.ld_aux + p.half + col), gt, uint16_t{});
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+          const float sg = sigmoid_fast(gt[u]);
+          dh[u] = da[u] * gt[u] * sg;
+          dg[u] = da[u] * h[u] * sg * (1.f + gt[u] * (1.f - sg));
+        }
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = pack_chunk(dh, uint16_t{});
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + col) = pack_chunk(dg, uint16_t{});
+      }
+    }
+  }
+}
+
+template <int MI, int NI>
+__device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* st, const f32x16_t (&acc)[MI][NI],
+                                                    int e, int m0, int n0, int wm0, int wn0) {
+  using S = WaveStage<NI * 32>;
+  const int lane = threadIdx.x & 63;
+  uint16_t* DW = reinterpret_cast<uint16_t*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
+  wave_stage_bf16(st, acc, 0, MI, nullptr);
+  for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
+    const int rr = idx / S::CPR, cc = idx % S::CPR;
+    const int m = m0 + wm0 + rr, n = n0 + wn0 + cc * 8;
+    if (m < p.Ndy && n < p.Kx)
+      *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+  }
+}
+
+// LDS of the bf16 kernels: two operand stages, reused by the wave staging areas
+// after the K loop, then the rows kernel's output-row table.
+template <int BM, int BN>
+constexpr int bf16_stage_bytes() {
+  constexpr int loop = 2 * (BM + BN) * 64 * 2;
+  constexpr int epi = 4 * (BM / 2) * WaveStage<BN / 2>::PITCH;
+  return loop > epi ? loop : epi;
+}
+
 template <int BM, int BN, bool B_T, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   extern __shared__ __align__(16) char smem[];
@@ -994,18 +1157,25 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   const int ktail = p.K % KS;
   const int nk = (p.K + KS - 1) / KS;
 
+  // Row indices (< 2^31) are read as the low 32-bit words of the int64 entries, all
+  // issued before any is used so their latencies overlap.
   RowLoad<BM> la;
+  int a_src[RowLoad<BM>::NQ];
 #pragma unroll
   for (int q = 0; q < RowLoad<BM>::NQ; ++q) {
     const int r = RowLoad<BM>::row_of(q);
-    uint32_t ro = kOOB;
-    if (r < rows) {
-      const int64_t i = row0 + r;
-      const int64_t src = p.a_rows ? (int64_t)((int)p.a_rows[i] / p.a_div) : i;
-      ro = (uint32_t)(src * p.lda * 2);
-    }
-    la.set(q, ro, ktail);
+    a_src[q] = (int)(row0 + (r < rows ? r : 0));
   }
+  if (p.a_rows != nullptr) {
+    const int* idx32 = reinterpret_cast<const int*>(p.a_rows);
+#pragma unroll
+    for (int q = 0; q < RowLoad<BM>::NQ; ++q) a_src[q] = idx32[2 * (int64_t)a_src[q]];
+#pragma unroll
+    for (int q = 0; q < RowLoad<BM>::NQ; ++q) a_src[q] /= p.a_div;
+  }
+#pragma unroll
+  for (int q = 0; q < RowLoad<BM>::NQ; ++q)
+    la.set(q, RowLoad<BM>::row_of(q) < rows ? (uint32_t)((int64_t)a_src[q] * p.lda * 2) : kOOB, ktail);
   const int ncol0 = nt * BN;
   RowLoad<B_T ? 32 : BN> lbn;
   KLoad<B_T ? BN : 128> lbt;
@@ -1057,9 +1227,23 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
 
-  kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {});
-  __syncthreads();  // every wave done with the stages before LDS is reused
-  rows_epilogue<uint16_t, BM, BN, EPI>(p, smem, acc, e, row0, rows, nt);
+  // The tile's output rows go to an LDS table above the operand stages: the index
+  // loads are issued before the first operand loads and stored once those are in
+  // flight, so their latency hides behind the first stage (row numbers < 2^31).
+  int* row_table = reinterpret_cast<int*>(smem + bf16_stage_bytes<BM, BN>());
+  int orow_v = 0;
+  if (threadIdx.x < BM) {
+    const int rl = (int)threadIdx.x;
+    const int64_t i = row0 + (rl < rows ? rl : 0);
+    orow_v = p.c_rows ? reinterpret_cast<const int*>(p.c_rows)[2 * i] : (int)i;
+  }
+  kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, [&] {
+    if (threadIdx.x < BM) row_table[threadIdx.x] = orow_v;
+  });
+  // every wave is done with the operand stages (and has written its row-table entries)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,
+                                  nt, wm0, wn0);
 }
 
 template <int BM, int BN, bool GATHER>
@@ -1168,9 +1352,9 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
 
   kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, [&](int kt) {
     if (GATHER && kt < nk) fetch_src(kt);
-  });
-  __syncthreads();  // every wave done with the stages before LDS is reused
-  wgrad_epilogue<uint16_t, BM, BN>(p, smem, acc, e, m0, n0);
+  }, [] {});
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
+  wgrad_epilogue_bf16(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, acc, e, m0, n0, wm0, wn0);
 }
 
 // ------------------------------------------------------------------ host side
@@ -1181,6 +1365,15 @@ constexpr int rows_lds_bytes() {
   constexpr int decode = (kGemmMaxE + 4 + 8) * 4;
   constexpr int m = main_loop > staging ? main_loop : staging;
   return m > decode ? m : decode;
+}
+
+// bf16 kernels: two 64-deep operand stages (+ the rows kernel's output-row table);
+// the epilogue works from registers.
+template <int BM, int BN>
+constexpr int bf16_lds_bytes() {
+  constexpr int main_loop = bf16_stage_bytes<BM, BN>() + BM * 4;  // stages / staging + output-row table
+  constexpr int decode = (kGemmMaxE + 4 + 8) * 4;
+  return main_loop > decode ? main_loop : decode;
 }
 
 template <typename K>
@@ -1215,7 +1408,7 @@ int launch_rows_f32(const RowsParams& p, int64_t R, hipStream_t s) {
 
 template <int BM, int BN, bool B_KN, int EPI>
 int launch_rows_bf16(const RowsParams& p, int64_t R, hipStream_t s) {
-  return launch_rows_kernel(rows_bf16_kernel<BM, BN, B_KN, EPI>, rows_lds_bytes<uint16_t, BM, BN>(), BM, p, R, s);
+  return launch_rows_kernel(rows_bf16_kernel<BM, BN, B_KN, EPI>, bf16_lds_bytes<BM, BN>(), BM, p, R, s);
 }
 
 template <typename K>
@@ -1326,7 +1519,8 @@ extern "C" int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const voi
     const int64_t b_span = span_bytes(N, w_stride_n, K, dtype);
     ZMOE_REQUIRE(b_span <= kMaxSpan, ZMOE_ERR_SHAPE, "scatter2scatter: one expert's W spans more than 2 GiB");
     p.b_bytes = (uint32_t)b_span;
-    return dispatch_rows<false, EPI_STORE>(dtype, p, R, (int)N, s);
+    return b ? dispatch_rows<false, EPI_STORE_BIAS>(dtype, p, R, (int)N, s)
+             : dispatch_rows<false, EPI_STORE>(dtype, p, R, (int)N, s);
   }
   ZMOE_REQUIRE(w_stride_n == 1, ZMOE_ERR_SHAPE, "scatter2scatter: W needs unit stride along K or N");
   ZMOE_REQUIRE(w_stride_k % v == 0, ZMOE_ERR_ALIGN, "scatter2scatter: weight row stride");
@@ -1334,7 +1528,8 @@ extern "C" int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const voi
   const int64_t b_span = span_bytes(K, w_stride_k, N, dtype);
   ZMOE_REQUIRE(b_span <= kMaxSpan, ZMOE_ERR_SHAPE, "scatter2scatter: one expert's W spans more than 2 GiB");
   p.b_bytes = (uint32_t)b_span;
-  return dispatch_rows<true, EPI_STORE>(dtype, p, R, (int)N, s);
+  return b ? dispatch_rows<true, EPI_STORE_BIAS>(dtype, p, R, (int)N, s)
+           : dispatch_rows<true, EPI_STORE>(dtype, p, R, (int)N, s);
 }
 
 extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
@@ -1454,14 +1649,14 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   if (dtype == ZMOE_DTYPE_BF16) {
     const bool big = use_big_tiles(M, E, N) && K >= 256;
     if (big && p.x_rows)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, true>, rows_lds_bytes<uint16_t, 256, 256>(), 256, 256, p, s);
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, true>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
     else if (big)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, false>, rows_lds_bytes<uint16_t, 256, 256>(), 256, 256, p,
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, false>, bf16_lds_bytes<256, 256>(), 256, 256, p,
                                s);
     else if (p.x_rows)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, true>, rows_lds_bytes<uint16_t, 128, 128>(), 128, 128, p, s);
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
     else
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, false>, rows_lds_bytes<uint16_t, 128, 128>(), 128, 128, p,
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, false>, bf16_lds_bytes<128, 128>(), 128, 128, p,
                                s);
   } else {
     rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
