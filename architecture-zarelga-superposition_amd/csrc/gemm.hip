@@ -1466,6 +1466,8 @@ int64_t span_bytes(int64_t rows, int64_t ld, int64_t cols, int dtype) {
 // Buffer-resource ranges: every valid offset stays below this, and the out-of-range
 // markers (kOOB = 2^31, gathered-row marker 2^31 - 16, plus column offsets) stay above it.
 constexpr int64_t kMaxSpan = 0x7fff0000LL;
+// Row counts and row indices travel as 32-bit values inside the kernels.
+constexpr int64_t kMaxRows = 0x7fffffffLL;
 bool ok_rows(int dtype, const void* ptr, int64_t ld) {
   return aligned16(ptr) && (ld % vec_elems(dtype)) == 0;
 }
@@ -1484,6 +1486,7 @@ extern "C" int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const voi
                "scatter2scatter: bad sizes (M=%lld K=%lld N=%lld E=%d k=%d)", (long long)M, (long long)K,
                (long long)N, E, k);
   ZMOE_REQUIRE(K < (1 << 30) && N < (1 << 30), ZMOE_ERR_SHAPE, "scatter2scatter: K/N too large");
+  ZMOE_REQUIRE(M < kMaxRows && M * k < kMaxRows, ZMOE_ERR_SHAPE, "scatter2scatter: M*k must be below 2^31");
   const int64_t R = x_grouped ? M : M * k;
   if (R == 0) return ZMOE_OK;
   ZMOE_REQUIRE(X && W && Y && expert_offsets, ZMOE_ERR_NULL, "scatter2scatter: null pointer");
@@ -1541,6 +1544,7 @@ extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void
   ZMOE_REQUIRE(T >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE && k >= 1, ZMOE_ERR_SHAPE,
                "glu_w1_forward: bad sizes");
   ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w1_forward: d/f too large");
+  ZMOE_REQUIRE(T * k < kMaxRows, ZMOE_ERR_SHAPE, "glu_w1_forward: T*k must be below 2^31");
   const int64_t R = T * k;
   if (R == 0) return ZMOE_OK;
   ZMOE_REQUIRE(X && W1 && H && A && sorted_scattered_idxs && expert_offsets, ZMOE_ERR_NULL,
@@ -1582,6 +1586,7 @@ extern "C" int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const vo
   ZMOE_REQUIRE(R >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE, ZMOE_ERR_SHAPE,
                "glu_w2_backward_dh: bad sizes");
   ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w2_backward_dh: d/f too large");
+  ZMOE_REQUIRE(R < kMaxRows, ZMOE_ERR_SHAPE, "glu_w2_backward_dh: R must be below 2^31");
   if (R == 0) return ZMOE_OK;
   ZMOE_REQUIRE(dYg && W2 && H && dH && expert_offsets, ZMOE_ERR_NULL, "glu_w2_backward_dh: null pointer");
   const int v = vec_elems(dtype);
@@ -1620,6 +1625,7 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && E >= 1 && E <= kGemmMaxE && x_gather_div >= 1, ZMOE_ERR_SHAPE,
                "group_bwd_w: bad sizes");
   ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30), ZMOE_ERR_SHAPE, "group_bwd_w: N/K too large");
+  ZMOE_REQUIRE(M < kMaxRows, ZMOE_ERR_SHAPE, "group_bwd_w: M must be below 2^31");
   ZMOE_REQUIRE(DWt && expert_offsets, ZMOE_ERR_NULL, "group_bwd_w: null pointer");
   ZMOE_REQUIRE(M == 0 || (DY && X), ZMOE_ERR_NULL, "group_bwd_w: null operand");
   const int v = vec_elems(dtype);

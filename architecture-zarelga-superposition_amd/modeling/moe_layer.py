@@ -35,7 +35,10 @@ class MoELayer(nn.Module):
         self.gate = MoEGate(config)
 
         shared_intermediate = config.intermediate_size * config.n_shared_experts
-        self.shared_experts = ExpertMLP(config, intermediate_size=shared_intermediate) if shared_intermediate else None
+        # As in the reference, n_shared_experts = 0 still yields a shared expert:
+        # ExpertMLP treats intermediate_size=0 as "use config.intermediate_size"
+        # (expert_layer.py:10), and forward always adds its output (moe_layer.py:47-53).
+        self.shared_experts = ExpertMLP(config, intermediate_size=shared_intermediate)
 
         self.routed_experts = GLUMLP(
             input_size=config.hidden_size,
@@ -62,13 +65,13 @@ class MoELayer(nn.Module):
             x = hidden_states
 
         topk_idx, topk_weight = self.gate(x)
-        shared_output = self.shared_experts(x) if self.shared_experts is not None else None
+        shared_output = self.shared_experts(x)
 
         flat_topk_idx = topk_idx.reshape(-1, self.n_experts_per_token)
         flat_topk_weight = topk_weight.reshape(-1, self.n_experts_per_token)
         routed_output = self.routed_experts(x, flat_topk_weight, flat_topk_idx)
 
-        out = routed_output if shared_output is None else shared_output + routed_output
+        out = shared_output + routed_output
 
         if unpad_indices is not None:
             out = pad_input(out.squeeze(0), unpad_indices, bsz, seq_len)

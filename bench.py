@@ -35,7 +35,7 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 WORKLOADS = {
-    # name: (T, d, E, k, f, shared_width, backward)
+    # name: (T, d, E, k, f, shared_width (0: n_shared_experts = 0), backward)
     "c2": (16384, 1024, 64, 8, 512, 0, False),
     "c3": (32768, 2048, 128, 8, 768, 1536, True),
     "c4": (8192, 7168, 256, 8, 2048, 2048, True),
@@ -43,6 +43,19 @@ WORKLOADS = {
 }
 
 GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bwd_w")
+
+# HBM-side bytes per launch at C3 (L2 -> memory fabric reads and writes), from two
+# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over this script, each scaled by what
+# the same counter reads for a plain 1 GiB copy (reads x 2.000, writes x 1.000); the
+# commands and raw counts are in profiles/grouped_gemm_c3_hbm_bytes.md.
+TRAFFIC_C3 = {
+    "glu_w1_forward#0": 5743576100,
+    "scatter2scatter#0": 2718421103,
+    "glu_w2_backward_dh#0": 3755448866,
+    "scatter2scatter#1": 4931326617,
+    "group_bwd_w#0": 2214023556,
+    "group_bwd_w#1": 3921409541,
+}
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "sum_k")
 
 
@@ -134,6 +147,48 @@ def cpu_baseline(T, d, E, k, f, fs, budget_s=20.0, sample_T=1024):
     }
 
 
+COPY_PROBE_BYTES = 1 << 30  # device-to-device copy used to calibrate FETCH_SIZE / WRITE_SIZE
+
+
+def copy_probe() -> int:
+    """Three 1 GiB device copies (run under rocprofv3 --pmc to calibrate the byte counters)."""
+    import torch
+
+    src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copy probe: 3 x {COPY_PROBE_BYTES} bytes", flush=True)
+    return 0
+
+
+def pmc_summary(path: str) -> int:
+    """Mean of each counter per dispatch, by kernel, in dispatch order of first appearance,
+    from the run_counter_collection.csv files under ``path`` (rocprofv3 --pmc output)."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        print(f"no counter_collection.csv under {path}", file=sys.stderr)
+        return 1
+    rows = {}
+    for fn in files:
+        with open(fn) as fh:
+            for r in csv.DictReader(fh):
+                key = (r["Kernel_Name"], r["Counter_Name"])
+                d = rows.setdefault(key, {"first": int(r.get("Dispatch_Id", 0) or 0), "v": {}})
+                d["v"][r.get("Dispatch_Id", len(d["v"]))] = d["v"].get(r.get("Dispatch_Id", len(d["v"])), 0.0) + float(
+                    r["Counter_Value"])
+    print(f"{'counter':12s} {'dispatches':>10s} {'mean/dispatch':>16s}  kernel")
+    for (kern, ctr), d in sorted(rows.items(), key=lambda kv: kv[1]["first"]):
+        vals = list(d["v"].values())
+        print(f"{ctr:12s} {len(vals):10d} {sum(vals) / len(vals):16.1f}  {kern[:110]}")
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,11 +197,18 @@ def main(argv=None):
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
+    ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 --pmc CSVs under DIR and exit")
     args = ap.parse_args(argv)
+    if args.pmc_summary:
+        return pmc_summary(args.pmc_summary)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the MoE layer would shard experts across GPUs; see DESIGN.md)", file=sys.stderr)
         return 2
+
+    if args.copy_probe:
+        return copy_probe()
 
     import torch
 
@@ -155,6 +217,8 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     T, d, E, k, f, fs, backward = WORKLOADS[args.workload]
     layer = build_layer(T, d, E, k, f, fs, dev)
+    # the reference layer always runs a shared expert; n_shared_experts = 0 gives width f
+    fs = layer.shared_experts.intermediate_size
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
     x = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16).requires_grad_(backward)
@@ -232,7 +296,7 @@ def main(argv=None):
         "data": "synthetic (seeded N(0,1) inputs and upstream grads; random-init weights)",
         "config": {
             "workload": (f"{args.workload}: MoE layer {'fwd+bwd' if backward else 'fwd'} T={T} d={d} E={E} "
-                         f"k={k} SwiGLU f={f}" + (f" + shared SwiGLU {fs}" if fs else "")),
+                         f"k={k} SwiGLU f={f} + shared SwiGLU {fs}"),
             "tokens": T, "d_model": d, "experts": E, "top_k": k, "ffn": f, "shared_ffn": fs,
             "parallelism": "single GPU",
         },
@@ -245,7 +309,7 @@ def main(argv=None):
             "unit": "TFLOP/s",
             "frac": dom["tflops"] / PEAK_BF16_TFLOPS,
             "avg_ms": dom["avg_ms"],
-            "traffic": None,
+            "traffic": TRAFFIC_C3.get(dom_name) if args.workload == "c3" else None,
         },
         "cpu_baseline": cpu,
     }

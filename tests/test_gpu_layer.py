@@ -17,6 +17,12 @@ from helpers import TOL, assert_close, gen, layer_inputs, np64
 pytestmark = pytest.mark.gpu
 
 
+def shared_width(f, n_shared):
+    """Width of the layer's shared expert: the reference's ExpertMLP reads a width of
+    0 (n_shared_experts = 0) as config.intermediate_size (expert_layer.py:10)."""
+    return f * n_shared or f
+
+
 def build_layer(P, d, E, k, f, n_shared, dtype, dev, fused=True):
     from modeling.model_config import ModelConfig
     from modeling.moe_layer import MoELayer
@@ -30,10 +36,9 @@ def build_layer(P, d, E, k, f, n_shared, dtype, dev, fused=True):
         layer.gate.expert_biases.copy_(P["bias"])
         layer.routed_experts.experts.weight.copy_(P["W1"])
         layer.routed_experts.output_experts.weight.copy_(P["W2"])
-        if n_shared:
-            layer.shared_experts.gate_proj.weight.copy_(P["shared"][0])
-            layer.shared_experts.up_proj.weight.copy_(P["shared"][1])
-            layer.shared_experts.down_proj.weight.copy_(P["shared"][2])
+        layer.shared_experts.gate_proj.weight.copy_(P["shared"][0])
+        layer.shared_experts.up_proj.weight.copy_(P["shared"][1])
+        layer.shared_experts.down_proj.weight.copy_(P["shared"][2])
     layer = layer.to(dev)
     if dtype != torch.float32:
         layer = layer.to(dtype)
@@ -43,7 +48,7 @@ def build_layer(P, d, E, k, f, n_shared, dtype, dev, fused=True):
 
 
 def run_and_compare(T, d, E, k, f, n_shared, dtype, dev, fused=True, bias_std=0.1, seed=0):
-    fs = f * n_shared
+    fs = shared_width(f, n_shared)
     P = layer_inputs(T, d, E, k, f, fs, seed=seed, dtype=dtype, bias_std=bias_std)
     layer = build_layer(P, d, E, k, f, n_shared, dtype, dev, fused=fused)
     x = P["x"].to(dtype).to(dev).view(1, T, d).requires_grad_(True)
@@ -57,7 +62,7 @@ def run_and_compare(T, d, E, k, f, n_shared, dtype, dev, fused=True, bias_std=0.
     assert_close(logits, ref_logits, **TOL[dtype], what="gate logits")
 
     orc = O.MoELayerOracle(np64(P["Wg"]), P["bias"].numpy(), np64(P["W1"]), np64(P["W2"]), k,
-                           shared=None if not n_shared else tuple(np64(w) for w in P["shared"]),
+                           shared=tuple(np64(w) for w in P["shared"]),
                            round_probs_bf16=dtype == torch.bfloat16)
     rout, ridx, _ = orc.forward(np64(P["x"]), logits=logits)
     np.testing.assert_array_equal(idx.view(T, k).cpu().numpy(), ridx)
@@ -68,16 +73,16 @@ def run_and_compare(T, d, E, k, f, n_shared, dtype, dev, fused=True, bias_std=0.
     assert_close(np64(layer.gate.weight.grad), g["gate_weight"], **tol, what="d gate.weight")
     assert_close(np64(layer.routed_experts.experts.weight.grad), g["W1"], **tol, what="dW1")
     assert_close(np64(layer.routed_experts.output_experts.weight.grad), g["W2"], **tol, what="dW2")
-    if n_shared:
-        se = layer.shared_experts
-        assert_close(np64(se.gate_proj.weight.grad), g["shared_gate"], **tol, what="d shared gate")
-        assert_close(np64(se.up_proj.weight.grad), g["shared_up"], **tol, what="d shared up")
-        assert_close(np64(se.down_proj.weight.grad), g["shared_down"], **tol, what="d shared down")
+    se = layer.shared_experts
+    assert_close(np64(se.gate_proj.weight.grad), g["shared_gate"], **tol, what="d shared gate")
+    assert_close(np64(se.up_proj.weight.grad), g["shared_up"], **tol, what="d shared up")
+    assert_close(np64(se.down_proj.weight.grad), g["shared_down"], **tol, what="d shared down")
     return layer
 
 
 def test_layer_c1_fp32(hip_device):
-    """BASELINE config 1 (T=2048 d=256 E=8 k=2 f=512, no shared expert) in fp32."""
+    """BASELINE config 1 (T=2048 d=256 E=8 k=2 f=512, n_shared_experts=0) in fp32; the
+    reference layer still runs a shared expert of width f in that case."""
     run_and_compare(2048, 256, 8, 2, 512, 0, torch.float32, hip_device, bias_std=0.0)
 
 
