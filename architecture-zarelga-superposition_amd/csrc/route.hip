@@ -2,27 +2,42 @@
 // the aux-loss-free bias update (main.py:161-175).
 //
 // One 64-lane wave owns one token row. Lane l holds experts l, l+64, ... so a
-// row of E <= 1024 scores sits in registers; k rounds of a wave-wide argmax
-// (xor-shuffle butterfly over (score, expert) pairs) pick the slots in the
+// row of E <= 1024 scores sits in registers; k rounds of a wave-wide max
+// (xor-shuffle butterfly over packed (score, expert) keys) pick the slots in the
 // contract order (score desc, expert asc, NaN first).
+#include <type_traits>
+
 #include "zmoe_internal.h"
 
 namespace zmoe {
 
 constexpr int kRouteMaxPerLane = 16;  // E <= 1024
-constexpr int kNoExpert = 0x7fffffff;
 
-// true when candidate (as, ae) ranks before (bs, be)
-__device__ __forceinline__ bool ranks_before(float as, int ae, float bs, int be) {
-  if (ae == kNoExpert) return false;
-  if (be == kNoExpert) return true;
-  const bool an = as != as, bn = bs != bs;
-  if (an != bn) return an;
-  if (!an && as != bs) return as > bs;
-  return ae < be;
+// Sort key of a routing candidate; a larger key takes an earlier slot. The high word is
+// a monotone image of the biased score (every NaN canonicalised above +inf, -0 folded
+// into +0), the low word the inverted expert id, so equal scores go to the lower expert.
+__device__ __forceinline__ uint64_t route_key(float s, int e) {
+  uint32_t b = __float_as_uint(s);
+  if (s != s) b = 0x7fffffffu;
+  else if (s == 0.f) b = 0u;
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)b << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+// key 0 is below every candidate's key (the high word of a real key is at least 0x007fffff)
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
 }
 
-template <typename LT>
+// sigmoid evaluated in double, rounded once to float
+__device__ __forceinline__ float sigmoid_f64(float z) { return (float)(1.0 / (1.0 + exp(-(double)z))); }
+
+// One wave per token; lane l holds experts l + 64 q (q < PL). The score is the sigmoid
+// evaluated in double and rounded once to float (then to bf16 when the gate ran in
+// bf16, as autocast stores it); k rounds of a wave-wide max over route_key pick the
+// slots in contract order.
+template <int PL, typename LT>
 __global__ __launch_bounds__(256) void route_topk_kernel(const LT* __restrict__ logits, int64_t T, int E,
                                                          int k, const float* __restrict__ bias,
                                                          int round_bf16, int64_t* __restrict__ out_idx,
@@ -33,61 +48,43 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const LT* __restrict__ 
   if (t >= T) return;
   const LT* row = logits + t * (int64_t)E;
 
-  float p[kRouteMaxPerLane], s[kRouteMaxPerLane];
-  uint32_t taken = 0;
-  const int per_lane = (E + 63) >> 6;
+  float p[PL];
+  uint64_t key[PL];
 #pragma unroll
-  for (int q = 0; q < kRouteMaxPerLane; ++q) {
+  for (int q = 0; q < PL; ++q) {
+    const int e = lane + 64 * q;
     p[q] = 0.f;
-    s[q] = 0.f;
-    if (q < per_lane) {
-      const int e = lane + 64 * q;
-      if (e < E) {
-        const double z = (double)to_f32(row[e]);
-        float pv = (float)(1.0 / (1.0 + exp(-z)));
-        if (round_bf16) pv = to_f32(bf16_bits(pv));
-        p[q] = pv;
-        s[q] = pv + bias[e];
-      } else {
-        taken |= 1u << q;  // padding lanes never compete
-      }
-    } else {
-      taken |= 1u << q;
+    key[q] = 0;  // padding never wins
+    if (e < E) {
+      const float z = to_f32(row[e]);
+      float pv = sigmoid_f64(z);
+      if (round_bf16) pv = to_f32(bf16_bits(pv));
+      p[q] = pv;
+      key[q] = route_key(pv + bias[e], e);
     }
   }
 
-  int my_e = kNoExpert;  // slot owned by this lane (lane j keeps slot j)
+  int my_e = 0;  // slot owned by this lane (lane j keeps slot j)
   float my_p = 0.f;
   for (int j = 0; j < k; ++j) {
-    float bs = 0.f;
-    int be = kNoExpert;
+    uint64_t best = key[0];
 #pragma unroll
-    for (int q = 0; q < kRouteMaxPerLane; ++q) {
-      if (!(taken & (1u << q))) {
-        const int e = lane + 64 * q;
-        if (ranks_before(s[q], e, bs, be)) {
-          bs = s[q];
-          be = e;
-        }
-      }
-    }
+    for (int q = 1; q < PL; ++q) best = key[q] > best ? key[q] : best;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-      const float os = __shfl_xor(bs, o, 64);
-      const int oe = __shfl_xor(be, o, 64);
-      if (ranks_before(os, oe, bs, be)) {
-        bs = os;
-        be = oe;
-      }
+      const uint64_t other = shfl_xor_u64(best, o);
+      best = other > best ? other : best;
     }
-    // be is now uniform across the wave
+    const int be = (int)(0xffffffffu - (uint32_t)best);  // uniform across the wave
     const int owner = be & 63, oq = be >> 6;
-    float pw = 0.f;
+    float pw = p[0];
 #pragma unroll
-    for (int q = 0; q < kRouteMaxPerLane; ++q)
-      if (q == oq) pw = p[q];
+    for (int q = 1; q < PL; ++q) pw = q == oq ? p[q] : pw;
     pw = __shfl(pw, owner, 64);
-    if (lane == owner) taken |= 1u << oq;
+    if (lane == owner) {
+#pragma unroll
+      for (int q = 0; q < PL; ++q) key[q] = q == oq ? 0 : key[q];
+    }
     if (lane == j) {
       my_e = be;
       my_p = pw;
@@ -165,13 +162,22 @@ extern "C" int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, 
   if (T == 0) return ZMOE_OK;
   ZMOE_REQUIRE(logits && expert_biases && topk_idx && topk_weight, ZMOE_ERR_NULL, "route_topk: null pointer");
   const dim3 grid((unsigned)cdiv(T, 4)), block(256);
-  if (logits_dtype == ZMOE_DTYPE_BF16)
-    hipLaunchKernelGGL(route_topk_kernel<uint16_t>, grid, block, 0, as_stream(stream),
-                       (const uint16_t*)logits, T, E, k, expert_biases, round_probs_bf16, topk_idx,
-                       topk_weight, topk_prob);
-  else
-    hipLaunchKernelGGL(route_topk_kernel<float>, grid, block, 0, as_stream(stream), (const float*)logits, T,
-                       E, k, expert_biases, round_probs_bf16, topk_idx, topk_weight, topk_prob);
+  const int per_lane = (E + 63) / 64;
+  auto launch = [&](auto pl, auto lt) {
+    using LT = decltype(lt);
+    hipLaunchKernelGGL((route_topk_kernel<decltype(pl)::value, LT>), grid, block, 0, as_stream(stream),
+                       (const LT*)logits, T, E, k, expert_biases, round_probs_bf16, topk_idx, topk_weight,
+                       topk_prob);
+  };
+  auto by_width = [&](auto lt) {
+    if (per_lane <= 1) launch(std::integral_constant<int, 1>{}, lt);
+    else if (per_lane <= 2) launch(std::integral_constant<int, 2>{}, lt);
+    else if (per_lane <= 4) launch(std::integral_constant<int, 4>{}, lt);
+    else if (per_lane <= 8) launch(std::integral_constant<int, 8>{}, lt);
+    else launch(std::integral_constant<int, 16>{}, lt);
+  };
+  if (logits_dtype == ZMOE_DTYPE_BF16) by_width(uint16_t{});
+  else by_width(float{});
   return check_launch("route_topk");
 }
 
