@@ -8,6 +8,8 @@
 // A group of TPR threads (64, 128 or 256; a whole number of waves) owns one row
 // and strides over its chunks, so every load and store is a coalesced 16-byte
 // access; a 256-thread block holds 256/TPR rows.
+#include <type_traits>
+
 #include "zmoe_internal.h"
 
 namespace zmoe {
@@ -58,12 +60,17 @@ __global__ __launch_bounds__(kRowThreads) void group_kernel(const T* __restrict_
   }
 }
 
+// The k-way row kernels below come in two forms: KF > 0 is compiled for exactly k = KF
+// (every slot row of a chunk is loaded before any is used, so k loads are in flight
+// per thread), KF = 0 loops over a runtime k.
+
 // ------------------------------------------------------------------ combine
-template <typename T>
+template <typename T, int KF>
 __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restrict__ Y, const float* __restrict__ g,
-                                                              const T* __restrict__ add, int64_t T_, int k,
+                                                              const T* __restrict__ add, int64_t T_, int k_rt,
                                                               int64_t d, T* __restrict__ out, int tpr) {
   constexpr int VN = V<T>::N;
+  const int k = KF > 0 ? KF : k_rt;
   const int rpb = kRowThreads / tpr;
   const int64_t t = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
   if (t >= T_) return;
@@ -80,12 +87,26 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
     float part[VN];
 #pragma unroll
     for (int q = 0; q < VN; ++q) part[q] = 0.f;
-    for (int j = 0; j < k; ++j) {
-      const float w = g[t * k + j];
-      float y[VN];
-      unpack_chunk(ld16(Y + (t * k + j) * d + ch * VN), y, T{});
+    if constexpr (KF > 0) {
+      uint4 yv[KF];
 #pragma unroll
-      for (int q = 0; q < VN; ++q) part[q] = fmaf(w, y[q], part[q]);
+      for (int j = 0; j < KF; ++j) yv[j] = ld16(Y + (t * KF + j) * d + ch * VN);
+#pragma unroll
+      for (int j = 0; j < KF; ++j) {
+        const float w = g[t * KF + j];
+        float y[VN];
+        unpack_chunk(yv[j], y, T{});
+#pragma unroll
+        for (int q = 0; q < VN; ++q) part[q] = fmaf(w, y[q], part[q]);
+      }
+    } else {
+      for (int j = 0; j < k; ++j) {
+        const float w = g[t * k + j];
+        float y[VN];
+        unpack_chunk(ld16(Y + (t * k + j) * d + ch * VN), y, T{});
+#pragma unroll
+        for (int q = 0; q < VN; ++q) part[q] = fmaf(w, y[q], part[q]);
+      }
     }
 #pragma unroll
     for (int q = 0; q < VN; ++q) acc[q] += part[q];
@@ -95,76 +116,77 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
 
 // ------------------------------------------------------------------ combine backward
 // d_gates[t,j] = <Y[t*k+j], dout[t]>; grouped[inverse[t*k+j]] = g[t,j] * dout[t].
-template <typename T>
+// KM: a compile-time bound on k (slot arrays sized KM; slots j >= k are skipped).
+template <typename T, int KM>
 __global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
     const T* __restrict__ Y, const T* __restrict__ dout, const float* __restrict__ g,
     const int32_t* __restrict__ inverse, int64_t T_, int k, int64_t d, float* __restrict__ d_gates,
     T* __restrict__ grouped, int tpr) {
   constexpr int VN = V<T>::N;
-  __shared__ float red[kRowThreads / 64][kMaxFanOut];
+  __shared__ float red[kRowThreads / 64][KM];
   const int rpb = kRowThreads / tpr;
   const int64_t t = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
   const bool live = t < T_;
   const int lt = threadIdx.x % tpr;
   const int64_t nch = d / VN;
-  float dot[kMaxFanOut];
+  float dot[KM];
 #pragma unroll
-  for (int j = 0; j < kMaxFanOut; ++j) dot[j] = 0.f;
+  for (int j = 0; j < KM; ++j) dot[j] = 0.f;
   if (live) {
-    int64_t dst[kMaxFanOut];
-    float w[kMaxFanOut];
+    int32_t dst[KM];
+    float w[KM];
 #pragma unroll
-    for (int j = 0; j < kMaxFanOut; ++j) {
-      if (j < k) {
-        dst[j] = inverse[t * k + j];
-        w[j] = g[t * k + j];
-      }
+    for (int j = 0; j < KM; ++j) {
+      // slots past k repeat slot k - 1 (their results are dropped), so every load stays in bounds
+      const int jj = j < k ? j : k - 1;
+      dst[j] = inverse[t * k + jj];
+      w[j] = g[t * k + jj];
     }
     for (int64_t ch = lt; ch < nch; ch += tpr) {
       float go[VN];
       unpack_chunk(ld16(dout + t * d + ch * VN), go, T{});
+      uint4 yv[KM];
 #pragma unroll
-      for (int j = 0; j < kMaxFanOut; ++j) {
-        if (j < k) {
-          float y[VN], s[VN];
-          unpack_chunk(ld16(Y + (t * k + j) * d + ch * VN), y, T{});
-          float acc = 0.f;
+      for (int j = 0; j < KM; ++j) yv[j] = ld16(Y + (t * k + (j < k ? j : k - 1)) * d + ch * VN);
 #pragma unroll
-          for (int q = 0; q < VN; ++q) {
-            acc = fmaf(y[q], go[q], acc);
-            s[q] = w[j] * go[q];
-          }
-          dot[j] += acc;
-          st16(grouped + dst[j] * d + ch * VN, pack_chunk(s, T{}));
+      for (int j = 0; j < KM; ++j) {
+        float y[VN], sv[VN];
+        unpack_chunk(yv[j], y, T{});
+        float acc = 0.f;
+#pragma unroll
+        for (int q = 0; q < VN; ++q) {
+          acc = fmaf(y[q], go[q], acc);
+          sv[q] = w[j] * go[q];
         }
+        dot[j] += acc;
+        if (j < k) st16(grouped + (int64_t)dst[j] * d + ch * VN, pack_chunk(sv, T{}));
       }
     }
   }
-  // reduce the k partial dots over the row's threads (whole waves)
+  // reduce the partial dots over the row's threads (whole waves)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < kMaxFanOut; ++j) {
-    if (j < k) {
-      const float s = wave_sum(dot[j]);
-      if (lane == 0) red[wave][j] = s;
-    }
+  for (int j = 0; j < KM; ++j) {
+    const float sj = wave_sum(dot[j]);
+    if (lane == 0) red[wave][j] = sj;
   }
   __syncthreads();
   const int wpr = tpr / 64;  // waves per row
   if (live && lt < k) {
     const int w0 = (threadIdx.x / tpr) * wpr;
-    float s = 0.f;
-    for (int w = 0; w < wpr; ++w) s += red[w0 + w][lt];
-    d_gates[t * k + lt] = s;
+    float sum = 0.f;
+    for (int w2 = 0; w2 < wpr; ++w2) sum += red[w0 + w2][lt];
+    d_gates[t * k + lt] = sum;
   }
 }
 
 // ------------------------------------------------------------------ k-sum
-template <typename T>
-__global__ __launch_bounds__(kRowThreads) void sum_k_kernel(const T* __restrict__ Xe, int64_t T_, int k, int64_t d,
+template <typename T, int KF>
+__global__ __launch_bounds__(kRowThreads) void sum_k_kernel(const T* __restrict__ Xe, int64_t T_, int k_rt, int64_t d,
                                                             const T* __restrict__ a0, const T* __restrict__ a1,
                                                             T* __restrict__ out, int tpr) {
   constexpr int VN = V<T>::N;
+  const int k = KF > 0 ? KF : k_rt;
   const int rpb = kRowThreads / tpr;
   const int64_t t = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
   if (t >= T_) return;
@@ -174,10 +196,22 @@ __global__ __launch_bounds__(kRowThreads) void sum_k_kernel(const T* __restrict_
     float acc[VN], x[VN];
 #pragma unroll
     for (int q = 0; q < VN; ++q) acc[q] = 0.f;
-    for (int j = 0; j < k; ++j) {
-      unpack_chunk(ld16(Xe + (t * k + j) * d + ch * VN), x, T{});
+    if constexpr (KF > 0) {
+      uint4 xv[KF];
 #pragma unroll
-      for (int q = 0; q < VN; ++q) acc[q] += x[q];
+      for (int j = 0; j < KF; ++j) xv[j] = ld16(Xe + (t * KF + j) * d + ch * VN);
+#pragma unroll
+      for (int j = 0; j < KF; ++j) {
+        unpack_chunk(xv[j], x, T{});
+#pragma unroll
+        for (int q = 0; q < VN; ++q) acc[q] += x[q];
+      }
+    } else {
+      for (int j = 0; j < k; ++j) {
+        unpack_chunk(ld16(Xe + (t * k + j) * d + ch * VN), x, T{});
+#pragma unroll
+        for (int q = 0; q < VN; ++q) acc[q] += x[q];
+      }
     }
     if (a0) {
       unpack_chunk(ld16(a0 + t * d + ch * VN), x, T{});
@@ -303,12 +337,20 @@ extern "C" int zmoe_combine(const void* Y, const float* gates, const void* adden
                ZMOE_ERR_ALIGN, "combine: d must be a multiple of %d, pointers 16-byte aligned", vec_of(dtype));
   const RowMap m = row_map(d / vec_of(dtype));
   const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
-  if (dtype == ZMOE_DTYPE_BF16)
-    hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)Y, gates,
-                       (const uint16_t*)addend, T, k, d, (uint16_t*)out, m.tpr);
-  else
-    hipLaunchKernelGGL(combine_kernel<float>, grid, block, 0, as_stream(stream), (const float*)Y, gates,
-                       (const float*)addend, T, k, d, (float*)out, m.tpr);
+  auto launch = [&](auto kf, auto tt) {
+    using TT = decltype(tt);
+    hipLaunchKernelGGL((combine_kernel<TT, decltype(kf)::value>), grid, block, 0, as_stream(stream), (const TT*)Y,
+                       gates, (const TT*)addend, T, k, d, (TT*)out, m.tpr);
+  };
+  auto by_k = [&](auto tt) {
+    if (k == 8) launch(std::integral_constant<int, 8>{}, tt);
+    else if (k == 2) launch(std::integral_constant<int, 2>{}, tt);
+    else if (k == 4) launch(std::integral_constant<int, 4>{}, tt);
+    else if (k == 6) launch(std::integral_constant<int, 6>{}, tt);
+    else launch(std::integral_constant<int, 0>{}, tt);
+  };
+  if (dtype == ZMOE_DTYPE_BF16) by_k(uint16_t{});
+  else by_k(float{});
   return check_launch("combine");
 }
 
@@ -327,13 +369,21 @@ extern "C" int zmoe_combine_backward(const void* Y, const void* grad_out, const 
                vec_of(dtype));
   const RowMap m = row_map(d / vec_of(dtype));
   const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
-  if (dtype == ZMOE_DTYPE_BF16)
-    hipLaunchKernelGGL(combine_backward_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)Y,
-                       (const uint16_t*)grad_out, gates, inverse, T, k, d, d_gates, (uint16_t*)grouped_grad_out,
+  auto launch = [&](auto km, auto tt) {
+    using TT = decltype(tt);
+    hipLaunchKernelGGL((combine_backward_kernel<TT, decltype(km)::value>), grid, block, 0, as_stream(stream),
+                       (const TT*)Y, (const TT*)grad_out, gates, inverse, T, k, d, d_gates, (TT*)grouped_grad_out,
                        m.tpr);
-  else
-    hipLaunchKernelGGL(combine_backward_kernel<float>, grid, block, 0, as_stream(stream), (const float*)Y,
-                       (const float*)grad_out, gates, inverse, T, k, d, d_gates, (float*)grouped_grad_out, m.tpr);
+  };
+  auto by_k = [&](auto tt) {
+    if (k <= 2) launch(std::integral_constant<int, 2>{}, tt);
+    else if (k <= 4) launch(std::integral_constant<int, 4>{}, tt);
+    else if (k <= 8) launch(std::integral_constant<int, 8>{}, tt);
+    else if (k <= 16) launch(std::integral_constant<int, 16>{}, tt);
+    else launch(std::integral_constant<int, kMaxFanOut>{}, tt);
+  };
+  if (dtype == ZMOE_DTYPE_BF16) by_k(uint16_t{});
+  else by_k(float{});
   return check_launch("combine_backward");
 }
 
@@ -348,12 +398,20 @@ extern "C" int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype
                ZMOE_ERR_ALIGN, "sum_k: d must be a multiple of %d, pointers 16-byte aligned", vec_of(dtype));
   const RowMap m = row_map(d / vec_of(dtype));
   const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
-  if (dtype == ZMOE_DTYPE_BF16)
-    hipLaunchKernelGGL(sum_k_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)Xe, T, k, d,
-                       (const uint16_t*)add0, (const uint16_t*)add1, (uint16_t*)out, m.tpr);
-  else
-    hipLaunchKernelGGL(sum_k_kernel<float>, grid, block, 0, as_stream(stream), (const float*)Xe, T, k, d,
-                       (const float*)add0, (const float*)add1, (float*)out, m.tpr);
+  auto launch = [&](auto kf, auto tt) {
+    using TT = decltype(tt);
+    hipLaunchKernelGGL((sum_k_kernel<TT, decltype(kf)::value>), grid, block, 0, as_stream(stream), (const TT*)Xe, T,
+                       k, d, (const TT*)add0, (const TT*)add1, (TT*)out, m.tpr);
+  };
+  auto by_k = [&](auto tt) {
+    if (k == 8) launch(std::integral_constant<int, 8>{}, tt);
+    else if (k == 2) launch(std::integral_constant<int, 2>{}, tt);
+    else if (k == 4) launch(std::integral_constant<int, 4>{}, tt);
+    else if (k == 6) launch(std::integral_constant<int, 6>{}, tt);
+    else launch(std::integral_constant<int, 0>{}, tt);
+  };
+  if (dtype == ZMOE_DTYPE_BF16) by_k(uint16_t{});
+  else by_k(float{});
   return check_launch("sum_k");
 }
 
