@@ -83,6 +83,39 @@ def row_bytes(name: str, T, d, E, k) -> float:
     }[name]
 
 
+def zipf_bias(logits, k: int, s: float = 1.1, seed: int = 0):
+    """Selection bias that skews expert popularity towards Zipf(s) (BASELINE.json C4).
+
+    b_e = c * log(rank_e ** -s) for a seeded random ranking of the experts; c is the
+    value on a log grid (refined once) whose realised top-k counts on ``logits`` are
+    closest to Zipf(s) over the ranks in Kolmogorov-Smirnov distance. Returns
+    (bias [E] fp32 on the logits' device, c, KS distance).
+    """
+    import torch
+
+    from zmoe import ops
+
+    E = logits.shape[1]
+    g = torch.Generator()
+    g.manual_seed(seed)
+    rank = torch.randperm(E, generator=g) + 1                    # rank of expert e (1 = most popular)
+    base = (-s * torch.log(rank.double())).float()
+    pmf = rank.double().sort().values.pow(-s)
+    target = torch.cumsum(pmf / pmf.sum(), 0)
+    order = torch.argsort(rank)                                   # experts by rank
+
+    def ks(c: float) -> float:
+        idx, _, _ = ops.route_topk(logits, (c * base).to(logits.device), k)
+        counts = torch.bincount(idx.view(-1), minlength=E).double().cpu()[order]
+        return float((torch.cumsum(counts / counts.sum(), 0) - target).abs().max())
+
+    grid = [0.0] + [10 ** (x / 8.0) for x in range(-24, 9)]       # 1e-3 .. ~10
+    best = min(grid, key=ks)
+    fine = [best * (1 + x / 10.0) for x in range(-5, 6)]
+    best = min(fine, key=ks)
+    return (best * base).to(logits.device), best, ks(best)
+
+
 def build_layer(T, d, E, k, f, fs, dev, seed=0):
     import torch
 
@@ -223,6 +256,13 @@ def main(argv=None):
     g.manual_seed(1234)
     x = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16).requires_grad_(backward)
     dout = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16)
+    skew = None
+    if args.workload == "c4":  # Zipf(1.1)-skewed expert popularity through the selection bias
+        with torch.no_grad():
+            logits = torch.nn.functional.linear(x.detach().view(T, d), layer.gate.weight)
+        bias, c, ks = zipf_bias(logits, k)
+        layer.gate.expert_biases.data = bias
+        skew = {"zipf_s": 1.1, "bias_scale": c, "ks_distance": ks}
     params = list(layer.parameters())
 
     def step():
@@ -299,6 +339,7 @@ def main(argv=None):
                          f"k={k} SwiGLU f={f} + shared SwiGLU {fs}"),
             "tokens": T, "d_model": d, "experts": E, "top_k": k, "ffn": f, "shared_ffn": fs,
             "parallelism": "single GPU",
+            **({"routing_skew": skew} if skew else {}),
         },
         "grouped_gemm_mfma_util_pct": 100.0 * util,
         "roofline": {
