@@ -133,8 +133,8 @@ def build_layer(T, d, E, k, f, fs, dev, seed=0):
     return layer
 
 
-def cpu_baseline(T, d, E, k, f, fs, budget_s=20.0, sample_T=1024):
-    """Time the numpy oracle (float32) fwd+bwd on ``sample_T`` tokens of the workload."""
+def cpu_baseline(T, d, E, k, f, fs, backward=True, budget_s=20.0, sample_T=1024):
+    """Time the numpy oracle (float32) fwd (+bwd) on ``sample_T`` tokens of the workload."""
     import numpy as np
 
     import oracle as O
@@ -162,7 +162,8 @@ def cpu_baseline(T, d, E, k, f, fs, budget_s=20.0, sample_T=1024):
     for i in range(6):
         t0 = time.perf_counter()
         orc.forward(x)
-        orc.backward(dout)
+        if backward:
+            orc.backward(dout)
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > budget_s and i >= 1:
             break
@@ -174,7 +175,8 @@ def cpu_baseline(T, d, E, k, f, fs, budget_s=20.0, sample_T=1024):
         "unit": "tokens/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": (f"numpy oracle (float32) MoE layer fwd+bwd on {sample_T} tokens of the same shape "
+        "sample": (f"numpy oracle (float32) MoE layer {'fwd+bwd' if backward else 'fwd'} on {sample_T} tokens "
+                   f"of the same shape "
                    f"(d={d}, E={E}, k={k}, f={f}, shared={fs}); mean of {len(timed)} steps after 1 warmup, "
                    f"{sec:.2f} s/step"),
     }
@@ -228,6 +230,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--tokens", type=int, default=None, help="override the workload's token count T")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
@@ -249,6 +252,8 @@ def main(argv=None):
 
     dev = torch.device("cuda:0")
     T, d, E, k, f, fs, backward = WORKLOADS[args.workload]
+    if args.tokens:
+        T = args.tokens
     layer = build_layer(T, d, E, k, f, fs, dev)
     # the reference layer always runs a shared expert; n_shared_experts = 0 gives width f
     fs = layer.shared_experts.intermediate_size
@@ -317,9 +322,21 @@ def main(argv=None):
     gemm_flops_total = sum(v["flops"] for v in gemm.values())
     util = gemm_flops_total / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
 
+    weight_stream = None
+    if not backward:
+        # expert-weight streaming of the routed GEMMs (HBM-bound at small T): bytes of the
+        # W1 and W2 slabs of every expert that received a token, over the two GEMMs' time
+        with torch.no_grad():
+            idx, _ = layer.gate(x)
+        U = int(torch.unique(idx).numel())
+        wbytes = U * (2 * f * d + d * f) * 2
+        t_ms = sum(v["avg_ms"] for n, v in kernels.items() if n.startswith(("glu_w1_forward", "scatter2scatter")))
+        weight_stream = {"experts_touched": U, "bytes": wbytes, "ms": t_ms,
+                         "gbs": wbytes / (t_ms * 1e-3) / 1e9, "frac_of_hbm_peak": wbytes / (t_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(T, d, E, k, f, fs)
+        cpu = cpu_baseline(T, d, E, k, f, fs, backward=backward, sample_T=min(1024, T))
 
     line = {
         "metric": METRIC,
@@ -354,6 +371,8 @@ def main(argv=None):
         },
         "cpu_baseline": cpu,
     }
+    if weight_stream:
+        line["weight_streaming"] = weight_stream
     if args.verbose:
         line["kernels"] = kernels
     print(json.dumps(line), flush=True)
