@@ -1246,7 +1246,31 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
                                   nt, wm0, wn0);
 }
 
-template <int BM, int BN, bool GATHER>
+// fp32 output straight from the accumulators (split-K partials; no rounding): lane
+// (r, g) stores columns 32 ni + 8 q + 4 g .. + 3 of row 32 mi + r as one 16-byte write.
+template <int MI, int NI>
+__device__ __forceinline__ void wgrad_epilogue_f32(const WgradParams& p, const f32x16_t (&acc)[MI][NI], int e,
+                                                   int m0, int n0, int wm0, int wn0) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31, g = lane >> 5;
+  float* DW = reinterpret_cast<float*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    const int m = m0 + wm0 + 32 * mi + r;
+    if (m >= p.Ndy) continue;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn0 + 32 * ni + 8 * q + 4 * g;
+        if (n < p.Kx)
+          *reinterpret_cast<float4*>(DW + (int64_t)m * p.Kx + n) =
+              make_float4(acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
+      }
+  }
+}
+
+template <int BM, int BN, bool GATHER, bool OUT_F32 = false>
 __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
   constexpr int KS = 64;
@@ -1354,7 +1378,41 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
     if (GATHER && kt < nk) fetch_src(kt);
   }, [] {});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
-  wgrad_epilogue_bf16(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, acc, e, m0, n0, wm0, wn0);
+  if constexpr (OUT_F32)
+    wgrad_epilogue_f32(p, acc, e, m0, n0, wm0, wn0);
+  else
+    wgrad_epilogue_bf16(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, acc, e, m0, n0, wm0, wn0);
+}
+
+// ------------------------------------------------------------------ dense split-K weight grads
+// Row ranges of the split-K partials as inclusive ends (the wgrad kernels' expert offsets):
+// S near-equal ranges, cut at multiples of 64 rows (whole K-loop stages).
+__global__ void split_offsets_kernel(int64_t* __restrict__ off, int64_t M, int S) {
+  const int s = threadIdx.x;
+  if (s >= S) return;
+  int64_t end = (s + 1 == S) ? M : ((M * (s + 1) / S + 63) / 64) * 64;
+  off[s] = end < M ? end : M;
+}
+
+// out[i] = sum over s of part[s][i] (fp32), rounded once to the output type.
+template <typename T>
+__global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restrict__ part, int S, int64_t n,
+                                                            T* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  float4 a = *reinterpret_cast<const float4*>(part + i);
+  for (int s2 = 1; s2 < S; ++s2) {
+    const float4 b = *reinterpret_cast<const float4*>(part + (int64_t)s2 * n + i);
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  }
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w));
+  } else {
+    *reinterpret_cast<float4*>(out + i) = a;
+  }
 }
 
 // ------------------------------------------------------------------ host side
@@ -1677,4 +1735,62 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
     hipLaunchKernelGGL(bias_grad_kernel<float>, grid, block, 0, s, (const float*)DY, dy_stride_m, expert_offsets,
                        (int)N, E, (float*)Db);
   return check_launch("bias_grad_kernel");
+}
+
+// Workspace: split offsets (256 bytes) + S fp32 partials of [N, K].
+extern "C" size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int splits) {
+  if (N < 1 || K < 1 || splits < 1) return 256;
+  return 256 + (size_t)splits * (size_t)N * (size_t)K * 4u;
+}
+
+extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m, int64_t M,
+                                int64_t N, int64_t K, int dtype, int splits, void* DW, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "dense_wgrad: dtype %d", dtype);
+  ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && splits >= 1 && splits <= 64, ZMOE_ERR_SHAPE,
+               "dense_wgrad: bad sizes (M=%lld N=%lld K=%lld splits=%d)", (long long)M, (long long)N, (long long)K,
+               splits);
+  ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30) && M < kMaxRows, ZMOE_ERR_SHAPE, "dense_wgrad: sizes too large");
+  ZMOE_REQUIRE(DW && workspace, ZMOE_ERR_NULL, "dense_wgrad: null pointer");
+  ZMOE_REQUIRE(M == 0 || (DY && X), ZMOE_ERR_NULL, "dense_wgrad: null operand");
+  const int S = dtype == ZMOE_DTYPE_BF16 ? splits : 1;  // fp32 runs unsplit (direct fp32 output)
+  ZMOE_REQUIRE(workspace_bytes >= zmoe_dense_wgrad_workspace_bytes(N, K, S > 1 ? S : 0), ZMOE_ERR_WORKSPACE,
+               "dense_wgrad: workspace of %zu bytes is too small", workspace_bytes);
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(N % v == 0 && K % v == 0 && aligned16(DW) && aligned16(workspace) &&
+                   (M == 0 || (ok_rows(dtype, DY, dy_stride_m) && ok_rows(dtype, X, x_stride_m))),
+               ZMOE_ERR_ALIGN, "dense_wgrad: N, K and strides must be multiples of %d elements", v);
+  hipStream_t s = as_stream(stream);
+  int64_t* off = reinterpret_cast<int64_t*>(workspace);
+  hipLaunchKernelGGL(split_offsets_kernel, dim3(1), dim3(64), 0, s, off, M, S);
+  int rc = check_launch("split_offsets_kernel");
+  if (rc) return rc;
+  if (S == 1) return zmoe_group_bwd_w(DY, dy_stride_m, X, x_stride_m, nullptr, 1, off, M, N, K, 1, dtype, DW,
+                                      nullptr, stream);
+  WgradParams p{};
+  p.dy = DY;
+  p.lddy = dy_stride_m;
+  p.x = X;
+  p.ldx = x_stride_m;
+  p.x_rows = nullptr;
+  p.x_div = 1;
+  p.x_div_shift = 0;
+  p.dw = reinterpret_cast<char*>(workspace) + 256;
+  p.offsets = off;
+  p.Ndy = (int)N;
+  p.Kx = (int)K;
+  p.E = S;
+  const int64_t dy_span = span_bytes(M, dy_stride_m, N, dtype), x_span = span_bytes(M, x_stride_m, K, dtype);
+  ZMOE_REQUIRE(dy_span <= kMaxSpan && x_span <= kMaxSpan, ZMOE_ERR_SHAPE, "dense_wgrad: DY or X spans more than 2 GiB");
+  p.dy_bytes = (uint32_t)dy_span;
+  p.x_bytes = (uint32_t)x_span;
+  if (use_big_tiles(M, S, N) && K >= 256)
+    rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, false, true>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+  else
+    rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, false, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
+  if (rc) return rc;
+  const int64_t n = N * K;  // multiple of 8
+  hipLaunchKernelGGL(reduce_splits_kernel<uint16_t>, dim3((unsigned)cdiv(n / 4, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const float*>(p.dw), S, n, reinterpret_cast<uint16_t*>(DW));
+  return check_launch("reduce_splits_kernel");
 }

@@ -1,10 +1,14 @@
 """Shared expert (reference modeling/expert_layer.py:5-24): dense SwiGLU.
 
-Its three bias-free projections are plain dense GEMMs and run on torch
-(hipBLASLt); state-dict keys gate_proj / up_proj / down_proj are unchanged.
+Its three bias-free projections are dense GEMMs (hipBLASLt through torch; the up
+and gate projections as one GEMM), the SwiGLU is a fused HIP pass and the weight
+grads are split-K HIP GEMMs (zmoe.functional.swiglu_mlp). State-dict keys
+gate_proj / up_proj / down_proj are unchanged.
 """
 
 import torch.nn as nn
+
+from zmoe import functional as _zf
 
 
 class ExpertMLP(nn.Module):
@@ -26,4 +30,5 @@ class ExpertMLP(nn.Module):
         nn.init.normal_(self.down_proj.weight, mean=0.0, std=self.initializer_range)
 
     def forward(self, x):
-        return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+        # down_proj(act_fn(gate_proj(x)) * up_proj(x)), expert_layer.py:23-24
+        return _zf.swiglu_mlp(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight)

@@ -1,7 +1,7 @@
 """Aux-loss-free sigmoid router (reference modeling/moe_gate.py:5-36) on MI355X.
 
-The gate projection stays a torch ``F.linear`` (a plain dense GEMM); the rest of
-the routing — sigmoid, +bias for selection, top-k, gather of the unbiased
+The gate projection is a library GEMM (its weight grad the split-K HIP kernel,
+zmoe.functional.linear); the rest of the routing — sigmoid, +bias for selection, top-k, gather of the unbiased
 probabilities and L1 renormalisation — is one HIP kernel (zmoe_route_topk) whose
 backward is the analytic gradient of the same expression.
 
@@ -13,8 +13,8 @@ bias add, as the reference's bf16 sigmoid does under autocast.
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
+from zmoe import functional as _zf
 from zmoe import ops as _z
 
 
@@ -56,6 +56,6 @@ class MoEGate(nn.Module):
     def forward(self, hidden_states):
         bsz, seq_len, h = hidden_states.shape
         hidden_states = hidden_states.view(-1, h)
-        gate_output = F.linear(hidden_states, self.weight, None)                # moe_gate.py:26
+        gate_output = _zf.linear(hidden_states, self.weight)                     # moe_gate.py:26
         topk_idx, topk_weight = RouteTopK.apply(gate_output, self.expert_biases, self.top_k)  # :27-34
         return topk_idx.view(bsz, seq_len, -1), topk_weight.view(bsz, seq_len, -1)

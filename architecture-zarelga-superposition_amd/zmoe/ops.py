@@ -234,6 +234,39 @@ def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor,
     return DWt, Db
 
 
+def dense_wgrad_splits(M: int, N: int, K: int) -> int:
+    """Row splits that give the dense weight-grad GEMM about one tile per CU."""
+    tile = 256 if (M >= 256 and N >= 256 and K >= 256) else 128
+    tiles = -(-N // tile) * -(-K // tile)
+    splits = max(1, min(64, -(-256 // tiles)))
+    while splits > 1 and M // splits < 1024:  # keep every split at >= 16 K-loop stages
+        splits -= 1
+    return splits
+
+
+def dense_wgrad(DY: torch.Tensor, X: torch.Tensor, splits: Optional[int] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """DW [N, K] = DY[M, N]^T X[M, K]: the weight grad of an nn.Linear (F.linear backward)."""
+    dev = _require_cuda(DY, X)
+    DY = _rows(DY)
+    X = _rows(X)
+    if DY.dtype != X.dtype or DY.shape[0] != X.shape[0]:
+        raise ValueError("dense_wgrad: DY and X must share dtype and row count")
+    M, N = DY.shape
+    K = X.shape[1]
+    if splits is None:
+        splits = dense_wgrad_splits(M, N, K)
+    DW = torch.empty((N, K), dtype=DY.dtype, device=dev) if out is None else out
+    if DW.shape != (N, K) or DW.dtype != DY.dtype or not DW.is_contiguous():
+        raise ValueError("dense_wgrad: bad out tensor")
+    nbytes = L.load().zmoe_dense_wgrad_workspace_bytes(N, K, splits if DY.dtype == torch.bfloat16 else 0)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with profiling.region("dense_wgrad", dev):
+        L.call("zmoe_dense_wgrad", _ptr(DY), DY.stride(0), _ptr(X), X.stride(0), M, N, K, _dtype_code(DY), splits,
+               _ptr(DW), _ptr(ws), nbytes, _stream(dev))
+    return DW
+
+
 def glu_w1_forward(x: torch.Tensor, W1: torch.Tensor, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
                    k: int):
     """W1 grouped GEMM with fused SwiGLU: returns H [R, 2f] and A [R, f] in sorted order."""

@@ -143,6 +143,23 @@ int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X,
                      void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Dense weight gradient DW[N, K] = DY^T X over M rows (DY [M, N], X [M, K]), for
+ * the nn.Linear weights around the routed experts: the shared expert's
+ * gate/up/down projections (modeling/expert_layer.py:23-24) and the gate
+ * projection (modeling/moe_gate.py:26), whose backward in the reference is
+ * torch autograd of F.linear. Their outputs are small next to M, so the rows are
+ * split into `splits` ranges computed by the grouped wgrad kernel into fp32
+ * partials, then summed in a fixed order and rounded once (deterministic).
+ * workspace: zmoe_dense_wgrad_workspace_bytes(N, K, splits) bytes, 16-byte
+ * aligned. fp32 runs unsplit.
+ * ------------------------------------------------------------------------- */
+size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int splits);
+int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void* X,
+                     int64_t x_stride_m, int64_t M, int64_t N, int64_t K,
+                     int dtype, int splits, void* DW, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * rowwise_sum_product — scattermoe/kernels/ops.py:9-80:
  *   out[t, j] = sum_h A[t, j, h] * B[t, h] (fp32 accumulation)
  * A [T, F, H], B [T, H] contiguous; each F32 or BF16; out F32 or BF16.

@@ -101,3 +101,28 @@ def test_glu_fused_forward_and_backward_dh(hip_device, dtype, T, d, f, E, k, ske
     if dtype == torch.bfloat16:
         dA = O.bf16_round(dA.astype(np.float32)).astype(np.float64)  # dA is stored in bf16 before the epilogue
     assert_close(np64(dH), O.swiglu_backward(dA, np64(H)), **tol, what="dH")
+
+
+@pytest.mark.parametrize("M,N,K,splits", [(1000, 128, 256, None), (1000, 128, 256, 3), (4100, 256, 512, 7),
+                                          (4096, 136, 264, 1), (0, 128, 128, 4), (20000, 1536, 512, None)])
+def test_dense_wgrad_bf16(hip_device, M, N, K, splits):
+    """DW = DY^T X with split-K fp32 partials (the nn.Linear weight grads of the shared
+    expert and gate projection) against float64."""
+    from zmoe import ops
+
+    g = gen(M + N + K)
+    DY = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    DW = ops.dense_wgrad(DY.to(hip_device), X.to(hip_device), splits=splits)
+    ref = np64(DY).T @ np64(X)
+    assert_close(np64(DW), ref, **TOL[torch.bfloat16], what=f"dense_wgrad M={M} splits={splits}")
+
+
+def test_dense_wgrad_f32(hip_device):
+    from zmoe import ops
+
+    g = gen(5)
+    DY = torch.randn(777, 64, generator=g)
+    X = torch.randn(777, 96, generator=g)
+    DW = ops.dense_wgrad(DY.to(hip_device), X.to(hip_device), splits=4)
+    assert_close(np64(DW), np64(DY).T @ np64(X), **TOL[torch.float32], what="dense_wgrad f32")
