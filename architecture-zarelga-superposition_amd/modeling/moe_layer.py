@@ -69,9 +69,9 @@ class MoELayer(nn.Module):
 
         flat_topk_idx = topk_idx.reshape(-1, self.n_experts_per_token)
         flat_topk_weight = topk_weight.reshape(-1, self.n_experts_per_token)
-        routed_output = self.routed_experts(x, flat_topk_weight, flat_topk_idx)
-
-        out = shared_output + routed_output
+        # out = shared_output + routed_output (moe_layer.py:48-53), the sum formed in the
+        # routed experts' combine pass
+        out = self.routed_experts(x, flat_topk_weight, flat_topk_idx, residual=shared_output)
 
         if unpad_indices is not None:
             out = pad_input(out.squeeze(0), unpad_indices, bsz, seq_len)

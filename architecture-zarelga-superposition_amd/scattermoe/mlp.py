@@ -32,12 +32,14 @@ class GLUExpertsFunction(torch.autograd.Function):
     """y = sum_j gates[:, j] * W2[e_j] silu(W1g[e_j] x) * (W1h[e_j] x) for every token."""
 
     @staticmethod
-    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int):
+    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int, residual=None):
         se, ss, off, inv = _z.flatten_sort_count(expert_idxs, num_experts)
         H, A = _z.glu_w1_forward(x, W1, se, ss, off, k)                       # mlp.py:96-102
         Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
                                expert_offsets=off)                             # mlp.py:103-108
-        out = _z.combine(Y, gates, k)                                          # parallel_experts.py:161-163
+        # + residual in the same pass (moe_layer.py:53 adds the shared expert's output)
+        out = _z.combine(Y, gates, k, addend=residual)                         # parallel_experts.py:161-163
+        ctx.has_residual = residual is not None
         ctx.save_for_backward(x, gates, W1, W2, se, ss, off, inv, H, A, Y)
         ctx.k = k
         ctx.num_experts = num_experts
@@ -55,7 +57,10 @@ class GLUExpertsFunction(torch.autograd.Function):
         dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False,
                                  expert_offsets=off)                           # :223-231 (W1)
         dx = _z.sum_k(dXe, k)                                                  # :236
-        return dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None
+        grads = (dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None)
+        if not ctx.has_residual:  # called without the residual argument
+            return grads
+        return grads + (dout if ctx.needs_input_grad[7] else None,)
 
 
 class MLP(nn.Module):
@@ -106,14 +111,18 @@ class GLUMLP(nn.Module):
     def extra_repr(self):
         return "k={}".format(self.top_k)
 
-    def forward(self, x: torch.Tensor, expert_p: torch.Tensor, expert_idxs: torch.Tensor):
+    def forward(self, x: torch.Tensor, expert_p: torch.Tensor, expert_idxs: torch.Tensor, residual=None):
+        """mlp.py:74-95. ``residual`` (not in the reference signature; default None keeps
+        its behaviour) is added to the output, in the combine pass on the fused path."""
         x_shape = x.size()
         x = x.view(-1, x_shape[-1])
         if self.fused:
             dtype = _compute_dtype(x)
+            res = None if residual is None else residual.reshape(-1, residual.shape[-1]).to(dtype)
             y = GLUExpertsFunction.apply(x.to(dtype), expert_p, expert_idxs,
                                          self.experts.compute_weight(dtype),
-                                         self.output_experts.compute_weight(dtype), self.top_k, self.num_experts)
+                                         self.output_experts.compute_weight(dtype), self.top_k, self.num_experts,
+                                         res)
             return y.view(*x_shape[:-1], y.size(-1))
         sorted_expert_idxs, sorted_scattered_idxs, expert_offsets = flatten_sort_count(
             expert_idxs, num_experts=self.num_experts)
@@ -123,4 +132,4 @@ class GLUMLP(nn.Module):
         y = self.output_experts(h, 1, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
                                 grouped_in=True, gates=expert_p)
         y = y.view(*x_shape[:-1], y.size(-1))
-        return y
+        return y if residual is None else residual + y

@@ -234,14 +234,23 @@ def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor,
     return DWt, Db
 
 
-def dense_wgrad_splits(M: int, N: int, K: int) -> int:
-    """Row splits that give the dense weight-grad GEMM about one tile per CU."""
+def dense_wgrad_splits(M: int, N: int, K: int, cus: int = 256) -> int:
+    """Row splits for the dense weight-grad GEMM: the split count minimising
+    (waves of tiles over the CUs) x (rows per split), plus the fp32 partials' extra
+    HBM traffic, with at least 16 K-loop stages (1024 rows) per split."""
     tile = 256 if (M >= 256 and N >= 256 and K >= 256) else 128
     tiles = -(-N // tile) * -(-K // tile)
-    splits = max(1, min(64, -(-256 // tiles)))
-    while splits > 1 and M // splits < 1024:  # keep every split at >= 16 K-loop stages
-        splits -= 1
-    return splits
+    stage_us, tile_fixed_us = 1.6, 11.0         # per 64-row stage and per tile, measured on MI355X
+    bytes_per_us = 5.0e6                        # partial write + read at ~5 TB/s
+
+    def cost(s: int) -> float:
+        waves = -(-tiles * s // cus)
+        stages = -(-M // (64 * s))
+        extra = 0.0 if s == 1 else 2.0 * s * N * K * 4 / bytes_per_us
+        return waves * (stages * stage_us + tile_fixed_us) + extra
+
+    cands = [s for s in range(1, 65) if s == 1 or M // s >= 1024]
+    return min(cands, key=cost)
 
 
 def dense_wgrad(DY: torch.Tensor, X: torch.Tensor, splits: Optional[int] = None,
