@@ -72,12 +72,15 @@ def gemm_flops(name: str, launch: int, T, d, k, f) -> float:
 
 
 def row_bytes(name: str, T, d, E, k) -> float:
-    """Algorithmic HBM bytes of one launch (bf16 rows, fp32 gates, int64 ids)."""
+    """Algorithmic HBM bytes of one launch (bf16 rows, fp32 gates, int64 ids).
+
+    The layer's combine also reads the shared expert's output [T, d] as its addend.
+    """
     R = T * k
     return {
         "route_topk": T * E * 2 + E * 4 + R * (8 + 4 + 4),
         "flatten_sort_count": R * 8 * 2 + R * 8 * 2 + R * 4,
-        "combine": R * d * 2 + R * 4 + T * d * 2,
+        "combine": R * d * 2 + R * 4 + T * d * 2 + T * d * 2,
         "combine_backward": R * d * 2 + T * d * 2 + R * (4 + 4 + 4) + R * d * 2,
         "sum_k": R * d * 2 + T * d * 2,
     }[name]
