@@ -40,8 +40,10 @@ constexpr int kGemmMaxE = 1024;
 constexpr int kXcds = 8;
 
 // EPI_STORE_BIAS: EPI_STORE plus a per-expert bias row (a separate instantiation keeps
-// the bias loads out of the common kernel's register budget).
-enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2, EPI_STORE_BIAS = 3 };
+// the bias loads out of the common kernel's register budget). EPI_NS: the Newton-Schulz
+// step outputs (bf16 only): t = bf16(acc); C = bf16(t + bf16(ns_beta * D)) when D
+// (p.aux) is given, else t; C2 = bf16(ns_gamma * t) when C2 is given.
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_SWIGLU_BWD = 2, EPI_STORE_BIAS = 3, EPI_NS = 4 };
 
 __device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
   return (uint32_t)(row * kRowBytes + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 7)) << 4));
@@ -280,8 +282,9 @@ struct RowsParams {
   const int64_t* c_rows;  // scatter: output row of sorted row i = c_rows[i] (null: i)
   void* c2;               // SwiGLU activation output
   int64_t ldc2;
-  const void* aux;        // H for the SwiGLU backward
+  const void* aux;        // H for the SwiGLU backward; D for EPI_NS
   int64_t ld_aux;
+  float ns_beta, ns_gamma; // EPI_NS scalars
   const void* bias;       // [E, N] or null
   int64_t bias_estride;
   const int64_t* offsets; // inclusive expert ends [E]
@@ -1087,6 +1090,37 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
         }
       }
     }
+  } else if constexpr (EPI == EPI_NS) {
+    // out = t + bf16(beta * D) and out2 = bf16(gamma * t) with t = bf16(acc): the rounding
+    // points of bf16 tensor arithmetic in muon.py:24-27 (each product and sum rounded)
+    const uint16_t* D = reinterpret_cast<const uint16_t*>(p.aux);
+    uint16_t* C2 = reinterpret_cast<uint16_t*>(p.c2);
+    wave_stage_bf16(st, acc, 0, MI, nullptr);
+    for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
+      const int rr = idx / S::CPR, cc = idx % S::CPR;
+      const int rl = wm0 + rr, col = ncol0 + cc * VEC;
+      if (rl < rows && col < p.N) {
+        const int64_t orow = row_table[rl];
+        const uint4 tv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+        float t[VEC];
+        unpack_chunk(tv, t, uint16_t{});
+        if (C2 != nullptr) {
+          float q[VEC];
+#pragma unroll
+          for (int u = 0; u < VEC; ++u) q[u] = p.ns_gamma * t[u];
+          *reinterpret_cast<uint4*>(C2 + orow * p.ldc2 + col) = pack_chunk(q, uint16_t{});
+        }
+        uint4 ov = tv;
+        if (D != nullptr) {
+          float dv[VEC], o[VEC];
+          unpack_chunk(ldg16(D + orow * p.ld_aux + col), dv, uint16_t{});
+#pragma unroll
+          for (int u = 0; u < VEC; ++u) o[u] = t[u] + to_f32(bf16_bits(p.ns_beta * dv[u]));
+          ov = pack_chunk(o, uint16_t{});
+        }
+        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = ov;
+      }
+    }
   } else {  // EPI_SWIGLU_BWD: staged dA (bf16, as the unfused path stores it); H rows in sorted order
     const uint16_t* Hs = reinterpret_cast<const uint16_t*>(p.aux);
     wave_stage_bf16(st, acc, 0, MI, nullptr);
@@ -1507,6 +1541,44 @@ int dispatch_rows(int dtype, RowsParams p, int64_t R, int bn_for_tiles_div, hipS
   }
   p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 64 : 128);
   return launch_rows_f32<128, 128, B_KN, EPI>(p, R, s);
+}
+
+int ns_gemm(const NsGemm& g, hipStream_t s) {
+  ZMOE_REQUIRE(g.E >= 1 && g.E <= kGemmMaxE && g.K >= 8 && g.N >= 8 && g.K % 8 == 0 && g.N % 8 == 0 &&
+                   g.R >= 0 && g.R < 0x7fffffffLL,
+               ZMOE_ERR_SHAPE, "ns_gemm: bad sizes");
+  if (g.R == 0) return ZMOE_OK;
+  RowsParams p{};
+  p.a = g.A;
+  p.lda = g.lda;
+  p.b = g.B;
+  p.b_estride = g.b_estride;
+  p.ldb = g.ldb;
+  p.c = g.C;
+  p.ldc = g.ldc;
+  p.c2 = g.C2;
+  p.ldc2 = g.ldc2;
+  p.aux = g.D;
+  p.ld_aux = g.ldd;
+  p.ns_beta = g.beta;
+  p.ns_gamma = g.gamma;
+  p.offsets = g.offsets;
+  p.K = g.K;
+  p.N = g.N;
+  p.E = g.E;
+  const int64_t a_span = ((g.R - 1) * g.lda + g.K) * 2;
+  const int64_t b_span = g.b_kn ? ((int64_t)(g.K - 1) * g.ldb + g.N) * 2 : ((int64_t)(g.N - 1) * g.ldb + g.K) * 2;
+  ZMOE_REQUIRE(a_span <= 0x7fff0000LL && b_span <= 0x7fff0000LL, ZMOE_ERR_SHAPE, "ns_gemm: operand spans 2 GiB");
+  p.a_bytes = (uint32_t)a_span;
+  p.b_bytes = (uint32_t)b_span;
+  if (use_big_tiles(g.R, g.E, g.N)) {
+    p.n_tiles = (int)cdiv(g.N, 256);
+    return g.b_kn ? launch_rows_bf16<256, 256, true, EPI_NS>(p, g.R, s)
+                  : launch_rows_bf16<256, 256, false, EPI_NS>(p, g.R, s);
+  }
+  p.n_tiles = (int)cdiv(g.N, 128);
+  return g.b_kn ? launch_rows_bf16<128, 128, true, EPI_NS>(p, g.R, s)
+                : launch_rows_bf16<128, 128, false, EPI_NS>(p, g.R, s);
 }
 
 }  // namespace zmoe

@@ -92,6 +92,31 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------- grouped GEMM, Newton-Schulz epilogue
+// C rows [R, N] (bf16; expert e owns rows offsets[e-1] .. offsets[e] - 1) = A rows [R, K] @ B_e,
+// where B_e sits at B + e * b_estride elements as [N][K] (K contiguous; b_kn false) or
+// [K][N] (N contiguous; b_kn true). Epilogue (t = bf16(acc)): C = bf16(t + bf16(beta * D))
+// when D is given, else t; C2 = bf16(gamma * t) when C2 is given. D and C2 share C's rows.
+struct NsGemm {
+  const void* A;
+  int64_t lda;
+  const void* B;
+  int64_t b_estride, ldb;
+  bool b_kn;
+  const int64_t* offsets;
+  int64_t R;
+  int K, N, E;
+  void* C;
+  int64_t ldc;
+  const void* D;
+  int64_t ldd;
+  float beta;
+  void* C2;
+  int64_t ldc2;
+  float gamma;
+};
+int ns_gemm(const NsGemm& g, hipStream_t s);
+
 // ---------------------------------------------------------------- host helpers
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);

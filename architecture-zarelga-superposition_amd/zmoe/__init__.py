@@ -6,7 +6,7 @@ of include/zmoe.h. The reference-shaped modules (``scattermoe``, ``modeling``)
 sit next to this package and call into it.
 """
 
-from . import _lib, functional, ops, profiling  # noqa: F401
+from . import _lib, functional, muon, ops, profiling  # noqa: F401
 from ._lib import LIB_PATH, ZmoeError, load  # noqa: F401
 
 __all__ = ["ops", "functional", "profiling", "load", "LIB_PATH", "ZmoeError"]

@@ -400,3 +400,36 @@ def bias_update_(expert_biases: torch.Tensor, expert_offsets: torch.Tensor, upda
     off = _idx64(expert_offsets)
     L.call("zmoe_bias_update", _ptr(off), off.numel(), float(update_rate), _ptr(expert_biases), _stream(dev))
     return expert_biases
+
+
+NS_COEFFS = (3.4445, -4.7750, 2.0315)  # optimizer/muon.py:16
+
+
+def newton_schulz5(G: torch.Tensor, steps: int, coeffs=NS_COEFFS) -> torch.Tensor:
+    """optimizer/muon.py:6-32 on G [..., m, n] (any float dtype): bf16 result of G's shape.
+
+    Leading dims form the stack (one matrix each, as the reference's batched matmuls
+    treat them); a tall stack (m > n) is transposed before and after, as muon.py:18-19
+    and :29-30 do. m and n must be multiples of 8.
+    """
+    dev = _require_cuda(G)
+    if G.ndim < 2:
+        raise ValueError("newton_schulz5: G needs at least 2 dims")
+    m, n = G.shape[-2], G.shape[-1]
+    X = G.to(torch.bfloat16).reshape(-1, m, n)
+    tall = m > n
+    if tall:
+        X = X.transpose(1, 2)
+    if X.data_ptr() == G.data_ptr() or not X.is_contiguous():
+        X = X.contiguous() if not X.is_contiguous() else X.clone()
+    E, mm, nn = X.shape
+    if E == 0:
+        return X.reshape(G.shape)
+    nbytes = int(L.load().zmoe_newton_schulz5_workspace_bytes(E, mm, nn))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    a, b, c = coeffs
+    L.call("zmoe_newton_schulz5", _ptr(X), E, mm, nn, int(steps), float(a), float(b), float(c), _ptr(ws), nbytes,
+           _stream(dev))
+    if tall:
+        X = X.transpose(1, 2)
+    return X.reshape(G.shape)

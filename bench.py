@@ -227,6 +227,74 @@ def pmc_summary(path: str) -> int:
     return 0
 
 
+def ns_flops(m: int, n: int, steps: int) -> float:
+    """Newton-Schulz GEMM flops for one m x n matrix (m <= n): X X^T, (cA) A, B X per step."""
+    m, n = min(m, n), max(m, n)
+    return steps * (2.0 * m * m * n + 2.0 * m * m * m + 2.0 * m * m * n)
+
+
+def muon_bench(args) -> int:
+    """Newton-Schulz (optimizer/muon.py:6-32, 5 steps) over the routed-expert weight stacks of
+    one C3 MoE layer (W1 [128, 1536, 2048], W2 [128, 2048, 768]), as the MuonMD step runs it
+    on 3-D expert weights (muon.py:449). Prints one JSON line; also times the same bf16
+    arithmetic through torch's batched matmuls (hipBLASLt) for comparison."""
+    import torch
+
+    from zmoe import ops
+
+    dev = torch.device("cuda:0")
+    E, d, f, steps = 128, 2048, 768, 5
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    stacks = [torch.randn(E, 2 * f, d, device=dev, generator=g), torch.randn(E, d, f, device=dev, generator=g)]
+    flops = sum(E * ns_flops(G.shape[1], G.shape[2], steps) for G in stacks)
+    a, b, c = ops.NS_COEFFS
+
+    def torch_ns(G):
+        # every batched-matmul operand is made contiguous: bf16 bmm on a transposed view
+        # (the .mT of a tall stack keeps its transposed strides through the elementwise
+        # ops) is avoided on this platform
+        X = G.bfloat16()
+        if G.size(-2) > G.size(-1):
+            X = X.mT.contiguous()
+        X = X / (X.norm(dim=(-2, -1), keepdim=True) + 1e-7)
+        for _ in range(steps):
+            A = X @ X.mT.contiguous()
+            B = b * A + c * A @ A
+            X = a * X + B @ X
+        return X.mT if G.size(-2) > G.size(-1) else X
+
+    def timed(fn, reps):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return 1000.0 * (time.perf_counter() - t0) / reps
+
+    reps = max(1, args.steps // 4)
+    print("muon bench: zmoe_newton_schulz5 on the two stacks", file=sys.stderr, flush=True)
+    ms = timed(lambda: [ops.newton_schulz5(G, steps) for G in stacks], reps)
+    print("muon bench: torch bf16 batched matmuls on the two stacks", file=sys.stderr, flush=True)
+    ms_torch = timed(lambda: [torch_ns(G) for G in stacks], reps)
+    tf = flops / (ms * 1e-3) / 1e12
+    out = {
+        "metric": "MuonMD Newton-Schulz (5 steps) over one C3 layer's routed-expert stacks, TFLOP/s",
+        "value": tf, "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 2, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) stacks)",
+        "config": {"workload": "muon-ns: W1 [128,1536,2048] + W2 [128,2048,768] (transposed to [128,768,2048]), 5 steps",
+                   "flops": flops},
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tf / PEAK_BF16_TFLOPS, "traffic": None},
+        "torch_bf16_bmm_ms": ms_torch, "speedup_vs_torch": ms_torch / ms,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -237,6 +305,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", action="store_true", help="run the counter-calibration copy and exit")
+    ap.add_argument("--muon", action="store_true",
+                    help="time the MuonMD Newton-Schulz step on the C3 routed-expert stacks instead of the layer")
     ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 --pmc CSVs under DIR and exit")
     args = ap.parse_args(argv)
     if args.pmc_summary:
@@ -248,6 +318,8 @@ def main(argv=None):
 
     if args.copy_probe:
         return copy_probe()
+    if args.muon:
+        return muon_bench(args)
 
     import torch
 

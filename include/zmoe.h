@@ -227,6 +227,17 @@ int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f,
 int zmoe_bias_update(const int64_t* expert_offsets, int E, float update_rate,
                      float* expert_biases, void* stream);
 
+/* optimizer/muon.py:6-32 (zeropower_via_newtonschulz5) on a stack of E matrices,
+ * the orthogonalisation inside the MuonMD step on 3-D expert weights
+ * (muon.py:399-508, called at :449). X [E, m, n] bf16, contiguous, m <= n (the
+ * caller transposes a tall stack first, as muon.py:18-19 does), updated in place:
+ *   X = X / (||X||_F + 1e-7);  repeat steps: A = X X^T; B = b A + (c A) A; X = a X + B X
+ * with bf16 rounding after every product and sum, as in bf16 tensor arithmetic.
+ * Workspace: zmoe_newton_schulz5_workspace_bytes(E, m, n), 256-byte aligned.      */
+size_t zmoe_newton_schulz5_workspace_bytes(int64_t E, int64_t m, int64_t n);
+int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int steps, float a, float b, float c,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

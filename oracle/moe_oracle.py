@@ -28,6 +28,10 @@ Pinning (what checks each function, all in ``tests/test_oracle.py``):
                            torch autograd of an independent dense formulation and
                            float64 central finite differences on tiny shapes.
 * ``bias_update``          closed form on a hand-built histogram.
+* ``newton_schulz5``       exact mode: the SVD closed form U phi^steps(S/||G||) V^T
+                           with phi(s) = a s + b s^3 + c s^5; transpose symmetry;
+                           bf16 mode: rounding points checked against torch's bf16
+                           tensor ops on tiny matrices.
 """
 
 from __future__ import annotations
@@ -71,6 +75,8 @@ __all__ = [
     "MoELayerOracle",
     "bias_update",
     "moe_load_metrics",
+    "NS_COEFFS",
+    "newton_schulz5",
 ]
 
 
@@ -504,3 +510,51 @@ def moe_load_metrics(topk_idx, E):
         max_expert_pct=float(counts.max()) * 100.0 / total,
         min_expert_pct=float(counts.min()) * 100.0 / total,
     )
+
+
+# --------------------------------------------------------------------------- #
+# (f)-3: Newton-Schulz orthogonalisation inside the MuonMD step
+# --------------------------------------------------------------------------- #
+NS_COEFFS = (3.4445, -4.7750, 2.0315)  # optimizer/muon.py:16
+
+
+def newton_schulz5(G, steps, coeffs=NS_COEFFS, bf16=True):
+    """optimizer/muon.py:6-32 on G [..., m, n] (float64 arithmetic).
+
+    bf16=True models the reference's bf16 tensor arithmetic: the input is rounded to
+    bf16; every GEMM result (float64 here, fp32-accumulated there) is rounded to
+    float32 and then to bf16; every elementwise product or sum is formed in float32
+    and rounded to bf16. ``c * A @ A`` parses as ``(c * A) @ A`` (muon.py:26).
+    bf16=False is exact arithmetic (no rounding), which the SVD closed form pins.
+    Returns float32 values (bf16-representable in bf16 mode).
+    """
+    a, b, c = (np.float32(v) for v in coeffs)
+    G = np.asarray(G)
+    tall = G.shape[-2] > G.shape[-1]
+
+    def rnd(x):
+        return bf16_round(np.asarray(x, dtype=np.float32)).astype(np.float64) if bf16 else np.asarray(x, np.float64)
+
+    def mul(s, x):  # python-float scalar times a bf16 tensor: float32 opmath, one rounding
+        return rnd(np.float32(s) * np.asarray(x, np.float32)) if bf16 else float(s) * x
+
+    def add(x, y):
+        return rnd(np.asarray(x, np.float32) + np.asarray(y, np.float32)) if bf16 else x + y
+
+    X = rnd(G.astype(np.float32) if bf16 else G.astype(np.float64))
+    if tall:
+        X = np.swapaxes(X, -1, -2)
+    nrm = np.sqrt((X * X).sum(axis=(-2, -1), keepdims=True))
+    if bf16:
+        nrm = rnd(nrm)
+        den = rnd(np.float32(nrm) + np.float32(1e-7))
+        X = rnd(np.asarray(X, np.float32) / np.asarray(den, np.float32))
+    else:
+        X = X / (nrm + 1e-7)
+    for _ in range(steps):
+        A = rnd(X @ np.swapaxes(X, -1, -2))
+        B = add(mul(b, A), rnd(mul(c, A) @ A))
+        X = add(mul(a, X), rnd(B @ X))
+    if tall:
+        X = np.swapaxes(X, -1, -2)
+    return np.asarray(X, dtype=np.float32)

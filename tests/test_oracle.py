@@ -297,3 +297,75 @@ def test_bias_update_closed_form():
     m = O.moe_load_metrics(idx, 4)
     assert m["pct_experts_used"] == 75.0 and m["max_expert_pct"] == 50.0 and m["min_expert_pct"] == 0.0
     assert abs(m["load_imbalance"] - np.mean(np.abs(np.array([3, 2, 1, 0]) / 1.5 - 1))) < 1e-12
+
+
+# ----------------------------------------------------------------- Newton-Schulz (MuonMD)
+def _phi_power(s, steps):
+    a, b, c = O.NS_COEFFS
+    for _ in range(steps):
+        s = a * s + b * s**3 + c * s**5
+    return s
+
+
+@pytest.mark.parametrize("shape", [(3, 6, 10), (2, 12, 5), (1, 9, 9)])
+@pytest.mark.parametrize("steps", [0, 1, 5])
+def test_newton_schulz_exact_is_svd_closed_form(shape, steps):
+    """Exact arithmetic: NS(G) = U phi^steps(S / (||G||_F + 1e-7)) V^T (muon.py:21-27)."""
+    G = np.random.default_rng(7).standard_normal(shape)
+    got = O.newton_schulz5(G, steps, bf16=False).astype(np.float64)
+    for e in range(shape[0]):
+        U, S, Vt = np.linalg.svd(G[e], full_matrices=False)
+        s = S / (np.linalg.norm(G[e]) + 1e-7)
+        ref = (U * _phi_power(s, steps)) @ Vt
+        np.testing.assert_allclose(got[e], ref, rtol=0, atol=1e-6 * max(1.0, np.abs(ref).max()))
+
+
+def test_newton_schulz_transpose_symmetry():
+    G = np.random.default_rng(8).standard_normal((2, 8, 24)).astype(np.float32)
+    for bf16 in (False, True):
+        a = O.newton_schulz5(G, 5, bf16=bf16)
+        b = O.newton_schulz5(np.swapaxes(G, -1, -2), 5, bf16=bf16)
+        np.testing.assert_array_equal(a, np.swapaxes(b, -1, -2))
+
+
+def _torch_ns_steps(G, steps):
+    """The reference expression in torch bf16 tensor ops (CPU), X after each step."""
+    a, b, c = O.NS_COEFFS
+    X = torch.from_numpy(G).bfloat16()
+    tall = X.size(-2) > X.size(-1)
+    if tall:
+        X = X.mT
+    X = X / (X.norm(dim=(-2, -1), keepdim=True) + 1e-7)
+    out = []
+    for _ in range(steps):
+        A = X @ X.mT
+        B = b * A + c * A @ A
+        X = a * X + B @ X
+        out.append((X.mT if tall else X).float().numpy())
+    return out
+
+
+@pytest.mark.parametrize("shape", [(3, 8, 16), (2, 16, 8), (4, 32, 48)])
+@pytest.mark.parametrize("seed", [9, 10, 11])
+def test_newton_schulz_bf16_rounding_points_match_torch(shape, seed):
+    """bf16 mode rounds where torch's bf16 tensor ops round (CPU torch, tiny sizes).
+
+    One step is compared bit for bit. Over five steps a single accumulation-order
+    flip in one GEMM output (torch sums in float32, the oracle in float64) is
+    amplified by the iteration (slope a = 3.44 at 0), so five steps are compared by
+    relative Frobenius error against the bf16 tolerance 2e-2.
+    """
+    G = np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+    ref = _torch_ns_steps(G, 5)
+    np.testing.assert_array_equal(O.newton_schulz5(G, 1), ref[0])
+    got5 = O.newton_schulz5(G, 5)
+    assert np.linalg.norm(got5 - ref[4]) <= 2e-2 * np.linalg.norm(ref[4])
+
+
+def test_newton_schulz_singular_values_land_in_band():
+    """The quintic drives every singular value of a well-conditioned input to ~[0.5, 1.5]."""
+    G = np.random.default_rng(10).standard_normal((2, 32, 64))
+    X = O.newton_schulz5(G, 5)
+    for e in range(2):
+        s = np.linalg.svd(X[e].astype(np.float64), compute_uv=False)
+        assert s.min() > 0.5 and s.max() < 1.5, (s.min(), s.max())
