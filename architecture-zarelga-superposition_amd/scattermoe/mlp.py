@@ -32,14 +32,21 @@ class GLUExpertsFunction(torch.autograd.Function):
     """y = sum_j gates[:, j] * W2[e_j] silu(W1g[e_j] x) * (W1h[e_j] x) for every token."""
 
     @staticmethod
-    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int, residual=None):
+    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int, *extra):
+        # extra: (residual [T, d] or None, stash dict or None); residual is added in the
+        # combine pass, and stash["expert_offsets"] receives the sort's offsets
+        residual = extra[0] if len(extra) > 0 else None
+        stash = extra[1] if len(extra) > 1 else None
         se, ss, off, inv = _z.flatten_sort_count(expert_idxs, num_experts)
+        if stash is not None:
+            stash["expert_offsets"] = off
         H, A = _z.glu_w1_forward(x, W1, se, ss, off, k)                       # mlp.py:96-102
         Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
                                expert_offsets=off)                             # mlp.py:103-108
         # + residual in the same pass (moe_layer.py:53 adds the shared expert's output)
         out = _z.combine(Y, gates, k, addend=residual)                         # parallel_experts.py:161-163
         ctx.has_residual = residual is not None
+        ctx.n_extra = len(extra)
         ctx.save_for_backward(x, gates, W1, W2, se, ss, off, inv, H, A, Y)
         ctx.k = k
         ctx.num_experts = num_experts
@@ -58,9 +65,10 @@ class GLUExpertsFunction(torch.autograd.Function):
                                  expert_offsets=off)                           # :223-231 (W1)
         dx = _z.sum_k(dXe, k)                                                  # :236
         grads = (dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None)
-        if not ctx.has_residual:  # called without the residual argument
-            return grads
-        return grads + (dout if ctx.needs_input_grad[7] else None,)
+        extra = [None] * ctx.n_extra  # one grad per extra input (residual, stash)
+        if ctx.has_residual and ctx.needs_input_grad[7]:
+            extra[0] = dout
+        return grads + tuple(extra)
 
 
 class MLP(nn.Module):
@@ -107,6 +115,8 @@ class GLUMLP(nn.Module):
         self.activation = activation
         # The fused kernels implement SiLU-gated units without expert biases.
         self.fused = fused and not bias and isinstance(activation, nn.SiLU)
+        # expert_offsets of the last forward's sort (device tensor; not module state)
+        self.last_expert_offsets = None
 
     def extra_repr(self):
         return "k={}".format(self.top_k)
@@ -119,13 +129,16 @@ class GLUMLP(nn.Module):
         if self.fused:
             dtype = _compute_dtype(x)
             res = None if residual is None else residual.reshape(-1, residual.shape[-1]).to(dtype)
+            stash = {}
             y = GLUExpertsFunction.apply(x.to(dtype), expert_p, expert_idxs,
                                          self.experts.compute_weight(dtype),
                                          self.output_experts.compute_weight(dtype), self.top_k, self.num_experts,
-                                         res)
+                                         res, stash)
+            self.last_expert_offsets = stash["expert_offsets"]
             return y.view(*x_shape[:-1], y.size(-1))
         sorted_expert_idxs, sorted_scattered_idxs, expert_offsets = flatten_sort_count(
             expert_idxs, num_experts=self.num_experts)
+        self.last_expert_offsets = expert_offsets
         h, gates = self.experts(x, self.top_k, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
                                 grouped_out=True).chunk(2, dim=-1)
         h = self.activation(gates) * h
