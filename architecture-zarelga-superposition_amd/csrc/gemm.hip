@@ -1040,6 +1040,12 @@ __device__ __forceinline__ void wave_stage_bf16(char* st, const f32x16_t (&acc)[
   }
 }
 
+// The store loops below run in batches of EPI_BATCH chunks per lane: every LDS read
+// (staged values, output-row numbers) and global read (H, D) of a batch is issued
+// before the first store of the batch, so their latencies overlap instead of adding up
+// chunk by chunk.
+constexpr int EPI_BATCH = 8;
+
 template <int BM, int BN, int EPI, int MI, int NI>
 __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st, const int* row_table,
                                                    const f32x16_t (&acc)[MI][NI], int e, int64_t row0, int rows,
@@ -1049,99 +1055,136 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
   const int lane = threadIdx.x & 63;
   uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
   const int ncol0 = nt * BN + wn0;
-  if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_BIAS) {
-    const uint16_t* bias = nullptr;
-    if constexpr (EPI == EPI_STORE_BIAS)
-      bias = reinterpret_cast<const uint16_t*>(p.bias) + (int64_t)e * p.bias_estride + ncol0;
-    wave_stage_bf16(st, acc, 0, MI, bias, p.N - ncol0);
-    for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
-      const int rr = idx / S::CPR, cc = idx % S::CPR;
-      const int rl = wm0 + rr, col = ncol0 + cc * VEC;
-      if (rl < rows && col < p.N)
-        *reinterpret_cast<uint4*>(C + (int64_t)row_table[rl] * p.ldc + col) =
-            *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
-    }
-  } else if constexpr (EPI == EPI_SWIGLU) {
+  if constexpr (EPI == EPI_SWIGLU) {
     // staged columns per 64: [h 32 | gate 32] for pair columns jj0 + 32 pb + 0..31;
     // A = silu(gate) * h from the bf16-rounded h and gate, as stored in H
     constexpr int PB = NI / 2, CPP = 32 / VEC;  // pair blocks, chunks per 32 columns
+    constexpr int ITERS = 16 * MI * PB * CPP / 64;
+    constexpr int B = ITERS < EPI_BATCH ? ITERS : EPI_BATCH;
+    static_assert(ITERS % B == 0, "batches tile the staged block");
     uint16_t* A2 = reinterpret_cast<uint16_t*>(p.c2);
     const int jj0 = nt * (BN / 2) + (wn0 / 64) * 32;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {  // two halves of the rows: 3 outputs per pair need room
       wave_stage_bf16(st, acc, half * MI / 2, (half + 1) * MI / 2, nullptr);
-      for (int idx = lane; idx < 16 * MI * PB * CPP; idx += 64) {
-        const int rr = idx / (PB * CPP), rem = idx % (PB * CPP);
-        const int pb = rem / CPP, cc = rem % CPP;
-        const int rl = wm0 + half * 16 * MI + rr;
-        const int jj = jj0 + pb * 32 + cc * VEC;
-        if (rl < rows && jj < p.half) {
-          const int64_t orow = row_table[rl];
-          const uint4 hv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + cc * VEC) * 2);
-          const uint4 gv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + 32 + cc * VEC) * 2);
-          float h[VEC], gt[VEC], a[VEC];
-          unpack_chunk(hv, h, uint16_t{});
-          unpack_chunk(gv, gt, uint16_t{});
 #pragma unroll
-          for (int u = 0; u < VEC; ++u) a[u] = silu_f(gt[u]) * h[u];
-          *reinterpret_cast<uint4*>(C + orow * p.ldc + jj) = hv;
-          *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + jj) = gv;
-          *reinterpret_cast<uint4*>(A2 + orow * p.ldc2 + jj) = pack_chunk(a, uint16_t{});
+      for (int i0 = 0; i0 < ITERS; i0 += B) {
+        uint4 hv[B], gv[B];
+        int orow[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int idx = lane + 64 * (i0 + u);
+          const int rr = idx / (PB * CPP), rem = idx % (PB * CPP);
+          const int pb = rem / CPP, cc = rem % CPP;
+          hv[u] = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + cc * VEC) * 2);
+          gv[u] = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + (pb * 64 + 32 + cc * VEC) * 2);
+          orow[u] = row_table[wm0 + half * 16 * MI + rr];
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int idx = lane + 64 * (i0 + u);
+          const int rr = idx / (PB * CPP), rem = idx % (PB * CPP);
+          const int pb = rem / CPP, cc = rem % CPP;
+          const int rl = wm0 + half * 16 * MI + rr;
+          const int jj = jj0 + pb * 32 + cc * VEC;
+          if (rl < rows && jj < p.half) {
+            float h[VEC], gt[VEC], a[VEC];
+            unpack_chunk(hv[u], h, uint16_t{});
+            unpack_chunk(gv[u], gt, uint16_t{});
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) a[q] = silu_f(gt[q]) * h[q];
+            const int64_t o = orow[u];
+            *reinterpret_cast<uint4*>(C + o * p.ldc + jj) = hv[u];
+            *reinterpret_cast<uint4*>(C + o * p.ldc + p.half + jj) = gv[u];
+            *reinterpret_cast<uint4*>(A2 + o * p.ldc2 + jj) = pack_chunk(a, uint16_t{});
+          }
         }
       }
     }
-  } else if constexpr (EPI == EPI_NS) {
-    // out = t + bf16(beta * D) and out2 = bf16(gamma * t) with t = bf16(acc): the rounding
-    // points of bf16 tensor arithmetic in muon.py:24-27 (each product and sum rounded)
-    const uint16_t* D = reinterpret_cast<const uint16_t*>(p.aux);
-    uint16_t* C2 = reinterpret_cast<uint16_t*>(p.c2);
-    wave_stage_bf16(st, acc, 0, MI, nullptr);
-    for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
-      const int rr = idx / S::CPR, cc = idx % S::CPR;
-      const int rl = wm0 + rr, col = ncol0 + cc * VEC;
-      if (rl < rows && col < p.N) {
-        const int64_t orow = row_table[rl];
-        const uint4 tv = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+    return;
+  }
+  constexpr int ITERS = 32 * MI * S::CPR / 64;
+  constexpr int B = ITERS < EPI_BATCH ? ITERS : EPI_BATCH;
+  constexpr int NB = ITERS / B;
+  static_assert(ITERS % B == 0, "batches tile the staged block");
+  const uint16_t* bias = nullptr;
+  if constexpr (EPI == EPI_STORE_BIAS)
+    bias = reinterpret_cast<const uint16_t*>(p.bias) + (int64_t)e * p.bias_estride + ncol0;
+  wave_stage_bf16(st, acc, 0, MI, bias, p.N - ncol0);
+  // chunk (row, column) of item u of batch i
+  auto item_rl = [&](int i, int u) { return wm0 + (lane + 64 * (i * B + u)) / S::CPR; };
+  auto item_cc = [&](int i, int u) { return (lane + 64 * (i * B + u)) % S::CPR; };
+  auto item_ok = [&](int i, int u) { return item_rl(i, u) < rows && ncol0 + item_cc(i, u) * VEC < p.N; };
+  // Global operands of the epilogue (H for EPI_SWIGLU_BWD, D for EPI_NS; both in the
+  // grouped row order row0 + rl) are read one batch ahead, before the stores of the
+  // current batch: a later wait on them then does not also wait for those stores.
+  constexpr bool kGlobal = EPI == EPI_SWIGLU_BWD || EPI == EPI_NS;
+  const uint16_t* G = reinterpret_cast<const uint16_t*>(p.aux);
+  const bool has_g = kGlobal && G != nullptr;
+  uint4 g0[2][B], g1[2][B];
+  auto load_globals = [&](int i, int buf) {
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (item_ok(i, u)) {
+        const uint16_t* r = G + (row0 + item_rl(i, u)) * p.ld_aux + ncol0 + item_cc(i, u) * VEC;
+        g0[buf][u] = ldg16(r);
+        if constexpr (EPI == EPI_SWIGLU_BWD) g1[buf][u] = ldg16(r + p.half);
+      }
+    }
+  };
+  if (has_g) load_globals(0, 0);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int cur = i & 1;
+    uint4 tv[B];
+    int orow[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      tv[u] = *reinterpret_cast<const uint4*>(st + (item_rl(i, u) - wm0) * S::PITCH + item_cc(i, u) * 16);
+      orow[u] = row_table[item_rl(i, u)];
+    }
+    if (has_g && i + 1 < NB) load_globals(i + 1, cur ^ 1);
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (!item_ok(i, u)) continue;
+      const int col = ncol0 + item_cc(i, u) * VEC;
+      const int64_t o = orow[u];
+      if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_BIAS) {
+        *reinterpret_cast<uint4*>(C + o * p.ldc + col) = tv[u];
+      } else if constexpr (EPI == EPI_NS) {
+        // out = t + bf16(beta * D) and out2 = bf16(gamma * t) with t = bf16(acc): the rounding
+        // points of bf16 tensor arithmetic in muon.py:24-27 (each product and sum rounded)
+        uint16_t* C2 = reinterpret_cast<uint16_t*>(p.c2);
         float t[VEC];
-        unpack_chunk(tv, t, uint16_t{});
+        unpack_chunk(tv[u], t, uint16_t{});
         if (C2 != nullptr) {
           float q[VEC];
 #pragma unroll
-          for (int u = 0; u < VEC; ++u) q[u] = p.ns_gamma * t[u];
-          *reinterpret_cast<uint4*>(C2 + orow * p.ldc2 + col) = pack_chunk(q, uint16_t{});
+          for (int v = 0; v < VEC; ++v) q[v] = p.ns_gamma * t[v];
+          *reinterpret_cast<uint4*>(C2 + o * p.ldc2 + col) = pack_chunk(q, uint16_t{});
         }
-        uint4 ov = tv;
-        if (D != nullptr) {
-          float dv[VEC], o[VEC];
-          unpack_chunk(ldg16(D + orow * p.ld_aux + col), dv, uint16_t{});
+        uint4 ov = tv[u];
+        if (has_g) {
+          float d[VEC], r[VEC];
+          unpack_chunk(g0[cur][u], d, uint16_t{});
 #pragma unroll
-          for (int u = 0; u < VEC; ++u) o[u] = t[u] + to_f32(bf16_bits(p.ns_beta * dv[u]));
-          ov = pack_chunk(o, uint16_t{});
+          for (int v = 0; v < VEC; ++v) r[v] = t[v] + to_f32(bf16_bits(p.ns_beta * d[v]));
+          ov = pack_chunk(r, uint16_t{});
         }
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = ov;
-      }
-    }
-  } else {  // EPI_SWIGLU_BWD: staged dA (bf16, as the unfused path stores it); H rows in sorted order
-    const uint16_t* Hs = reinterpret_cast<const uint16_t*>(p.aux);
-    wave_stage_bf16(st, acc, 0, MI, nullptr);
-    for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
-      const int rr = idx / S::CPR, cc = idx % S::CPR;
-      const int rl = wm0 + rr, col = ncol0 + cc * VEC;
-      if (rl < rows && col < p.N) {
-        const int64_t i = row0 + rl;
-        const int64_t orow = row_table[rl];
+        *reinterpret_cast<uint4*>(C + o * p.ldc + col) = ov;
+      } else {  // EPI_SWIGLU_BWD: staged dA (bf16, as the unfused path stores it), H rows in sorted order
         float da[VEC], h[VEC], gt[VEC], dh[VEC], dg[VEC];
-        unpack_chunk(*reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16), da, uint16_t{});
-        unpack_chunk(ldg16(Hs + i * p.ld_aux + col), h, uint16_t{});
-        unpack_chunk(ldg16(Hs + i * p.ld_aux + p.half + col), gt, uint16_t{});
+        unpack_chunk(tv[u], da, uint16_t{});
+        unpack_chunk(g0[cur][u], h, uint16_t{});
+        unpack_chunk(g1[cur][u], gt, uint16_t{});
 #pragma unroll
-        for (int u = 0; u < VEC; ++u) {
-          const float sg = sigmoid_fast(gt[u]);
-          dh[u] = da[u] * gt[u] * sg;
-          dg[u] = da[u] * h[u] * sg * (1.f + gt[u] * (1.f - sg));
+        for (int v = 0; v < VEC; ++v) {
+          const float sg = sigmoid_fast(gt[v]);
+          dh[v] = da[v] * gt[v] * sg;
+          dg[v] = da[v] * h[v] * sg * (1.f + gt[v] * (1.f - sg));
         }
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + col) = pack_chunk(dh, uint16_t{});
-        *reinterpret_cast<uint4*>(C + orow * p.ldc + p.half + col) = pack_chunk(dg, uint16_t{});
+        *reinterpret_cast<uint4*>(C + o * p.ldc + col) = pack_chunk(dh, uint16_t{});
+        *reinterpret_cast<uint4*>(C + o * p.ldc + p.half + col) = pack_chunk(dg, uint16_t{});
       }
     }
   }
@@ -1151,14 +1194,26 @@ template <int MI, int NI>
 __device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* st, const f32x16_t (&acc)[MI][NI],
                                                     int e, int m0, int n0, int wm0, int wn0) {
   using S = WaveStage<NI * 32>;
+  constexpr int ITERS = 32 * MI * S::CPR / 64;
+  constexpr int B = ITERS < EPI_BATCH ? ITERS : EPI_BATCH;
+  static_assert(ITERS % B == 0, "batches tile the staged block");
   const int lane = threadIdx.x & 63;
   uint16_t* DW = reinterpret_cast<uint16_t*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
   wave_stage_bf16(st, acc, 0, MI, nullptr);
-  for (int idx = lane; idx < 32 * MI * S::CPR; idx += 64) {
-    const int rr = idx / S::CPR, cc = idx % S::CPR;
-    const int m = m0 + wm0 + rr, n = n0 + wn0 + cc * 8;
-    if (m < p.Ndy && n < p.Kx)
-      *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) = *reinterpret_cast<const uint4*>(st + rr * S::PITCH + cc * 16);
+#pragma unroll
+  for (int i0 = 0; i0 < ITERS; i0 += B) {
+    uint4 v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int idx = lane + 64 * (i0 + u);
+      v[u] = *reinterpret_cast<const uint4*>(st + (idx / S::CPR) * S::PITCH + (idx % S::CPR) * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int idx = lane + 64 * (i0 + u);
+      const int m = m0 + wm0 + idx / S::CPR, n = n0 + wn0 + (idx % S::CPR) * 8;
+      if (m < p.Ndy && n < p.Kx) *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) = v[u];
+    }
   }
 }
 
