@@ -65,10 +65,14 @@ __global__ __launch_bounds__(kRowThreads) void group_kernel(const T* __restrict_
 // per thread), KF = 0 loops over a runtime k.
 
 // ------------------------------------------------------------------ combine
+// out_rows (optional): token t's output row (the re-pad of moe_layer.py:55-56 folded in);
+// a row outside [0, out_total) is not written.
 template <typename T, int KF>
 __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restrict__ Y, const float* __restrict__ g,
                                                               const T* __restrict__ add, int64_t T_, int k_rt,
-                                                              int64_t d, T* __restrict__ out, int tpr) {
+                                                              int64_t d, T* __restrict__ out,
+                                                              const int64_t* __restrict__ out_rows, int64_t out_total,
+                                                              int tpr) {
   constexpr int VN = V<T>::N;
   const int k = KF > 0 ? KF : k_rt;
   const int rpb = kRowThreads / tpr;
@@ -76,6 +80,8 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
   if (t >= T_) return;
   const int lt = threadIdx.x % tpr;
   const int64_t nch = d / VN;
+  const int64_t orow = out_rows ? out_rows[t] : t;
+  if (orow < 0 || orow >= out_total) return;
   for (int64_t ch = lt; ch < nch; ch += tpr) {
     float acc[VN];
     if (add) {
@@ -110,18 +116,20 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
     }
 #pragma unroll
     for (int q = 0; q < VN; ++q) acc[q] += part[q];
-    st16(out + t * d + ch * VN, pack_chunk(acc, T{}));
+    st16(out + orow * d + ch * VN, pack_chunk(acc, T{}));
   }
 }
 
 // ------------------------------------------------------------------ combine backward
 // d_gates[t,j] = <Y[t*k+j], dout[t]>; grouped[inverse[t*k+j]] = g[t,j] * dout[t].
 // KM: a compile-time bound on k (slot arrays sized KM; slots j >= k are skipped).
+// dout_rows (optional): token t's row of dout (the padded layout's gradient read in place);
+// a row outside [0, dout_total) reads as zero.
 template <typename T, int KM>
 __global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
-    const T* __restrict__ Y, const T* __restrict__ dout, const float* __restrict__ g,
-    const int32_t* __restrict__ inverse, int64_t T_, int k, int64_t d, float* __restrict__ d_gates,
-    T* __restrict__ grouped, int tpr) {
+    const T* __restrict__ Y, const T* __restrict__ dout, const int64_t* __restrict__ dout_rows, int64_t dout_total,
+    const float* __restrict__ g, const int32_t* __restrict__ inverse, int64_t T_, int k, int64_t d,
+    float* __restrict__ d_gates, T* __restrict__ grouped, int tpr) {
   constexpr int VN = V<T>::N;
   __shared__ float red[kRowThreads / 64][KM];
   const int rpb = kRowThreads / tpr;
@@ -142,9 +150,16 @@ __global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
       dst[j] = inverse[t * k + jj];
       w[j] = g[t * k + jj];
     }
+    const int64_t drow = dout_rows ? dout_rows[t] : t;
+    const bool drow_ok = drow >= 0 && drow < dout_total;
     for (int64_t ch = lt; ch < nch; ch += tpr) {
       float go[VN];
-      unpack_chunk(ld16(dout + t * d + ch * VN), go, T{});
+      if (drow_ok) {
+        unpack_chunk(ld16(dout + drow * d + ch * VN), go, T{});
+      } else {
+#pragma unroll
+        for (int q = 0; q < VN; ++q) go[q] = 0.f;
+      }
       uint4 yv[KM];
 #pragma unroll
       for (int j = 0; j < KM; ++j) yv[j] = ld16(Y + (t * k + (j < k ? j : k - 1)) * d + ch * VN);
@@ -326,8 +341,10 @@ extern "C" int zmoe_group(const void* A, int64_t lda, int64_t K, int dtype, cons
   return check_launch("group");
 }
 
-extern "C" int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t T, int k, int64_t d,
-                            int dtype, void* out, void* stream) {
+namespace {
+
+int combine_impl(const void* Y, const float* gates, const void* addend, int64_t T, int k, int64_t d, int dtype,
+                 const int64_t* out_rows, int64_t out_total, void* out, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "combine: dtype");
   ZMOE_REQUIRE(T >= 0 && k >= 1 && d >= 0, ZMOE_ERR_SHAPE, "combine: bad sizes");
   if (T == 0 || d == 0) return ZMOE_OK;
@@ -340,7 +357,7 @@ extern "C" int zmoe_combine(const void* Y, const float* gates, const void* adden
   auto launch = [&](auto kf, auto tt) {
     using TT = decltype(tt);
     hipLaunchKernelGGL((combine_kernel<TT, decltype(kf)::value>), grid, block, 0, as_stream(stream), (const TT*)Y,
-                       gates, (const TT*)addend, T, k, d, (TT*)out, m.tpr);
+                       gates, (const TT*)addend, T, k, d, (TT*)out, out_rows, out_total, m.tpr);
   };
   auto by_k = [&](auto tt) {
     if (k == 8) launch(std::integral_constant<int, 8>{}, tt);
@@ -354,9 +371,9 @@ extern "C" int zmoe_combine(const void* Y, const float* gates, const void* adden
   return check_launch("combine");
 }
 
-extern "C" int zmoe_combine_backward(const void* Y, const void* grad_out, const float* gates, const int32_t* inverse,
-                                     int64_t T, int k, int64_t d, int dtype, float* d_gates, void* grouped_grad_out,
-                                     void* stream) {
+int combine_backward_impl(const void* Y, const void* grad_out, const int64_t* grad_rows, int64_t grad_total,
+                          const float* gates, const int32_t* inverse, int64_t T, int k, int64_t d, int dtype,
+                          float* d_gates, void* grouped_grad_out, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "combine_backward: dtype");
   ZMOE_REQUIRE(T >= 0 && k >= 1 && k <= kMaxFanOut && d >= 0, ZMOE_ERR_SHAPE,
                "combine_backward: need 1 <= k <= %d", kMaxFanOut);
@@ -372,8 +389,8 @@ extern "C" int zmoe_combine_backward(const void* Y, const void* grad_out, const 
   auto launch = [&](auto km, auto tt) {
     using TT = decltype(tt);
     hipLaunchKernelGGL((combine_backward_kernel<TT, decltype(km)::value>), grid, block, 0, as_stream(stream),
-                       (const TT*)Y, (const TT*)grad_out, gates, inverse, T, k, d, d_gates, (TT*)grouped_grad_out,
-                       m.tpr);
+                       (const TT*)Y, (const TT*)grad_out, grad_rows, grad_total, gates, inverse, T, k, d,
+                       d_gates, (TT*)grouped_grad_out, m.tpr);
   };
   auto by_k = [&](auto tt) {
     if (k <= 2) launch(std::integral_constant<int, 2>{}, tt);
@@ -385,6 +402,37 @@ extern "C" int zmoe_combine_backward(const void* Y, const void* grad_out, const 
   if (dtype == ZMOE_DTYPE_BF16) by_k(uint16_t{});
   else by_k(float{});
   return check_launch("combine_backward");
+}
+
+}  // namespace
+
+extern "C" int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t T, int k, int64_t d,
+                            int dtype, void* out, void* stream) {
+  return combine_impl(Y, gates, addend, T, k, d, dtype, nullptr, T, out, stream);
+}
+
+extern "C" int zmoe_combine_rows(const void* Y, const float* gates, const void* addend, int64_t T, int k, int64_t d,
+                                 int dtype, const int64_t* out_rows, int64_t out_total, void* out, void* stream) {
+  ZMOE_REQUIRE(T == 0 || out_rows, ZMOE_ERR_NULL, "combine_rows: null out_rows");
+  ZMOE_REQUIRE(out_total >= 0, ZMOE_ERR_SHAPE, "combine_rows: out_total < 0");
+  return combine_impl(Y, gates, addend, T, k, d, dtype, out_rows, out_total, out, stream);
+}
+
+extern "C" int zmoe_combine_backward(const void* Y, const void* grad_out, const float* gates, const int32_t* inverse,
+                                     int64_t T, int k, int64_t d, int dtype, float* d_gates, void* grouped_grad_out,
+                                     void* stream) {
+  return combine_backward_impl(Y, grad_out, nullptr, T, gates, inverse, T, k, d, dtype, d_gates, grouped_grad_out,
+                               stream);
+}
+
+extern "C" int zmoe_combine_backward_rows(const void* Y, const void* grad_out, const int64_t* grad_rows,
+                                          int64_t grad_total, const float* gates, const int32_t* inverse, int64_t T,
+                                          int k, int64_t d, int dtype, float* d_gates, void* grouped_grad_out,
+                                          void* stream) {
+  ZMOE_REQUIRE(T == 0 || grad_rows, ZMOE_ERR_NULL, "combine_backward_rows: null grad_rows");
+  ZMOE_REQUIRE(grad_total >= 0, ZMOE_ERR_SHAPE, "combine_backward_rows: grad_total < 0");
+  return combine_backward_impl(Y, grad_out, grad_rows, grad_total, gates, inverse, T, k, d, dtype, d_gates,
+                               grouped_grad_out, stream);
 }
 
 extern "C" int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype, const void* add0, const void* add1,

@@ -2,8 +2,9 @@
 
 Same submodules, parameters and state-dict keys as the reference:
 ``gate`` (MoEGate), ``shared_experts`` (ExpertMLP), ``routed_experts`` (GLUMLP).
-The optional unpad/re-pad around the layer (the reference uses flash-attn's
-index_first_axis / pad_input) is done with torch index ops.
+The optional unpad around the layer (the reference uses flash-attn's
+index_first_axis) is a torch gather; the re-pad of the output (pad_input) is folded
+into the routed experts' combine pass, which writes the padded layout directly.
 """
 
 import torch
@@ -70,11 +71,11 @@ class MoELayer(nn.Module):
         flat_topk_idx = topk_idx.reshape(-1, self.n_experts_per_token)
         flat_topk_weight = topk_weight.reshape(-1, self.n_experts_per_token)
         # out = shared_output + routed_output (moe_layer.py:48-53), the sum formed in the
-        # routed experts' combine pass
-        out = self.routed_experts(x, flat_topk_weight, flat_topk_idx, residual=shared_output)
-
-        if unpad_indices is not None:
-            out = pad_input(out.squeeze(0), unpad_indices, bsz, seq_len)
-            topk_idx = pad_input(topk_idx.squeeze(0), unpad_indices, bsz, seq_len)
-
-        return out, topk_idx
+        # routed experts' combine pass, which also writes the re-padded layout (:55-56)
+        # directly when unpad_indices is given
+        if unpad_indices is None:
+            return self.routed_experts(x, flat_topk_weight, flat_topk_idx, residual=shared_output), topk_idx
+        out = self.routed_experts(x, flat_topk_weight, flat_topk_idx, residual=shared_output,
+                                  pad=(unpad_indices, bsz * seq_len))
+        topk_idx = pad_input(topk_idx.squeeze(0), unpad_indices, bsz, seq_len)
+        return out.view(bsz, seq_len, -1), topk_idx

@@ -33,10 +33,13 @@ class GLUExpertsFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int, *extra):
-        # extra: (residual [T, d] or None, stash dict or None); residual is added in the
-        # combine pass, and stash["expert_offsets"] receives the sort's offsets
+        # extra: (residual [T, d] or None, stash dict or None, pad_rows [T] or None, pad_total):
+        # residual is added in the combine pass; stash["expert_offsets"] receives the sort's
+        # offsets; with pad_rows the output is the padded [pad_total, d] (moe_layer.py:55-56)
         residual = extra[0] if len(extra) > 0 else None
         stash = extra[1] if len(extra) > 1 else None
+        pad_rows = extra[2] if len(extra) > 2 else None
+        pad_total = extra[3] if len(extra) > 3 else None
         se, ss, off, inv = _z.flatten_sort_count(expert_idxs, num_experts)
         if stash is not None:
             stash["expert_offsets"] = off
@@ -44,9 +47,10 @@ class GLUExpertsFunction(torch.autograd.Function):
         Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
                                expert_offsets=off)                             # mlp.py:103-108
         # + residual in the same pass (moe_layer.py:53 adds the shared expert's output)
-        out = _z.combine(Y, gates, k, addend=residual)                         # parallel_experts.py:161-163
+        out = _z.combine(Y, gates, k, addend=residual, out_rows=pad_rows, out_total=pad_total)  # :161-163
         ctx.has_residual = residual is not None
         ctx.n_extra = len(extra)
+        ctx.pad_rows = pad_rows
         ctx.save_for_backward(x, gates, W1, W2, se, ss, off, inv, H, A, Y)
         ctx.k = k
         ctx.num_experts = num_experts
@@ -57,7 +61,7 @@ class GLUExpertsFunction(torch.autograd.Function):
         x, gates, W1, W2, se, ss, off, inv, H, A, Y = ctx.saved_tensors
         k, E = ctx.k, ctx.num_experts
         dout = dout.to(x.dtype)
-        d_gates, dYg = _z.combine_backward(Y, dout, gates, inv)               # parallel_experts.py:191-208
+        d_gates, dYg = _z.combine_backward(Y, dout, gates, inv, grad_rows=ctx.pad_rows)  # :191-208
         dH = _z.glu_w2_backward_dh(dYg, W2, H, se, off)                        # :223-231 + silu*mul backward
         dW2, _ = _z.group_bwd_w(dYg, A, off, E)                                # :216-221 (W2)
         dW1, _ = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)          # :213-221 (W1, x gathered)
@@ -65,9 +69,9 @@ class GLUExpertsFunction(torch.autograd.Function):
                                  expert_offsets=off)                           # :223-231 (W1)
         dx = _z.sum_k(dXe, k)                                                  # :236
         grads = (dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None)
-        extra = [None] * ctx.n_extra  # one grad per extra input (residual, stash)
+        extra = [None] * ctx.n_extra  # one grad per extra input (residual, stash, pad_rows, pad_total)
         if ctx.has_residual and ctx.needs_input_grad[7]:
-            extra[0] = dout
+            extra[0] = dout if ctx.pad_rows is None else dout.index_select(0, ctx.pad_rows)
         return grads + tuple(extra)
 
 
@@ -121,21 +125,24 @@ class GLUMLP(nn.Module):
     def extra_repr(self):
         return "k={}".format(self.top_k)
 
-    def forward(self, x: torch.Tensor, expert_p: torch.Tensor, expert_idxs: torch.Tensor, residual=None):
-        """mlp.py:74-95. ``residual`` (not in the reference signature; default None keeps
-        its behaviour) is added to the output, in the combine pass on the fused path."""
+    def forward(self, x: torch.Tensor, expert_p: torch.Tensor, expert_idxs: torch.Tensor, residual=None, pad=None):
+        """mlp.py:74-95. Two arguments beyond the reference signature (their defaults keep its
+        behaviour): ``residual`` is added to the output, in the combine pass on the fused
+        path; ``pad = (rows, total)`` returns the padded [total, d] output whose row rows[t]
+        is token t's (moe_layer.py:55-56), written by the combine in place."""
         x_shape = x.size()
         x = x.view(-1, x_shape[-1])
         if self.fused:
             dtype = _compute_dtype(x)
             res = None if residual is None else residual.reshape(-1, residual.shape[-1]).to(dtype)
             stash = {}
+            args = (res, stash) if pad is None else (res, stash, pad[0], int(pad[1]))
             y = GLUExpertsFunction.apply(x.to(dtype), expert_p, expert_idxs,
                                          self.experts.compute_weight(dtype),
                                          self.output_experts.compute_weight(dtype), self.top_k, self.num_experts,
-                                         res, stash)
+                                         *args)
             self.last_expert_offsets = stash["expert_offsets"]
-            return y.view(*x_shape[:-1], y.size(-1))
+            return y if pad is not None else y.view(*x_shape[:-1], y.size(-1))
         sorted_expert_idxs, sorted_scattered_idxs, expert_offsets = flatten_sort_count(
             expert_idxs, num_experts=self.num_experts)
         self.last_expert_offsets = expert_offsets
@@ -145,4 +152,9 @@ class GLUMLP(nn.Module):
         y = self.output_experts(h, 1, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
                                 grouped_in=True, gates=expert_p)
         y = y.view(*x_shape[:-1], y.size(-1))
-        return y if residual is None else residual + y
+        y = y if residual is None else residual + y
+        if pad is not None:
+            rows, total = pad
+            y = torch.zeros((int(total), y.size(-1)), dtype=y.dtype, device=y.device).index_copy(
+                0, rows, y.reshape(-1, y.size(-1)))
+        return y

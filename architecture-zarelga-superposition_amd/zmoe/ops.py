@@ -310,34 +310,60 @@ def glu_w2_backward_dh(dYg: torch.Tensor, W2: torch.Tensor, H: torch.Tensor, sor
 
 
 # --------------------------------------------------------------------- combine / reductions
-def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out[t] = addend[t] + sum_j gates[t, j] * Y[t*k + j]."""
-    dev = _require_cuda(Y, gates, addend)
+def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch.Tensor] = None,
+            out_rows: Optional[torch.Tensor] = None, out_total: Optional[int] = None) -> torch.Tensor:
+    """out[t] = addend[t] + sum_j gates[t, j] * Y[t*k + j].
+
+    With ``out_rows`` (int64 [T]) the result is the padded [out_total, d] tensor whose row
+    out_rows[t] is token t's output and whose other rows are zero (moe_layer.py:55-56).
+    """
+    dev = _require_cuda(Y, gates, addend, out_rows)
     Y = Y.contiguous()
     d = Y.shape[-1]
     T = Y.numel() // (d * k)
     g = gates.reshape(T, k).to(torch.float32).contiguous()
     if addend is not None:
         addend = addend.reshape(T, d).to(Y.dtype).contiguous()
-    out = torch.empty((T, d), dtype=Y.dtype, device=dev)
     with profiling.region("combine", dev):
-        L.call("zmoe_combine", _ptr(Y), _ptr(g), _ptr(addend), T, k, d, _dtype_code(Y), _ptr(out), _stream(dev))
+        if out_rows is None:
+            out = torch.empty((T, d), dtype=Y.dtype, device=dev)
+            L.call("zmoe_combine", _ptr(Y), _ptr(g), _ptr(addend), T, k, d, _dtype_code(Y), _ptr(out), _stream(dev))
+        else:
+            rows = _idx64(out_rows)
+            if rows.numel() != T:
+                raise ValueError("combine: out_rows must hold one row per token")
+            out = torch.zeros((out_total, d), dtype=Y.dtype, device=dev)
+            L.call("zmoe_combine_rows", _ptr(Y), _ptr(g), _ptr(addend), T, k, d, _dtype_code(Y), _ptr(rows),
+                   int(out_total), _ptr(out), _stream(dev))
     return out
 
 
-def combine_backward(Y: torch.Tensor, grad_out: torch.Tensor, gates: torch.Tensor, inverse: torch.Tensor):
-    """(d_gates [T, k] f32, grouped_grad_out [T*k, d] in sorted order)."""
-    dev = _require_cuda(Y, grad_out, gates, inverse)
+def combine_backward(Y: torch.Tensor, grad_out: torch.Tensor, gates: torch.Tensor, inverse: torch.Tensor,
+                     grad_rows: Optional[torch.Tensor] = None):
+    """(d_gates [T, k] f32, grouped_grad_out [T*k, d] in sorted order).
+
+    With ``grad_rows`` (int64 [T]) token t's gradient is row grad_rows[t] of the padded
+    ``grad_out`` [rows, d], read in place.
+    """
+    dev = _require_cuda(Y, grad_out, gates, inverse, grad_rows)
     Y = Y.contiguous()
     d = Y.shape[-1]
     T, k = gates.shape
     g = gates.to(torch.float32).contiguous()
-    go = grad_out.reshape(T, d).to(Y.dtype).contiguous()
     d_gates = torch.empty((T, k), dtype=torch.float32, device=dev)
     grouped = torch.empty((T * k, d), dtype=Y.dtype, device=dev)
     with profiling.region("combine_backward", dev):
-        L.call("zmoe_combine_backward", _ptr(Y), _ptr(go), _ptr(g), _ptr(inverse), T, k, d, _dtype_code(Y),
-               _ptr(d_gates), _ptr(grouped), _stream(dev))
+        if grad_rows is None:
+            go = grad_out.reshape(T, d).to(Y.dtype).contiguous()
+            L.call("zmoe_combine_backward", _ptr(Y), _ptr(go), _ptr(g), _ptr(inverse), T, k, d, _dtype_code(Y),
+                   _ptr(d_gates), _ptr(grouped), _stream(dev))
+        else:
+            go = grad_out.reshape(-1, d).to(Y.dtype).contiguous()
+            rows = _idx64(grad_rows)
+            if rows.numel() != T:
+                raise ValueError("combine_backward: grad_rows must hold one row per token")
+            L.call("zmoe_combine_backward_rows", _ptr(Y), _ptr(go), _ptr(rows), go.shape[0], _ptr(g), _ptr(inverse),
+                   T, k, d, _dtype_code(Y), _ptr(d_gates), _ptr(grouped), _stream(dev))
     return d_gates, grouped
 
 

@@ -210,6 +210,19 @@ int zmoe_combine_backward(const void* Y, const void* grad_out, const float* gate
                           int dtype, float* d_gates, void* grouped_grad_out,
                           void* stream);
 
+/* The two calls above with the unpad/re-pad of moe_layer.py:39-42 and :55-56 folded in:
+ * token t's output row is out_rows[t] of out [out_total, d] (rows not listed are left
+ * untouched, so the caller zero-fills the padded output), and token t's gradient is read
+ * from row grad_rows[t] of the padded grad_out [grad_total, d]. Row numbers outside
+ * [0, total) are not written / read as zero.                                      */
+int zmoe_combine_rows(const void* Y, const float* gates, const void* addend, int64_t T,
+                      int k, int64_t d, int dtype, const int64_t* out_rows, int64_t out_total,
+                      void* out, void* stream);
+int zmoe_combine_backward_rows(const void* Y, const void* grad_out, const int64_t* grad_rows,
+                               int64_t grad_total, const float* gates, const int32_t* inverse,
+                               int64_t T, int k, int64_t d, int dtype, float* d_gates,
+                               void* grouped_grad_out, void* stream);
+
 /* scattermoe/parallel_experts.py:236 (d_expanded_input.view(T,k,d).sum(-2))
  * plus up to two addends (gate and shared-expert input grads):
  *   out[t, :] = sum_j Xe[t*k + j, :] + add0[t, :] + add1[t, :]               */

@@ -116,6 +116,38 @@ def test_layer_unpad_indices(hip_device):
     assert torch.equal(idx.view(B * S, -1)[valid], ref_idx.view(-1, 2))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_layer_unpad_backward_matches_unpadded(hip_device, dtype):
+    """The re-pad folded into the combine (and the padded gradient read in place by its
+    backward) gives the gradients of the unpadded computation: bit-identical parameter
+    grads, hidden-state grads equal on valid rows and zero on padding."""
+    from modeling.model_config import ModelConfig
+    from modeling.moe_layer import MoELayer
+
+    torch.manual_seed(1)
+    cfg = ModelConfig(hidden_size=128, intermediate_size=64, n_experts=10, n_shared_experts=2, n_experts_per_token=2)
+    layer = MoELayer(cfg).to(hip_device).to(dtype)
+    layer.gate.expert_biases.data = layer.gate.expert_biases.data.float()
+    B, S = 3, 40
+    valid = torch.tensor([i for i in range(B * S) if (i % 5) != 1], device=hip_device)
+    h = torch.randn(B, S, 128, device=hip_device).to(dtype).requires_grad_(True)
+    dout = torch.randn(B, S, 128, device=hip_device).to(dtype)
+    out, _ = layer(h, unpad_indices=valid)
+    out.backward(dout)
+    grads = {n: p.grad.clone() for n, p in layer.named_parameters()}
+    layer.zero_grad(set_to_none=True)
+    hu = h.detach().view(1, B * S, 128)[:, valid].clone().requires_grad_(True)
+    ref, _ = layer(hu)
+    ref.backward(dout.view(B * S, 128)[valid].view(1, -1, 128))
+    for n, p in layer.named_parameters():
+        assert torch.equal(grads[n], p.grad), n
+    hg = h.grad.view(B * S, 128)
+    assert torch.equal(hg[valid], hu.grad.view(-1, 128))
+    pad = torch.ones(B * S, dtype=torch.bool, device=hip_device)
+    pad[valid] = False
+    assert (hg[pad] == 0).all()
+
+
 def test_c3_full_size_properties(hip_device):
     """BASELINE config 3 at full size (T=32768 d=2048 E=128 k=8 f=768, shared 1536):
     sort invariants, linearity of the routed combine in the gates (exact for a

@@ -85,3 +85,35 @@ def test_swiglu(hip_device, dtype):
     assert_close(np64(A), O.swiglu(np64(H)), **TOL[dtype], what="swiglu")
     dH = ops.swiglu_backward(dA.to(hip_device), H.to(hip_device))
     assert_close(np64(dH), O.swiglu_backward(np64(dA), np64(H)), **TOL[dtype], what="swiglu_backward")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_combine_rows_writes_padded_layout(hip_device, dtype):
+    """zmoe_combine_rows / zmoe_combine_backward_rows (the re-pad of moe_layer.py:55-56 folded
+    in) against the row-contiguous calls; row numbers outside [0, total) are skipped on write
+    and read as zero."""
+    from zmoe import ops
+
+    T, k, d, total = 37, 4, 96, 60
+    g = gen(12)
+    Y = torch.randn(T * k, d, generator=g).to(dtype).to(hip_device)
+    w = torch.rand(T, k, generator=g).to(hip_device)
+    add = torch.randn(T, d, generator=g).to(dtype).to(hip_device)
+    rows = torch.randperm(total, generator=g)[:T].to(hip_device)
+    rows[5] = -1        # outside the padded output: not written
+    rows[9] = total     # outside: not written
+    ref = ops.combine(Y, w, k, addend=add)
+    out = ops.combine(Y, w, k, addend=add, out_rows=rows, out_total=total)
+    ok = (rows >= 0) & (rows < total)
+    assert torch.equal(out[rows[ok]], ref[ok])
+    written = torch.zeros(total, dtype=torch.bool, device=hip_device)
+    written[rows[ok]] = True
+    assert (out[~written] == 0).all()
+
+    dout_pad = torch.randn(total, d, generator=g).to(dtype).to(hip_device)
+    _, ss, _, inv = ops.flatten_sort_count(random_topk(T, 8, k, seed=12).to(hip_device), 8)
+    dout = torch.zeros(T, d, dtype=dtype, device=hip_device)
+    dout[ok] = dout_pad[rows[ok]]
+    dg_ref, gr_ref = ops.combine_backward(Y, dout, w, inv)
+    dg, gr = ops.combine_backward(Y, dout_pad, w, inv, grad_rows=rows)
+    assert torch.equal(dg, dg_ref) and torch.equal(gr, gr_ref)
