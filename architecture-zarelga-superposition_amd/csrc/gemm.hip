@@ -1392,24 +1392,28 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
   const char* x_base = reinterpret_cast<const char*>(p.x);
 
   // Gathered x rows: the wave's 16 k-rows of a stage come as byte offsets in scalar
-  // registers, loaded one stage ahead with scalar loads (they count on lgkmcnt, so
-  // waiting for them never drains in-flight LDS loads). Rows past the expert's end
-  // get kOOBRow, which stays out of range after adding any column offset.
+  // registers. Their indices are fetched one stage ahead with one vector load per wave
+  // (lanes 0..15, the low 32-bit words of the int64 entries) and moved to scalar
+  // registers with v_readlane when the stage's loads are set up. A vector load counts
+  // on vmcnt, which the K loop only waits on at its barrier; scalar loads would count on
+  // lgkmcnt and stall every fragment-read wait until they returned. Rows past the
+  // expert's end get kOOBRow, which stays out of range after adding any column offset.
   constexpr uint32_t kOOBRow = 0x7ffffff0u;
-  typedef const __attribute__((address_space(4))) int64_t cidx_t;
-  cidx_t* xr = (cidx_t*)(p.x_rows);  // global -> constant address space (scalar loads)
+  const uint32_t* xr32 = reinterpret_cast<const uint32_t*>(p.x_rows);
   uint32_t src_off[16];
+  uint32_t pend = 0;  // this lane's index word for the next stage (lanes 0..15 hold the wave's 16 k-rows)
   const int64_t ldx2 = p.ldx * 2;
+  auto issue_idx = [&](int kt) -> uint32_t {
+    const int pos = kt * KS + 16 * wu + (int)(threadIdx.x & 15);
+    return xr32[2 * (r_begin + (pos < nrows ? pos : nrows - 1))];
+  };
   auto fetch_src = [&](int kt) {
+    if (kt == 0) pend = issue_idx(0);
     const int base = kt * KS + 16 * wu;
     uint32_t v[16];  // gather indices are below 2^31 (R < 2^31)
-    if (base + 16 <= nrows) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = (uint32_t)xr[r_begin + base + j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = (uint32_t)xr[r_begin + min(base + j, nrows - 1)];
-    }
+    for (int j = 0; j < 16; ++j) v[j] = (uint32_t)__builtin_amdgcn_readlane((int)pend, j);
+    if (kt + 1 < nk) pend = issue_idx(kt + 1);
     if (p.x_div_shift >= 0) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) v[j] >>= p.x_div_shift;
