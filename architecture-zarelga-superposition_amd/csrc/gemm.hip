@@ -285,6 +285,8 @@ struct RowsParams {
   const void* aux;        // H for the SwiGLU backward; D for EPI_NS
   int64_t ld_aux;
   float ns_beta, ns_gamma; // EPI_NS scalars
+  int ns_sym_m;            // EPI_NS: > 0 when every expert's output is a symmetric m x m matrix:
+                           // only tiles on or above the diagonal run, and they also write their mirror
   const void* bias;       // [E, N] or null
   int64_t bias_estride;
   const int64_t* offsets; // inclusive expert ends [E]
@@ -311,13 +313,31 @@ struct WgradParams {
 };
 
 struct RowsTile {
-  int e, nt, rows;
+  int e, nt, rows, mt;  // mt: m-tile index within the expert (symmetric launches)
   int64_t row0;
 };
 
 // Map this workgroup to (expert, m-tile, n-tile) of a rows launch; false if it has no tile.
 template <int BM>
 __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem, RowsTile& t) {
+  if (p.ns_sym_m > 0) {
+    // m x m outputs, one per expert: the upper-triangle tiles (nt >= mt) in row order
+    const int nm = (p.ns_sym_m + BM - 1) / BM;
+    const int tri = nm * (nm + 1) / 2;
+    const int logical = xcd_logical_tile(p.E * tri);
+    if (logical < 0) return false;
+    t.e = logical / tri;
+    int r = logical % tri, mt = 0;
+    while (r >= nm - mt) {
+      r -= nm - mt;
+      ++mt;
+    }
+    t.mt = mt;
+    t.nt = mt + r;
+    t.row0 = (int64_t)t.e * p.ns_sym_m + (int64_t)mt * BM;
+    t.rows = min(BM, p.ns_sym_m - mt * BM);
+    return true;
+  }
   int* tstart = reinterpret_cast<int*>(smem);
   int* tmp = tstart + kGemmMaxE + 4;
   const int mtiles = build_tile_starts<BM>(p.offsets, p.E, tstart, tmp);
@@ -332,6 +352,7 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
     else hi = mid - 1;
   }
   t.e = lo;
+  t.mt = 0;
   const int64_t e_begin = lo ? p.offsets[lo - 1] : 0;
   t.row0 = e_begin + (int64_t)(mt - tstart[lo]) * BM;
   t.rows = (int)min((int64_t)BM, p.offsets[lo] - t.row0);
@@ -1049,7 +1070,7 @@ constexpr int EPI_BATCH = 8;
 template <int BM, int BN, int EPI, int MI, int NI>
 __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st, const int* row_table,
                                                    const f32x16_t (&acc)[MI][NI], int e, int64_t row0, int rows,
-                                                   int nt, int wm0, int wn0) {
+                                                   int nt, int wm0, int wn0, int mt = 0) {
   using S = WaveStage<NI * 32>;
   constexpr int VEC = 8;
   const int lane = threadIdx.x & 63;
@@ -1185,6 +1206,72 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
         }
         *reinterpret_cast<uint4*>(C + o * p.ldc + col) = pack_chunk(dh, uint16_t{});
         *reinterpret_cast<uint4*>(C + o * p.ldc + p.half + col) = pack_chunk(dg, uint16_t{});
+      }
+    }
+  }
+  if constexpr (EPI == EPI_NS) {
+    // Symmetric output (the Gram products of the Newton-Schulz step): a tile above the
+    // diagonal also writes its mirror. Output row j of the mirror block is column j of
+    // the staged block, read 8 rows at a time with 16-bit LDS reads.
+    if (p.ns_sym_m > 0 && nt != mt) {
+      constexpr int CPC = 32 * MI / VEC;                 // 16-byte chunks per mirrored row
+      constexpr int MITERS = NI * 32 * CPC / 64;
+      constexpr int MB = MITERS < EPI_BATCH ? MITERS : EPI_BATCH;
+      static_assert(MITERS % MB == 0, "batches tile the mirrored block");
+      const uint16_t* D = reinterpret_cast<const uint16_t*>(p.aux);
+      uint16_t* C2 = reinterpret_cast<uint16_t*>(p.c2);
+      const int64_t ebase = row0 - (int64_t)mt * BM;     // the expert's first row
+      const int jcol0 = nt * BN + wn0;                   // the block's first column = first mirrored row
+#pragma unroll
+      for (int i0 = 0; i0 < MITERS; i0 += MB) {
+        uint4 tv[MB], dv[MB];
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+          const int idx = lane + 64 * (i0 + u);
+          const int c = idx / CPC, rc = idx % CPC;       // staged column, chunk of 8 staged rows
+          uint32_t w[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = *reinterpret_cast<const uint16_t*>(st + (rc * VEC + 2 * q) * S::PITCH + c * 2);
+            const uint32_t hi = *reinterpret_cast<const uint16_t*>(st + (rc * VEC + 2 * q + 1) * S::PITCH + c * 2);
+            w[q] = lo | (hi << 16);
+          }
+          tv[u] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        if (D != nullptr) {
+#pragma unroll
+          for (int u = 0; u < MB; ++u) {
+            const int idx = lane + 64 * (i0 + u);
+            const int c = idx / CPC, rc = idx % CPC;
+            if (jcol0 + c < p.N && wm0 + rc * VEC < rows)
+              dv[u] = ldg16(D + (ebase + jcol0 + c) * p.ld_aux + mt * BM + wm0 + rc * VEC);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+          const int idx = lane + 64 * (i0 + u);
+          const int c = idx / CPC, rc = idx % CPC;
+          if (jcol0 + c >= p.N || wm0 + rc * VEC >= rows) continue;
+          const int64_t o = ebase + jcol0 + c;
+          const int col = mt * BM + wm0 + rc * VEC;
+          float t[VEC];
+          unpack_chunk(tv[u], t, uint16_t{});
+          if (C2 != nullptr) {
+            float q[VEC];
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) q[v] = p.ns_gamma * t[v];
+            *reinterpret_cast<uint4*>(C2 + o * p.ldc2 + col) = pack_chunk(q, uint16_t{});
+          }
+          uint4 ov = tv[u];
+          if (D != nullptr) {
+            float d[VEC], r[VEC];
+            unpack_chunk(dv[u], d, uint16_t{});
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) r[v] = t[v] + to_f32(bf16_bits(p.ns_beta * d[v]));
+            ov = pack_chunk(r, uint16_t{});
+          }
+          *reinterpret_cast<uint4*>(C + o * p.ldc + col) = ov;
+        }
       }
     }
   }
@@ -1332,7 +1419,7 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   // every wave is done with the operand stages (and has written its row-table entries)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,
-                                  nt, wm0, wn0);
+                                  nt, wm0, wn0, tile.mt);
 }
 
 // fp32 output straight from the accumulators (split-K partials; no rounding): lane
@@ -1621,6 +1708,7 @@ int ns_gemm(const NsGemm& g, hipStream_t s) {
   p.ld_aux = g.ldd;
   p.ns_beta = g.beta;
   p.ns_gamma = g.gamma;
+  p.ns_sym_m = g.sym_m;
   p.offsets = g.offsets;
   p.K = g.K;
   p.N = g.N;

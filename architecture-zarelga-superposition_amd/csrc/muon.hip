@@ -9,9 +9,10 @@
 //   repeat steps:  A = X X^T;  B = b A + (c A) A;  X = a X + B X
 // The three GEMMs of a step are the grouped rows kernel with one "expert" per
 // matrix: A = X X^T reads its right operand as nn.Linear-style rows of X; (cA) A
-// and B X read A and X as [K][N]. Their epilogues
-// form cA (a second output of the first GEMM) and the b A and a X sums, so each
-// step is three launches and no elementwise passes.
+// and B X read A and X as [K][N]. Their epilogues form cA (a second output of the
+// first GEMM) and the b A and a X sums, so each step is three launches and no
+// elementwise passes. A and B are symmetric, so their GEMMs run only the tiles on
+// or above the diagonal and write each off-diagonal tile's mirror as well.
 //
 // The Frobenius norm is a deterministic two-pass reduction: fp32 partial sums
 // of squares per (matrix, slice), then every slice block sums its matrix's
@@ -174,6 +175,7 @@ extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int
     g1.offsets = offsets; g1.R = R; g1.K = (int)n; g1.N = (int)m; g1.E = (int)E;
     g1.C = Abuf; g1.ldc = m;
     g1.C2 = Pbuf; g1.ldc2 = m; g1.gamma = c;
+    g1.sym_m = (int)m;  // X X^T is symmetric: upper-triangle tiles plus their mirror
     rc = ns_gemm(g1, s);
     if (rc) return rc;
     // B = (cA) A + bA, A read as [K][N] (its columns), so the product does not rely on
@@ -184,6 +186,7 @@ extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int
     g2.offsets = offsets; g2.R = R; g2.K = (int)m; g2.N = (int)m; g2.E = (int)E;
     g2.C = Bbuf; g2.ldc = m;
     g2.D = Abuf; g2.ldd = m; g2.beta = b;
+    g2.sym_m = (int)m;  // (cA) A + bA is symmetric (polynomial in the symmetric A)
     rc = ns_gemm(g2, s);
     if (rc) return rc;
     // X' = B X + aX

@@ -114,6 +114,8 @@ struct NsGemm {
   void* C2;
   int64_t ldc2;
   float gamma;
+  int sym_m;  // > 0: each expert's output is a symmetric sym_m x sym_m matrix (N == sym_m, uniform
+              // rows): only the tiles on or above the diagonal run and they write their mirror
 };
 int ns_gemm(const NsGemm& g, hipStream_t s);
 

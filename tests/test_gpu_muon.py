@@ -3,12 +3,16 @@ the C ABI (``zmoe_newton_schulz5`` via ``zmoe.ops.newton_schulz5``).
 
 Comparisons are against the oracle's bf16 mode, which rounds where the reference's
 bf16 tensor arithmetic rounds (pinned against torch's own bf16 ops on the CPU).
-The normalisation alone (steps = 0) is compared bit for bit. After GEMM steps a
-1-ulp difference from a different fp32 accumulation order is amplified by the
-iteration (slope a = 3.44 at 0), so results are compared by relative Frobenius
-error per matrix against the bf16 tolerance 2e-2. At the C3 expert-stack sizes the
-check is the same on sampled matrices, plus the singular values of the result
-against the exact-arithmetic closed form U phi^5(S / ||G||) V^T.
+The normalisation alone (steps = 0) is compared bit for bit. One and two steps are
+compared by relative Frobenius error per matrix against 2e-3: the only differences
+left are fp32 accumulation order inside the GEMMs (and, for the symmetric products,
+the mirrored tiles), which flip a few bf16 roundings. The iteration amplifies such
+flips about tenfold per step from the third step on (its slope at 0 is a = 3.44), so
+after five steps two correct bf16 implementations already differ by up to ~1.5% (the
+oracle against torch's own CPU bf16 arithmetic on these shapes); five steps are
+compared against 5e-2. At the C3 stack sizes the check is the same on sampled
+matrices, plus the singular values of the result against the exact-arithmetic closed
+form U phi^5(S / ||G||) V^T, which the rounding noise does not move.
 """
 
 import numpy as np
@@ -19,7 +23,7 @@ import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-REL_FRO = 2e-2
+REL_FRO = {1: 2e-3, 2: 2e-3, 5: 5e-2}  # by step count (see the module docstring)
 
 
 def rel_fro(got, ref):
@@ -34,7 +38,7 @@ def make_stack(shape, seed, dev):
     return torch.randn(*shape, device=dev, generator=g)
 
 
-@pytest.mark.parametrize("shape", [(3, 64, 128), (2, 128, 64), (1, 256, 256), (4, 40, 72), (2, 512, 768)])
+@pytest.mark.parametrize("shape", [(3, 64, 128), (2, 128, 64), (1, 256, 256), (4, 40, 72), (2, 512, 768), (3, 200, 264), (2, 648, 1024)])
 def test_normalisation_bit_exact(hip_device, shape):
     from zmoe import ops
 
@@ -44,7 +48,9 @@ def test_normalisation_bit_exact(hip_device, shape):
     np.testing.assert_array_equal(got.float().cpu().numpy(), O.newton_schulz5(G.cpu().numpy(), 0))
 
 
-@pytest.mark.parametrize("shape", [(3, 64, 128), (2, 128, 64), (1, 256, 256), (4, 40, 72), (2, 512, 768)])
+# (2, 512, 768), (3, 200, 264) and (2, 648, 1024) span several tiles per matrix (128 and 256
+# tiles, full and partial), so the symmetric products' mirrored tiles are exercised
+@pytest.mark.parametrize("shape", [(3, 64, 128), (2, 128, 64), (1, 256, 256), (4, 40, 72), (2, 512, 768), (3, 200, 264), (2, 648, 1024)])
 @pytest.mark.parametrize("steps", [1, 2, 5])
 def test_steps_match_oracle(hip_device, shape, steps):
     from zmoe import ops
@@ -54,7 +60,7 @@ def test_steps_match_oracle(hip_device, shape, steps):
     ref = O.newton_schulz5(G.cpu().numpy(), steps)
     for e in range(shape[0]):
         err = rel_fro(got[e], ref[e])
-        assert err <= REL_FRO, (shape, steps, e, err)
+        assert err <= REL_FRO[steps], (shape, steps, e, err)
 
 
 def test_input_untouched_and_dropin_name(hip_device):
@@ -65,7 +71,7 @@ def test_input_untouched_and_dropin_name(hip_device):
     out = zeropower_via_newtonschulz5(G, 5)
     assert torch.equal(G, G0)  # the bf16 input is not overwritten
     assert out.dtype == torch.bfloat16 and out.shape == G.shape
-    assert rel_fro(out.float().cpu().numpy()[1], O.newton_schulz5(G.float().cpu().numpy(), 5)[1]) <= REL_FRO
+    assert rel_fro(out.float().cpu().numpy()[1], O.newton_schulz5(G.float().cpu().numpy(), 5)[1]) <= REL_FRO[5]
 
 
 def test_rejects_unaligned_sizes(hip_device):
@@ -90,7 +96,7 @@ def test_c3_expert_stack(hip_device, name, shape):
         g = G[e].cpu().numpy()
         got = out[e].float().cpu().numpy()
         ref = O.newton_schulz5(g[None], 5)[0]
-        assert rel_fro(got, ref) <= REL_FRO, (name, e, rel_fro(got, ref))
+        assert rel_fro(got, ref) <= REL_FRO[5], (name, e, rel_fro(got, ref))
         s_got = np.linalg.svd(got.astype(np.float64), compute_uv=False)
         S = np.linalg.svd(g.astype(np.float64), compute_uv=False)
         s = S / (np.linalg.norm(g.astype(np.float64)) + 1e-7)
