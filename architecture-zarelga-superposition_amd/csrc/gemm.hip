@@ -1,33 +1,38 @@
 // Grouped expert GEMMs for gfx950 (scattermoe/kernels/ops.py:122-255 and
-// :263-438, plus the fused SwiGLU forward/backward of scattermoe/mlp.py:96-102).
+// :263-438, plus the fused SwiGLU forward/backward of scattermoe/mlp.py:96-102),
+// the split-K dense weight grads of the shared expert and gate, and the grouped
+// GEMMs of the Newton-Schulz step (optimizer/muon.py:6-32).
 //
-// Two kernels share one tile machinery:
-//   * grouped_rows_kernel:  C[i, :] = A(i, :) @ B_e   for the sorted rows i of
-//     expert e (forward and input-grad GEMMs). Tiles never straddle experts: the
-//     M tiles of each expert are laid out back to back, so boundary rows cost at
-//     most one partial tile per expert instead of a K-loop per expert present.
-//   * grouped_wgrad_kernel: C_e[m, n] = sum_{i in e} DY[i, m] X(i)[n]  (weight grads).
+// Two GEMM shapes, each in a bf16 kernel (the fast path) and an f32 kernel:
+//   * rows: C[i, :] = A(i, :) @ B_e for the sorted rows i of expert e (forward and
+//     input-grad GEMMs; rows_bf16_kernel / grouped_rows_kernel). Tiles never
+//     straddle experts: the M tiles of each expert are laid out back to back, so
+//     boundary rows cost at most one partial tile per expert instead of a K loop
+//     per expert present in a block.
+//   * wgrad: C_e[m, n] = sum_{i in e} DY[i, m] X(i)[n] (weight grads;
+//     wgrad_bf16_kernel / grouped_wgrad_kernel), x rows optionally gathered.
 //
-// Tile machinery (256 threads = 4 waves in a 2x2 grid, BM x BN tile):
-//   * LDS holds both operands as [rows][128 bytes] with the reduction dimension
-//     contiguous (64 bf16 or 32 f32 per row), 16-byte chunks XOR-swizzled by
-//     ((row>>1) ^ (row>>3)) & 7 so that MFMA fragment reads and both store
-//     patterns are bank-conflict free. Two stages; the next tile's global loads
-//     are issued before the current tile's MFMAs and written to the other stage
-//     afterwards, one barrier per K step.
-//   * Operands whose reduction dimension is contiguous in HBM (x rows, nn.Linear
-//     weights) are copied chunk by chunk. Operands whose reduction dimension is
-//     strided (weights read transposed, and both wgrad operands) are loaded as
-//     VEC x VEC blocks and transposed in registers (v_perm_b32 for bf16).
-//   * bf16: v_mfma_f32_32x32x16_bf16; f32: 4 x v_mfma_f32_32x32x2f32 per chunk.
-//     The B tile is fed as the MFMA's first operand, so each lane ends up holding
-//     4 consecutive output columns of one output row.
-//   * Epilogue: accumulators go through LDS (rounded to the output type, as the
-//     reference stores its GEMM outputs) and leave as coalesced 16-byte stores
-//     to grouped or scattered rows, optionally through SwiGLU or its backward.
+// bf16 tile machinery (256 threads = 4 waves in a 2x2 grid, BM x BN = 256 x 256
+// or 128 x 128):
+//   * Operands go HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) in
+//     64-deep stages, double-buffered: 128-byte rows with the reduction dimension
+//     contiguous (16-byte chunks XOR-swizzled by row), or K-major tiles read with
+//     ds_read_b64_tr_b16 for operands whose reduction dimension is strided. Each
+//     stage has its own scalar buffer descriptor (the k advance and the tail
+//     clipping), so issuing a load costs no vector ALU.
+//   * v_mfma_f32_32x32x16_bf16 with the B tile as the first operand: each lane ends
+//     up holding 4 consecutive output columns of one output row. Every MFMA slot of
+//     the K loop is pinned with sched_barrier so loads, fragment reads and the one
+//     barrier per stage interleave with the MFMAs (kloop64).
+//   * Epilogue: each wave stages its block in LDS (rounded to the output type, as
+//     the reference stores its GEMM outputs) and writes full 128-byte lines to
+//     grouped or scattered rows, optionally through SwiGLU, its backward, or the
+//     Newton-Schulz terms.
 //   * Workgroup -> tile: XCD-aware. Workgroup b runs on XCD b % 8; each XCD takes
 //     a contiguous range of the (expert, m-tile, n-tile) sequence so that tiles
 //     sharing an expert's weights and rows run on one XCD and share its L2.
+// The f32 kernels use the same tiling with VGPR-staged loads, 32-deep stages and
+// v_mfma_f32_32x32x2f32 (four per 16-byte fragment).
 #include <cstdlib>
 
 #include "zmoe_internal.h"
