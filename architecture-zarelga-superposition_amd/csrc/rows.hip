@@ -28,6 +28,13 @@ inline RowMap row_map(int64_t nchunks) {
 }
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// Rows read exactly once (slot rows of Y / dXe, the addends, H in the SwiGLU passes):
+// non-temporal loads, so the stream does not evict lines that other rows still use
+// (measured: combine 0.267 -> 0.232 ms at C3).
+typedef unsigned v4u32_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16_stream(const void* p) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const v4u32_t*>(p)));
+}
 __device__ __forceinline__ void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
 
 template <typename T> struct V { static constexpr int N = 16 / sizeof(T); };
@@ -85,7 +92,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
   for (int64_t ch = lt; ch < nch; ch += tpr) {
     float acc[VN];
     if (add) {
-      unpack_chunk(ld16(add + t * d + ch * VN), acc, T{});
+      unpack_chunk(ld16_stream(add + t * d + ch * VN), acc, T{});
     } else {
 #pragma unroll
       for (int q = 0; q < VN; ++q) acc[q] = 0.f;
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
     if constexpr (KF > 0) {
       uint4 yv[KF];
 #pragma unroll
-      for (int j = 0; j < KF; ++j) yv[j] = ld16(Y + (t * KF + j) * d + ch * VN);
+      for (int j = 0; j < KF; ++j) yv[j] = ld16_stream(Y + (t * KF + j) * d + ch * VN);
 #pragma unroll
       for (int j = 0; j < KF; ++j) {
         const float w = g[t * KF + j];
@@ -109,7 +116,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
       for (int j = 0; j < k; ++j) {
         const float w = g[t * k + j];
         float y[VN];
-        unpack_chunk(ld16(Y + (t * k + j) * d + ch * VN), y, T{});
+        unpack_chunk(ld16_stream(Y + (t * k + j) * d + ch * VN), y, T{});
 #pragma unroll
         for (int q = 0; q < VN; ++q) part[q] = fmaf(w, y[q], part[q]);
       }
@@ -155,14 +162,14 @@ __global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
     for (int64_t ch = lt; ch < nch; ch += tpr) {
       float go[VN];
       if (drow_ok) {
-        unpack_chunk(ld16(dout + drow * d + ch * VN), go, T{});
+        unpack_chunk(ld16_stream(dout + drow * d + ch * VN), go, T{});
       } else {
 #pragma unroll
         for (int q = 0; q < VN; ++q) go[q] = 0.f;
       }
       uint4 yv[KM];
 #pragma unroll
-      for (int j = 0; j < KM; ++j) yv[j] = ld16(Y + (t * k + (j < k ? j : k - 1)) * d + ch * VN);
+      for (int j = 0; j < KM; ++j) yv[j] = ld16_stream(Y + (t * k + (j < k ? j : k - 1)) * d + ch * VN);
 #pragma unroll
       for (int j = 0; j < KM; ++j) {
         float y[VN], sv[VN];
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(kRowThreads) void sum_k_kernel(const T* __restrict_
     if constexpr (KF > 0) {
       uint4 xv[KF];
 #pragma unroll
-      for (int j = 0; j < KF; ++j) xv[j] = ld16(Xe + (t * KF + j) * d + ch * VN);
+      for (int j = 0; j < KF; ++j) xv[j] = ld16_stream(Xe + (t * KF + j) * d + ch * VN);
 #pragma unroll
       for (int j = 0; j < KF; ++j) {
         unpack_chunk(xv[j], x, T{});
@@ -223,18 +230,18 @@ __global__ __launch_bounds__(kRowThreads) void sum_k_kernel(const T* __restrict_
       }
     } else {
       for (int j = 0; j < k; ++j) {
-        unpack_chunk(ld16(Xe + (t * k + j) * d + ch * VN), x, T{});
+        unpack_chunk(ld16_stream(Xe + (t * k + j) * d + ch * VN), x, T{});
 #pragma unroll
         for (int q = 0; q < VN; ++q) acc[q] += x[q];
       }
     }
     if (a0) {
-      unpack_chunk(ld16(a0 + t * d + ch * VN), x, T{});
+      unpack_chunk(ld16_stream(a0 + t * d + ch * VN), x, T{});
 #pragma unroll
       for (int q = 0; q < VN; ++q) acc[q] += x[q];
     }
     if (a1) {
-      unpack_chunk(ld16(a1 + t * d + ch * VN), x, T{});
+      unpack_chunk(ld16_stream(a1 + t * d + ch * VN), x, T{});
 #pragma unroll
       for (int q = 0; q < VN; ++q) acc[q] += x[q];
     }
@@ -270,8 +277,8 @@ __global__ __launch_bounds__(kRowThreads) void swiglu_kernel(const T* __restrict
   if (i >= R * nch) return;
   const int64_t r = i / nch, ch = i % nch;
   float h[VN], g[VN], a[VN];
-  unpack_chunk(ld16(H + r * 2 * f + ch * VN), h, T{});
-  unpack_chunk(ld16(H + r * 2 * f + f + ch * VN), g, T{});
+  unpack_chunk(ld16_stream(H + r * 2 * f + ch * VN), h, T{});
+  unpack_chunk(ld16_stream(H + r * 2 * f + f + ch * VN), g, T{});
 #pragma unroll
   for (int q = 0; q < VN; ++q) a[q] = silu_f(g[q]) * h[q];
   st16(A + r * f + ch * VN, pack_chunk(a, T{}));
@@ -287,9 +294,9 @@ __global__ __launch_bounds__(kRowThreads) void swiglu_backward_kernel(const T* _
   if (i >= R * nch) return;
   const int64_t r = i / nch, ch = i % nch;
   float h[VN], g[VN], da[VN], dh[VN], dg[VN];
-  unpack_chunk(ld16(H + r * 2 * f + ch * VN), h, T{});
-  unpack_chunk(ld16(H + r * 2 * f + f + ch * VN), g, T{});
-  unpack_chunk(ld16(dA + r * f + ch * VN), da, T{});
+  unpack_chunk(ld16_stream(H + r * 2 * f + ch * VN), h, T{});
+  unpack_chunk(ld16_stream(H + r * 2 * f + f + ch * VN), g, T{});
+  unpack_chunk(ld16_stream(dA + r * f + ch * VN), da, T{});
 #pragma unroll
   for (int q = 0; q < VN; ++q) {
     const float s = sigmoid_fast(g[q]);
