@@ -1451,7 +1451,9 @@ __device__ __forceinline__ void wgrad_epilogue_f32(const WgradParams& p, const f
   }
 }
 
-template <int BM, int BN, bool GATHER, bool OUT_F32 = false>
+// GATHER: 0 = x rows in sorted order; 1 = gathered, row = index >> shift; 2 = gathered,
+// row = index / x_div. Both gathered forms keep the K loop free of branches.
+template <int BM, int BN, int GATHER, bool OUT_F32 = false>
 __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
   constexpr int KS = 64;
@@ -1499,14 +1501,15 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
     const int pos = kt * KS + 16 * wu + (int)(threadIdx.x & 15);
     return xr32[2 * (r_begin + (pos < nrows ? pos : nrows - 1))];
   };
+  // stage kt's indices (in pend) -> src_off, and the next stage's load issued; stages at or
+  // past nk get kOOBRow everywhere and re-read the last valid index (no branch in the loop)
   auto fetch_src = [&](int kt) {
-    if (kt == 0) pend = issue_idx(0);
     const int base = kt * KS + 16 * wu;
     uint32_t v[16];  // gather indices are below 2^31 (R < 2^31)
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = (uint32_t)__builtin_amdgcn_readlane((int)pend, j);
-    if (kt + 1 < nk) pend = issue_idx(kt + 1);
-    if (p.x_div_shift >= 0) {
+    pend = issue_idx(kt + 1);
+    if constexpr (GATHER == 1) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) v[j] >>= p.x_div_shift;
     } else {
@@ -1525,7 +1528,7 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
       const int64_t pitch = p.lddy * 2;
       la.issue(q, stage_rsrc(dy_base, p.dy_bytes, (r_begin + k0) * pitch, ((int64_t)nrows - k0) * pitch, on), sa,
                wu);
-    } else if constexpr (GATHER) {
+    } else if constexpr (GATHER != 0) {
       const int qq = q - LA::NQ;
       // this lane's k-row is qq * RPI + sub of the wave's 16; qq is a compile-time
       // constant here (unrolled), so the pick indexes the array with constants only
@@ -1559,8 +1562,11 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
 #pragma unroll
       for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
 
+  if constexpr (GATHER != 0) {
+    if (nk > 0) pend = issue_idx(0);
+  }
   kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, [&](int kt) {
-    if (GATHER && kt < nk) fetch_src(kt);
+    if constexpr (GATHER != 0) fetch_src(kt);
   }, [] {});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
   if constexpr (OUT_F32)
@@ -1936,16 +1942,19 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   int rc;
   if (dtype == ZMOE_DTYPE_BF16) {
     const bool big = use_big_tiles(M, E, N) && K >= 256;
-    if (big && p.x_rows)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, true>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+    const int gather = p.x_rows ? (p.x_div_shift >= 0 ? 1 : 2) : 0;
+    if (big && gather == 1)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 1>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+    else if (big && gather == 2)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 2>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
     else if (big)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, false>, bf16_lds_bytes<256, 256>(), 256, 256, p,
-                               s);
-    else if (p.x_rows)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 0>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+    else if (gather == 1)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
+    else if (gather == 2)
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
     else
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, false>, bf16_lds_bytes<128, 128>(), 128, 128, p,
-                               s);
+      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
   } else {
     rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
                              s);
@@ -2009,9 +2018,9 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
   p.dy_bytes = (uint32_t)dy_span;
   p.x_bytes = (uint32_t)x_span;
   if (use_big_tiles(M, S, N) && K >= 256)
-    rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, false, true>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+    rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 0, true>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
   else
-    rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, false, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
+    rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
   if (rc) return rc;
   const int64_t n = N * K;  // multiple of 8
   hipLaunchKernelGGL(reduce_splits_kernel<uint16_t>, dim3((unsigned)cdiv(n / 4, 256)), dim3(256), 0, s,

@@ -19,6 +19,8 @@ SHAPES = [
     (1500, 256, 256, 16, 4, 1.5),   # skewed: some experts empty
     (64, 128, 64, 32, 8, 0.0),      # few rows per expert
     (3, 64, 32, 8, 2, 0.0),         # tiny
+    (1024, 256, 512, 8, 6, 0.0),    # k = 6: gathered rows divided by a non-power of two (256 tiles)
+    (600, 128, 128, 12, 3, 0.5),    # k = 3 with 128 tiles
 ]
 
 
