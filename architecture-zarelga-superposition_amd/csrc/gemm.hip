@@ -212,6 +212,7 @@ struct TransOperand {
 };
 
 // ------------------------------------------------------------------ block scan
+template <int NT = kGemmThreads>
 __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
@@ -224,7 +225,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
   __syncthreads();
   int base = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < kGemmThreads / 64; ++w) {
+  for (int w = 0; w < NT / 64; ++w) {
     const int t = tmp[w];
     if (w < wave) base += t;
     tot += t;
@@ -234,9 +235,9 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
 }
 
 // tstart[e] = first m-tile of expert e (tiles of BM rows, back to back); tstart[E] = total.
-template <int BM>
+template <int BM, int NT = kGemmThreads>
 __device__ int build_tile_starts(const int64_t* __restrict__ off, int E, int* tstart, int* tmp) {
-  const int ept = (E + kGemmThreads - 1) / kGemmThreads;  // <= 4
+  const int ept = (E + NT - 1) / NT;  // <= 4
   const int e0 = threadIdx.x * ept;
   int nt[4] = {0, 0, 0, 0};
   int local = 0;
@@ -252,7 +253,7 @@ __device__ int build_tile_starts(const int64_t* __restrict__ off, int E, int* ts
     }
   }
   int total;
-  int run = block_exclusive_scan(local, tmp, &total);
+  int run = block_exclusive_scan<NT>(local, tmp, &total);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = e0 + q;
@@ -323,7 +324,7 @@ struct RowsTile {
 };
 
 // Map this workgroup to (expert, m-tile, n-tile) of a rows launch; false if it has no tile.
-template <int BM>
+template <int BM, int NT = kGemmThreads>
 __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem, RowsTile& t) {
   if (p.ns_sym_m > 0) {
     // m x m outputs, one per expert: the upper-triangle tiles (nt >= mt) in row order
@@ -345,7 +346,7 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
   }
   int* tstart = reinterpret_cast<int*>(smem);
   int* tmp = tstart + kGemmMaxE + 4;
-  const int mtiles = build_tile_starts<BM>(p.offsets, p.E, tstart, tmp);
+  const int mtiles = build_tile_starts<BM, NT>(p.offsets, p.E, tstart, tmp);
   const int logical = xcd_logical_tile(mtiles * p.n_tiles);
   if (logical < 0) return false;
   const int mt = logical / p.n_tiles;
@@ -732,12 +733,15 @@ typedef __attribute__((address_space(3))) uint4 lds_uint4;
 
 constexpr uint32_t kOOB = 0x80000000u;  // any offset >= num_records reads zero
 
+
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 __device__ __forceinline__ void buf_to_lds(__amdgpu_buffer_rsrc_t r, lds_char* dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
 }
+
 
 // s_waitcnt immediate that waits until at most n vector-memory ops are outstanding.
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -746,12 +750,12 @@ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 // chunks XOR-swizzled by row so MFMA fragment reads are bank-conflict free.
 template <int KS>
 __device__ __forceinline__ uint32_t nt_off(int row, int chunk) {
-  if constexpr (KS == 64) return (uint32_t)(row * 128 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 7)) << 4));
+  if constexpr (KS == 64) return (uint32_t)(row * 128 + ((chunk ^ ((row & 7) ^ ((row >> 3) & 1))) << 4));
   else return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
 }
 template <int KS>
 __device__ __forceinline__ int nt_swz(int row) {
-  if constexpr (KS == 64) return ((row >> 1) ^ (row >> 3)) & 7;
+  if constexpr (KS == 64) return (row & 7) ^ ((row >> 3) & 1);
   else return (row >> 2) & 3;
 }
 
@@ -846,6 +850,8 @@ struct Frag {
 // takes physical chunk i % 8 of its row, i.e. logical chunk (i % 8) ^ swizzle(row).
 // Offsets are relative to the stage's buffer resource (based at k0), so issuing a
 // load costs no vector ALU work: the per-stage advance lives in the scalar resource.
+// The load slot of a wave is its index mod 4 (in the 8-wave kernels waves w and w + 4
+// share slot w and split its loads).
 template <int ROWS>
 struct RowLoad {
   static constexpr int NQ = ROWS / 32;  // instructions per wave per stage
@@ -853,7 +859,7 @@ struct RowLoad {
   uint32_t tail[NQ];                    // the same for the final partial stage (chunks past K: kOOB)
 
   __device__ __forceinline__ static int row_of(int q) {
-    return 8 * ((int)(threadIdx.x >> 6) * NQ + q) + (int)((threadIdx.x & 63) >> 3);
+    return 8 * ((int)((threadIdx.x >> 6) & 3) * NQ + q) + (int)((threadIdx.x & 63) >> 3);
   }
   __device__ __forceinline__ static int chunk_of(int q) { return (int)(threadIdx.x & 7) ^ nt_swz<64>(row_of(q)); }
   // row_off: byte offset of the row at k = 0, or kOOB; ktail = K % 64 (0: no partial stage)
@@ -862,13 +868,16 @@ struct RowLoad {
     off[q] = row_off == kOOB ? kOOB : row_off + 16u * (uint32_t)c;
     tail[q] = (ktail == 0 || 8 * c < ktail) ? off[q] : kOOB;
   }
+  // (a select between the two array elements would be turned back into a dynamically
+  // indexed array in scratch memory; the masked XOR keeps both indices constant)
   __device__ __forceinline__ void issue(int q, __amdgpu_buffer_rsrc_t rs, lds_char* stage, int wu, bool last) const {
-    buf_to_lds(rs, stage + (wu * NQ + q) * 1024, last ? tail[q] : off[q]);
+    const uint32_t m = 0u - (uint32_t)last;
+    buf_to_lds(rs, stage + (wu * NQ + q) * 1024, off[q] ^ ((off[q] ^ tail[q]) & m));
   }
 };
 
 // K-major tile loader: [64 k-rows][COLS] per stage, COLS contiguous in HBM. Each
-// wave instruction fills 1 KB = RPI k-rows; wave w covers k-rows 16 w .. 16 w + 15.
+// wave instruction fills 1 KB = RPI k-rows; load slot w covers k-rows 16 w .. 16 w + 15.
 template <int COLS>
 struct KLoad {
   static constexpr int CPR = COLS / 8;       // chunks per k-row
@@ -879,14 +888,14 @@ struct KLoad {
   uint32_t voff[NQ];  // coff + (k-row within the stage) * row pitch, or kOOB
 
   __device__ __forceinline__ static int krow_of(int q) {
-    return (((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63)) / CPR;
+    return (((int)((threadIdx.x >> 6) & 3) * NQ + q) * 64 + (int)(threadIdx.x & 63)) / CPR;
   }
   // k-row of this lane within its wave's 16 for instruction q: q * RPI + sub()
   __device__ __forceinline__ static int sub() { return (int)(threadIdx.x & 63) / CPR; }
   __device__ __forceinline__ void init(int mn0, int ncols, int64_t pitch_bytes) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const int f = ((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63);
+      const int f = ((int)((threadIdx.x >> 6) & 3) * NQ + q) * 64 + (int)(threadIdx.x & 63);
       const int kr = f / CPR;
       const int c = (f % CPR) ^ ((kr & 3) << 2);
       const int col = mn0 + 8 * c;
@@ -927,10 +936,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const char* base, u
 // dma(q, buf, kt, on) issues load instruction q (0..LPS-1) of stage kt into buffer
 // buf (reading zeros when !on); prefetch(kt) readies the gather indices of stage kt;
 // after_prologue_loads() runs once the first loads are in flight.
-template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch,
-          typename Hook>
-__device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI], Dma dma,
-                                        Prefetch prefetch, Hook after_prologue_loads) {
+template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, int NW, int GRP, typename Dma,
+          typename Prefetch, typename Hook>
+__device__ __forceinline__ void kloop64_group(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI],
+                                              Dma dma_slot, Prefetch prefetch, Hook after_prologue_loads) {
   constexpr int KS = 64;
   constexpr int kStage = (BM + BN) * KS * 2;
   constexpr int AR = Frag<A_T>::kReads, BR = Frag<B_T>::kReads;
@@ -938,9 +947,16 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
   constexpr int NMMA = MI * NI;                   // MFMAs per step
   constexpr int RPS = (NREAD + NMMA - 1) / NMMA;  // reads per MFMA slot
   constexpr int WIN = 2 * NMMA;                   // load window: step 3 + step 0
-  // load j goes to window slot j * WIN / LPS (evenly spread); loads in slots < NMMA
+  // With 8 waves, waves w and w + 4 split the LPS loads of load slot w & 3.
+  constexpr int LPW = LPS / (NW / 4);             // loads per wave per stage
+  static_assert(LPW * (NW / 4) == LPS, "loads split evenly");
+  // load j goes to window slot j * WIN / LPW (evenly spread); loads in slots < NMMA
   // belong to step 3 of the previous stage
-  constexpr int kEarly = (NMMA * LPS + WIN - 1) / WIN;  // loads j with j * WIN / LPS < NMMA
+  constexpr int kEarly = (NMMA * LPW + WIN - 1) / WIN;  // loads j with j * WIN / LPW < NMMA
+  // wave group GRP (waves 4 GRP .. 4 GRP + 3) issues loads [GRP LPW, (GRP + 1) LPW) of its slot
+  auto dma = [&](int j, int buf, int kt, bool on) __attribute__((always_inline)) {
+    dma_slot(j + GRP * LPW, buf, kt, on);
+  };
   Frag<A_T> fa[2][MI];
   Frag<B_T> fb[2][NI];
   auto read_piece = [&](int buf, const lds_char* st, int s, int i) {
@@ -969,8 +985,8 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
     for (int i = 0; i < NMMA; ++i) {
       mma(cur, i);
 #pragma unroll
-      for (int j = 0; j < LPS; ++j)
-        if (w0 >= 0 && j * WIN / LPS == w0 + i) dma(j, lbuf, lkt, lon);
+      for (int j = 0; j < LPW; ++j)
+        if (w0 >= 0 && j * WIN / LPW == w0 + i) dma(j, lbuf, lkt, lon);
 #pragma unroll
       for (int r = 0; r < RPS; ++r)
         if (i * RPS + r < NREAD) read_piece(cur ^ 1, rst, rs, i * RPS + r);
@@ -985,7 +1001,7 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
   }
   prefetch(0);
 #pragma unroll
-  for (int j = 0; j < LPS; ++j) dma(j, 0, 0, true);
+  for (int j = 0; j < LPW; ++j) dma(j, 0, 0, true);
   prefetch(1);
 #pragma unroll
   for (int j = 0; j < kEarly; ++j) dma(j, 1, 1, nk > 1);
@@ -1012,6 +1028,22 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
   __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
 }
 
+// kloop64 for 4 waves, or for 8 waves (two per SIMD, output blocks of 128 x 64 per wave):
+// each wave group runs its own instance, so every load index stays a compile-time
+// constant (a runtime group offset would turn the loaders' offset arrays into
+// dynamically indexed scratch memory).
+template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, int NW, typename Dma, typename Prefetch,
+          typename Hook>
+__device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI], Dma dma_slot,
+                                        Prefetch prefetch, Hook after_prologue_loads) {
+  if (NW == 8 && __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= 4)
+    kloop64_group<LPS, MI, NI, A_T, B_T, BM, BN, NW, 1>(nk, lds, wm0, wn0, acc, dma_slot, prefetch,
+                                                        after_prologue_loads);
+  else
+    kloop64_group<LPS, MI, NI, A_T, B_T, BM, BN, NW, 0>(nk, lds, wm0, wn0, acc, dma_slot, prefetch,
+                                                        after_prologue_loads);
+}
+
 // Epilogues: each wave stages its own WM x WN accumulator block in its own LDS area
 // (bf16, rows of WN * 2 + 16 bytes) and writes it out row-contiguously, 16 bytes
 // per lane, so every store instruction covers whole 128-byte lines. The MFMA layout
@@ -1025,6 +1057,9 @@ struct WaveStage {
   static constexpr int PITCH = WN * 2 + 16;  // bytes per staged row
   static constexpr int CPR = WN / 8;          // 16-byte chunks per row
 };
+
+// GEMM output stores (16 bytes per lane; non-temporal stores measured no faster)
+__device__ __forceinline__ void st_out(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
 
 __device__ __forceinline__ uint2 pack4_bf16(const float (&v)[4]) {
   return make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -1120,9 +1155,9 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
 #pragma unroll
             for (int q = 0; q < VEC; ++q) a[q] = silu_f(gt[q]) * h[q];
             const int64_t o = orow[u];
-            *reinterpret_cast<uint4*>(C + o * p.ldc + jj) = hv[u];
-            *reinterpret_cast<uint4*>(C + o * p.ldc + p.half + jj) = gv[u];
-            *reinterpret_cast<uint4*>(A2 + o * p.ldc2 + jj) = pack_chunk(a, uint16_t{});
+            st_out(C + o * p.ldc + jj, hv[u]);
+            st_out(C + o * p.ldc + p.half + jj, gv[u]);
+            st_out(A2 + o * p.ldc2 + jj, pack_chunk(a, uint16_t{}));
           }
         }
       }
@@ -1176,7 +1211,7 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
       const int col = ncol0 + item_cc(i, u) * VEC;
       const int64_t o = orow[u];
       if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_BIAS) {
-        *reinterpret_cast<uint4*>(C + o * p.ldc + col) = tv[u];
+        st_out(C + o * p.ldc + col, tv[u]);
       } else if constexpr (EPI == EPI_NS) {
         // out = t + bf16(beta * D) and out2 = bf16(gamma * t) with t = bf16(acc): the rounding
         // points of bf16 tensor arithmetic in muon.py:24-27 (each product and sum rounded)
@@ -1187,7 +1222,7 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
           float q[VEC];
 #pragma unroll
           for (int v = 0; v < VEC; ++v) q[v] = p.ns_gamma * t[v];
-          *reinterpret_cast<uint4*>(C2 + o * p.ldc2 + col) = pack_chunk(q, uint16_t{});
+          st_out(C2 + o * p.ldc2 + col, pack_chunk(q, uint16_t{}));
         }
         uint4 ov = tv[u];
         if (has_g) {
@@ -1197,7 +1232,7 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
           for (int v = 0; v < VEC; ++v) r[v] = t[v] + to_f32(bf16_bits(p.ns_beta * d[v]));
           ov = pack_chunk(r, uint16_t{});
         }
-        *reinterpret_cast<uint4*>(C + o * p.ldc + col) = ov;
+        st_out(C + o * p.ldc + col, ov);
       } else {  // EPI_SWIGLU_BWD: staged dA (bf16, as the unfused path stores it), H rows in sorted order
         float da[VEC], h[VEC], gt[VEC], dh[VEC], dg[VEC];
         unpack_chunk(tv[u], da, uint16_t{});
@@ -1209,8 +1244,8 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
           dh[v] = da[v] * gt[v] * sg;
           dg[v] = da[v] * h[v] * sg * (1.f + gt[v] * (1.f - sg));
         }
-        *reinterpret_cast<uint4*>(C + o * p.ldc + col) = pack_chunk(dh, uint16_t{});
-        *reinterpret_cast<uint4*>(C + o * p.ldc + p.half + col) = pack_chunk(dg, uint16_t{});
+        st_out(C + o * p.ldc + col, pack_chunk(dh, uint16_t{}));
+        st_out(C + o * p.ldc + p.half + col, pack_chunk(dg, uint16_t{}));
       }
     }
   }
@@ -1265,7 +1300,7 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
             float q[VEC];
 #pragma unroll
             for (int v = 0; v < VEC; ++v) q[v] = p.ns_gamma * t[v];
-            *reinterpret_cast<uint4*>(C2 + o * p.ldc2 + col) = pack_chunk(q, uint16_t{});
+            st_out(C2 + o * p.ldc2 + col, pack_chunk(q, uint16_t{}));
           }
           uint4 ov = tv[u];
           if (D != nullptr) {
@@ -1275,7 +1310,7 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
             for (int v = 0; v < VEC; ++v) r[v] = t[v] + to_f32(bf16_bits(p.ns_beta * d[v]));
             ov = pack_chunk(r, uint16_t{});
           }
-          *reinterpret_cast<uint4*>(C + o * p.ldc + col) = ov;
+          st_out(C + o * p.ldc + col, ov);
         }
       }
     }
@@ -1304,36 +1339,48 @@ __device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* 
     for (int u = 0; u < B; ++u) {
       const int idx = lane + 64 * (i0 + u);
       const int m = m0 + wm0 + idx / S::CPR, n = n0 + wn0 + (idx % S::CPR) * 8;
-      if (m < p.Ndy && n < p.Kx) *reinterpret_cast<uint4*>(DW + (int64_t)m * p.Kx + n) = v[u];
+      if (m < p.Ndy && n < p.Kx) st_out(DW + (int64_t)m * p.Kx + n, v[u]);
     }
   }
 }
 
+// Wave layout of the bf16 kernels: NW = 4 waves in a 2 x 2 grid (kloop64), or NW = 8
+// in a 2 x 4 grid whose waves w and w + 4 share a SIMD (kloop64 with NW = 8).
+template <int BM, int BN, int NW>
+struct WaveGrid {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  static constexpr int WM = BM / 2, WN = BN / (NW / 2);
+  static constexpr int MI = WM / 32, NI = WN / 32;
+  __device__ __forceinline__ static int wm0(int wave) { return (wave / (NW / 2)) * WM; }
+  __device__ __forceinline__ static int wn0(int wave) { return (wave % (NW / 2)) * WN; }
+};
+
 // LDS of the bf16 kernels: two operand stages, reused by the wave staging areas
 // after the K loop, then the rows kernel's output-row table.
-template <int BM, int BN>
+template <int BM, int BN, int NW = 4>
 constexpr int bf16_stage_bytes() {
   constexpr int loop = 2 * (BM + BN) * 64 * 2;
-  constexpr int epi = 4 * (BM / 2) * WaveStage<BN / 2>::PITCH;
+  constexpr int epi = NW * WaveGrid<BM, BN, NW>::WM * WaveStage<WaveGrid<BM, BN, NW>::WN>::PITCH;
   return loop > epi ? loop : epi;
 }
 
-template <int BM, int BN, bool B_T, int EPI>
-__global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
+template <int BM, int BN, bool B_T, int EPI, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
   extern __shared__ __align__(16) char smem[];
   constexpr int KS = 64;
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int MI = WM / 32, NI = WN / 32;
+  using WG = WaveGrid<BM, BN, NW>;
+  constexpr int WN = WG::WN;
+  constexpr int MI = WG::MI, NI = WG::NI;
   constexpr int kStage = (BM + BN) * KS * 2;
   static_assert(EPI != EPI_SWIGLU || WN % 64 == 0, "SwiGLU pairs 32-column blocks inside a wave");
 
   RowsTile tile;
-  if (!decode_rows_tile<BM>(p, smem, tile)) return;  // uniform per workgroup
+  if (!decode_rows_tile<BM, NW * 64>(p, smem, tile)) return;  // uniform per workgroup
   const int e = __builtin_amdgcn_readfirstlane(tile.e);
   const int nt = __builtin_amdgcn_readfirstlane(tile.nt);
   const int rows = tile.rows;
   const int64_t row0 = tile.row0;
-  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int wu = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));  // load slot
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
   const int ktail = p.K % KS;
   const int nk = (p.K + KS - 1) / KS;
@@ -1399,7 +1446,7 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   };
 
   const int wave = threadIdx.x >> 6;
-  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
   f32x16_t acc[MI][NI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
@@ -1411,16 +1458,19 @@ __global__ __launch_bounds__(kGemmThreads) void rows_bf16_kernel(RowsParams p) {
   // The tile's output rows go to an LDS table above the operand stages: the index
   // loads are issued before the first operand loads and stored once those are in
   // flight, so their latency hides behind the first stage (row numbers < 2^31).
-  int* row_table = reinterpret_cast<int*>(smem + bf16_stage_bytes<BM, BN>());
+  // (With 8 waves, the table is written by waves 0-3, which run the loads.)
+  static_assert(BM <= 256, "row table written by the first 256 threads");
+  int* row_table = reinterpret_cast<int*>(smem + bf16_stage_bytes<BM, BN, NW>());
   int orow_v = 0;
   if (threadIdx.x < BM) {
     const int rl = (int)threadIdx.x;
     const int64_t i = row0 + (rl < rows ? rl : 0);
     orow_v = p.c_rows ? reinterpret_cast<const int*>(p.c_rows)[2 * i] : (int)i;
   }
-  kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, [&] {
+  auto hook = [&] {
     if (threadIdx.x < BM) row_table[threadIdx.x] = orow_v;
-  });
+  };
+  kloop64<LPS, MI, NI, false, B_T, BM, BN, NW>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
   // every wave is done with the operand stages (and has written its row-table entries)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,
@@ -1453,12 +1503,13 @@ __device__ __forceinline__ void wgrad_epilogue_f32(const WgradParams& p, const f
 
 // GATHER: 0 = x rows in sorted order; 1 = gathered, row = index >> shift; 2 = gathered,
 // row = index / x_div. Both gathered forms keep the K loop free of branches.
-template <int BM, int BN, int GATHER, bool OUT_F32 = false>
-__global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p) {
+template <int BM, int BN, int GATHER, bool OUT_F32 = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
   constexpr int KS = 64;
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int MI = WM / 32, NI = WN / 32;
+  using WG = WaveGrid<BM, BN, NW>;
+  constexpr int WN = WG::WN;
+  constexpr int MI = WG::MI, NI = WG::NI;
   constexpr int kStage = (BM + BN) * KS * 2;
 
   const int per_e = p.m_tiles * p.n_tiles;
@@ -1471,7 +1522,7 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
   const int64_t r_end = p.offsets[e];
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   const int m0 = mt * BM, n0 = nt * BN;
-  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int wu = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));  // load slot
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
   const int nk = (nrows + KS - 1) / KS;
 
@@ -1553,7 +1604,7 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
   };
 
   const int wave = threadIdx.x >> 6;
-  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
   f32x16_t acc[MI][NI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
@@ -1565,9 +1616,10 @@ __global__ __launch_bounds__(kGemmThreads) void wgrad_bf16_kernel(WgradParams p)
   if constexpr (GATHER != 0) {
     if (nk > 0) pend = issue_idx(0);
   }
-  kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, [&](int kt) {
+  auto prefetch = [&](int kt) {
     if constexpr (GATHER != 0) fetch_src(kt);
-  }, [] {});
+  };
+  kloop64<LPS, MI, NI, true, true, BM, BN, NW>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
   if constexpr (OUT_F32)
     wgrad_epilogue_f32(p, acc, e, m0, n0, wm0, wn0);
@@ -1618,9 +1670,9 @@ constexpr int rows_lds_bytes() {
 
 // bf16 kernels: two 64-deep operand stages (+ the rows kernel's output-row table);
 // the epilogue works from registers.
-template <int BM, int BN>
+template <int BM, int BN, int NW = 4>
 constexpr int bf16_lds_bytes() {
-  constexpr int main_loop = bf16_stage_bytes<BM, BN>() + BM * 4;  // stages / staging + output-row table
+  constexpr int main_loop = bf16_stage_bytes<BM, BN, NW>() + BM * 4;  // stages / staging + output-row table
   constexpr int decode = (kGemmMaxE + 4 + 8) * 4;
   return main_loop > decode ? main_loop : decode;
 }
@@ -1638,14 +1690,15 @@ int prepare(K kernel, int lds_bytes) {
 }
 
 template <typename K>
-int launch_rows_kernel(K kern, int lds, int BM, const RowsParams& p, int64_t R, hipStream_t s) {
+int launch_rows_kernel(K kern, int lds, int BM, const RowsParams& p, int64_t R, hipStream_t s,
+                       int threads = kGemmThreads) {
   int rc = prepare(kern, lds);
   if (rc) return rc;
   const int64_t mt_bound = cdiv(R, BM) + (R < p.E ? R : p.E);
   int64_t total = mt_bound * p.n_tiles;
   total = cdiv(total, kXcds) * kXcds;
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "grouped gemm: too many tiles");
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(kGemmThreads), lds, s, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads), lds, s, p);
   return check_launch("grouped rows kernel");
 }
 
@@ -1655,13 +1708,17 @@ int launch_rows_f32(const RowsParams& p, int64_t R, hipStream_t s) {
                             R, s);
 }
 
+// 256 x 256 tiles run with 8 waves (two per SIMD: while one wave is held issuing its
+// LDS-DMA loads, the other issues MFMAs), 128 x 128 tiles with 4.
 template <int BM, int BN, bool B_KN, int EPI>
 int launch_rows_bf16(const RowsParams& p, int64_t R, hipStream_t s) {
-  return launch_rows_kernel(rows_bf16_kernel<BM, BN, B_KN, EPI>, bf16_lds_bytes<BM, BN>(), BM, p, R, s);
+  constexpr int NW = BM == 256 ? 8 : 4;
+  return launch_rows_kernel(rows_bf16_kernel<BM, BN, B_KN, EPI, NW>, bf16_lds_bytes<BM, BN, NW>(), BM, p, R, s,
+                            NW * 64);
 }
 
 template <typename K>
-int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStream_t s) {
+int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStream_t s, int threads = kGemmThreads) {
   int rc = prepare(kern, lds);
   if (rc) return rc;
   p.m_tiles = (int)cdiv(p.Ndy, BM);
@@ -1669,8 +1726,14 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   int64_t total = (int64_t)p.E * p.m_tiles * p.n_tiles;
   total = cdiv(total, kXcds) * kXcds;
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(kGemmThreads), lds, s, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads), lds, s, p);
   return check_launch("grouped wgrad kernel");
+}
+
+template <int GATHER, bool OUT_F32>
+int launch_wgrad_big(const WgradParams& p, hipStream_t s) {
+  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, 8>, bf16_lds_bytes<256, 256, 8>(), 256, 256,
+                             p, s, 512);
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
@@ -1944,11 +2007,11 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
     const bool big = use_big_tiles(M, E, N) && K >= 256;
     const int gather = p.x_rows ? (p.x_div_shift >= 0 ? 1 : 2) : 0;
     if (big && gather == 1)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 1>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+      rc = launch_wgrad_big<1, false>(p, s);
     else if (big && gather == 2)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 2>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+      rc = launch_wgrad_big<2, false>(p, s);
     else if (big)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 0>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+      rc = launch_wgrad_big<0, false>(p, s);
     else if (gather == 1)
       rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
     else if (gather == 2)
@@ -2018,7 +2081,7 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
   p.dy_bytes = (uint32_t)dy_span;
   p.x_bytes = (uint32_t)x_span;
   if (use_big_tiles(M, S, N) && K >= 256)
-    rc = launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, 0, true>, bf16_lds_bytes<256, 256>(), 256, 256, p, s);
+    rc = launch_wgrad_big<0, true>(p, s);
   else
     rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
   if (rc) return rc;
