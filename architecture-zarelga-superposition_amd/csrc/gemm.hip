@@ -12,11 +12,12 @@
 //   * wgrad: C_e[m, n] = sum_{i in e} DY[i, m] X(i)[n] (weight grads;
 //     wgrad_bf16_kernel / grouped_wgrad_kernel), x rows optionally gathered.
 //
-// bf16 tile machinery (256 threads = 4 waves in a 2x2 grid, BM x BN = 256 x 256
-// or 128 x 128):
+// bf16 tile machinery (BM x BN = 256 x 256 on 8 waves in a 2x4 grid, two waves per
+// SIMD and 128 x 64 outputs per wave; or 128 x 128 on 4 waves in a 2x2 grid):
 //   * Operands go HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) in
-//     64-deep stages, double-buffered: 128-byte rows with the reduction dimension
-//     contiguous (16-byte chunks XOR-swizzled by row), or K-major tiles read with
+//     64-deep stages, double-buffered, every wave loading its own share: 128-byte
+//     rows with the reduction dimension contiguous (16-byte chunks XOR-swizzled by
+//     row so that each 8- or 16-lane group of a fragment read hits distinct banks), or K-major tiles read with
 //     ds_read_b64_tr_b16 for operands whose reduction dimension is strided. Each
 //     stage has its own scalar buffer descriptor (the k advance and the tail
 //     clipping), so issuing a load costs no vector ALU.
@@ -850,16 +851,16 @@ struct Frag {
 // takes physical chunk i % 8 of its row, i.e. logical chunk (i % 8) ^ swizzle(row).
 // Offsets are relative to the stage's buffer resource (based at k0), so issuing a
 // load costs no vector ALU work: the per-stage advance lives in the scalar resource.
-// The load slot of a wave is its index mod 4 (in the 8-wave kernels waves w and w + 4
-// share slot w and split its loads).
-template <int ROWS>
+// Each of the NS waves loads its own 8 NQ rows.
+template <int ROWS, int NS = 4>
 struct RowLoad {
-  static constexpr int NQ = ROWS / 32;  // instructions per wave per stage
-  uint32_t off[NQ];                     // byte offset of this lane's chunk at k0 = 0, or kOOB
-  uint32_t tail[NQ];                    // the same for the final partial stage (chunks past K: kOOB)
+  static constexpr int NQ = ROWS / (8 * NS);  // instructions per wave per stage
+  static_assert(NQ >= 1, "at least one load per wave");
+  uint32_t off[NQ];                           // byte offset of this lane's chunk at k0 = 0, or kOOB
+  uint32_t tail[NQ];                          // the same for the final partial stage (chunks past K: kOOB)
 
   __device__ __forceinline__ static int row_of(int q) {
-    return 8 * ((int)((threadIdx.x >> 6) & 3) * NQ + q) + (int)((threadIdx.x & 63) >> 3);
+    return 8 * ((int)(threadIdx.x >> 6) * NQ + q) + (int)((threadIdx.x & 63) >> 3);
   }
   __device__ __forceinline__ static int chunk_of(int q) { return (int)(threadIdx.x & 7) ^ nt_swz<64>(row_of(q)); }
   // row_off: byte offset of the row at k = 0, or kOOB; ktail = K % 64 (0: no partial stage)
@@ -877,25 +878,26 @@ struct RowLoad {
 };
 
 // K-major tile loader: [64 k-rows][COLS] per stage, COLS contiguous in HBM. Each
-// wave instruction fills 1 KB = RPI k-rows; load slot w covers k-rows 16 w .. 16 w + 15.
-template <int COLS>
+// wave instruction fills 1 KB = RPI k-rows; wave w of NS covers k-rows KR w .. KR w + KR - 1.
+template <int COLS, int NS = 4>
 struct KLoad {
-  static constexpr int CPR = COLS / 8;       // chunks per k-row
-  static constexpr int NQ = 64 * CPR / 256;  // instructions per wave per stage
-  static constexpr int RPI = 64 / CPR;       // k-rows per instruction
-  static_assert(NQ * RPI == 16, "16 k-rows per wave per stage");
+  static constexpr int CPR = COLS / 8;   // chunks per k-row
+  static constexpr int NQ = CPR / NS;    // instructions per wave per stage
+  static constexpr int RPI = 64 / CPR;   // k-rows per instruction
+  static constexpr int KR = 64 / NS;     // k-rows per wave per stage
+  static_assert(NQ >= 1 && NQ * RPI == KR, "the waves' k-rows tile the stage");
   uint32_t coff[NQ];  // column byte offset of this lane's chunk, or kOOB past the operand's width
   uint32_t voff[NQ];  // coff + (k-row within the stage) * row pitch, or kOOB
 
   __device__ __forceinline__ static int krow_of(int q) {
-    return (((int)((threadIdx.x >> 6) & 3) * NQ + q) * 64 + (int)(threadIdx.x & 63)) / CPR;
+    return (((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63)) / CPR;
   }
-  // k-row of this lane within its wave's 16 for instruction q: q * RPI + sub()
+  // k-row of this lane within its wave's KR for instruction q: q * RPI + sub()
   __device__ __forceinline__ static int sub() { return (int)(threadIdx.x & 63) / CPR; }
   __device__ __forceinline__ void init(int mn0, int ncols, int64_t pitch_bytes) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const int f = ((int)((threadIdx.x >> 6) & 3) * NQ + q) * 64 + (int)(threadIdx.x & 63);
+      const int f = ((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63);
       const int kr = f / CPR;
       const int c = (f % CPR) ^ ((kr & 3) << 2);
       const int col = mn0 + 8 * c;
@@ -936,10 +938,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const char* base, u
 // dma(q, buf, kt, on) issues load instruction q (0..LPS-1) of stage kt into buffer
 // buf (reading zeros when !on); prefetch(kt) readies the gather indices of stage kt;
 // after_prologue_loads() runs once the first loads are in flight.
-template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, int NW, int GRP, typename Dma,
-          typename Prefetch, typename Hook>
-__device__ __forceinline__ void kloop64_group(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI],
-                                              Dma dma_slot, Prefetch prefetch, Hook after_prologue_loads) {
+template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch, typename Hook>
+__device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI], Dma dma,
+                                        Prefetch prefetch, Hook after_prologue_loads) {
   constexpr int KS = 64;
   constexpr int kStage = (BM + BN) * KS * 2;
   constexpr int AR = Frag<A_T>::kReads, BR = Frag<B_T>::kReads;
@@ -947,16 +948,9 @@ __device__ __forceinline__ void kloop64_group(int nk, lds_char* lds, int wm0, in
   constexpr int NMMA = MI * NI;                   // MFMAs per step
   constexpr int RPS = (NREAD + NMMA - 1) / NMMA;  // reads per MFMA slot
   constexpr int WIN = 2 * NMMA;                   // load window: step 3 + step 0
-  // With 8 waves, waves w and w + 4 split the LPS loads of load slot w & 3.
-  constexpr int LPW = LPS / (NW / 4);             // loads per wave per stage
-  static_assert(LPW * (NW / 4) == LPS, "loads split evenly");
-  // load j goes to window slot j * WIN / LPW (evenly spread); loads in slots < NMMA
+  // load j goes to window slot j * WIN / LPS (evenly spread); loads in slots < NMMA
   // belong to step 3 of the previous stage
-  constexpr int kEarly = (NMMA * LPW + WIN - 1) / WIN;  // loads j with j * WIN / LPW < NMMA
-  // wave group GRP (waves 4 GRP .. 4 GRP + 3) issues loads [GRP LPW, (GRP + 1) LPW) of its slot
-  auto dma = [&](int j, int buf, int kt, bool on) __attribute__((always_inline)) {
-    dma_slot(j + GRP * LPW, buf, kt, on);
-  };
+  constexpr int kEarly = (NMMA * LPS + WIN - 1) / WIN;  // loads j with j * WIN / LPS < NMMA
   Frag<A_T> fa[2][MI];
   Frag<B_T> fb[2][NI];
   auto read_piece = [&](int buf, const lds_char* st, int s, int i) {
@@ -985,8 +979,8 @@ __device__ __forceinline__ void kloop64_group(int nk, lds_char* lds, int wm0, in
     for (int i = 0; i < NMMA; ++i) {
       mma(cur, i);
 #pragma unroll
-      for (int j = 0; j < LPW; ++j)
-        if (w0 >= 0 && j * WIN / LPW == w0 + i) dma(j, lbuf, lkt, lon);
+      for (int j = 0; j < LPS; ++j)
+        if (w0 >= 0 && j * WIN / LPS == w0 + i) dma(j, lbuf, lkt, lon);
 #pragma unroll
       for (int r = 0; r < RPS; ++r)
         if (i * RPS + r < NREAD) read_piece(cur ^ 1, rst, rs, i * RPS + r);
@@ -1001,7 +995,7 @@ __device__ __forceinline__ void kloop64_group(int nk, lds_char* lds, int wm0, in
   }
   prefetch(0);
 #pragma unroll
-  for (int j = 0; j < LPW; ++j) dma(j, 0, 0, true);
+  for (int j = 0; j < LPS; ++j) dma(j, 0, 0, true);
   prefetch(1);
 #pragma unroll
   for (int j = 0; j < kEarly; ++j) dma(j, 1, 1, nk > 1);
@@ -1026,22 +1020,6 @@ __device__ __forceinline__ void kloop64_group(int nk, lds_char* lds, int wm0, in
     step(1, nst, 0, 0, buf, kt + 2, kt + 2 < nk);  // first part of stage kt + 2's loads
   }
   __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
-}
-
-// kloop64 for 4 waves, or for 8 waves (two per SIMD, output blocks of 128 x 64 per wave):
-// each wave group runs its own instance, so every load index stays a compile-time
-// constant (a runtime group offset would turn the loaders' offset arrays into
-// dynamically indexed scratch memory).
-template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, int NW, typename Dma, typename Prefetch,
-          typename Hook>
-__device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0, f32x16_t (&acc)[MI][NI], Dma dma_slot,
-                                        Prefetch prefetch, Hook after_prologue_loads) {
-  if (NW == 8 && __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) >= 4)
-    kloop64_group<LPS, MI, NI, A_T, B_T, BM, BN, NW, 1>(nk, lds, wm0, wn0, acc, dma_slot, prefetch,
-                                                        after_prologue_loads);
-  else
-    kloop64_group<LPS, MI, NI, A_T, B_T, BM, BN, NW, 0>(nk, lds, wm0, wn0, acc, dma_slot, prefetch,
-                                                        after_prologue_loads);
 }
 
 // Epilogues: each wave stages its own WM x WN accumulator block in its own LDS area
@@ -1344,15 +1322,16 @@ __device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* 
   }
 }
 
-// Wave layout of the bf16 kernels: NW = 4 waves in a 2 x 2 grid (kloop64), or NW = 8
-// in a 2 x 4 grid whose waves w and w + 4 share a SIMD (kloop64 with NW = 8).
+// Wave layout of the bf16 kernels: NW = 4 waves in a 2 x 2 grid, 8 in a 2 x 4 grid or 16
+// in a 4 x 4 grid (waves w, w + 4, ... share SIMD w % 4).
 template <int BM, int BN, int NW>
 struct WaveGrid {
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-  static constexpr int WM = BM / 2, WN = BN / (NW / 2);
+  static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
+  static constexpr int GM = NW == 16 ? 4 : 2, GN = NW / GM;
+  static constexpr int WM = BM / GM, WN = BN / GN;
   static constexpr int MI = WM / 32, NI = WN / 32;
-  __device__ __forceinline__ static int wm0(int wave) { return (wave / (NW / 2)) * WM; }
-  __device__ __forceinline__ static int wn0(int wave) { return (wave % (NW / 2)) * WN; }
+  __device__ __forceinline__ static int wm0(int wave) { return (wave / GN) * WM; }
+  __device__ __forceinline__ static int wn0(int wave) { return (wave % GN) * WN; }
 };
 
 // LDS of the bf16 kernels: two operand stages, reused by the wave staging areas
@@ -1380,37 +1359,40 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
   const int nt = __builtin_amdgcn_readfirstlane(tile.nt);
   const int rows = tile.rows;
   const int64_t row0 = tile.row0;
-  const int wu = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));  // load slot
+  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
   const int ktail = p.K % KS;
   const int nk = (p.K + KS - 1) / KS;
 
   // Row indices (< 2^31) are read as the low 32-bit words of the int64 entries, all
   // issued before any is used so their latencies overlap.
-  RowLoad<BM> la;
-  int a_src[RowLoad<BM>::NQ];
+  using LA = RowLoad<BM, NW>;
+  using LBN = RowLoad<B_T ? 8 * NW : BN, NW>;  // (placeholder sizes for the unused loader)
+  using LBT = KLoad<B_T ? BN : 8 * NW, NW>;
+  LA la;
+  int a_src[LA::NQ];
 #pragma unroll
-  for (int q = 0; q < RowLoad<BM>::NQ; ++q) {
-    const int r = RowLoad<BM>::row_of(q);
+  for (int q = 0; q < LA::NQ; ++q) {
+    const int r = LA::row_of(q);
     a_src[q] = (int)(row0 + (r < rows ? r : 0));
   }
   if (p.a_rows != nullptr) {
     const int* idx32 = reinterpret_cast<const int*>(p.a_rows);
 #pragma unroll
-    for (int q = 0; q < RowLoad<BM>::NQ; ++q) a_src[q] = idx32[2 * (int64_t)a_src[q]];
+    for (int q = 0; q < LA::NQ; ++q) a_src[q] = idx32[2 * (int64_t)a_src[q]];
 #pragma unroll
-    for (int q = 0; q < RowLoad<BM>::NQ; ++q) a_src[q] /= p.a_div;
+    for (int q = 0; q < LA::NQ; ++q) a_src[q] /= p.a_div;
   }
 #pragma unroll
-  for (int q = 0; q < RowLoad<BM>::NQ; ++q)
-    la.set(q, RowLoad<BM>::row_of(q) < rows ? (uint32_t)((int64_t)a_src[q] * p.lda * 2) : kOOB, ktail);
+  for (int q = 0; q < LA::NQ; ++q)
+    la.set(q, LA::row_of(q) < rows ? (uint32_t)((int64_t)a_src[q] * p.lda * 2) : kOOB, ktail);
   const int ncol0 = nt * BN;
-  RowLoad<B_T ? 32 : BN> lbn;
-  KLoad<B_T ? BN : 128> lbt;
+  LBN lbn;
+  LBT lbt;
   if constexpr (!B_T) {
 #pragma unroll
-    for (int q = 0; q < RowLoad<BN>::NQ; ++q) {
-      const int r = RowLoad<BN>::row_of(q);
+    for (int q = 0; q < LBN::NQ; ++q) {
+      const int r = LBN::row_of(q);
       int n;
       bool ok;
       if constexpr (EPI == EPI_SWIGLU) {
@@ -1428,8 +1410,8 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
   }
   const char* a_base = reinterpret_cast<const char*>(p.a);
   const char* b_base = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride);
-  constexpr int NQA = RowLoad<BM>::NQ;
-  constexpr int LPS = NQA + (B_T ? KLoad<BN>::NQ : RowLoad<BN>::NQ);
+  constexpr int NQA = LA::NQ;
+  constexpr int LPS = NQA + (B_T ? LBT::NQ : LBN::NQ);  // loads per wave per stage
   auto dma = [&](int q, int buf, int kt, bool on) {
     lds_char* sa = lds + buf * kStage;
     lds_char* sb = sa + BM * KS * 2;
@@ -1470,7 +1452,7 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
   auto hook = [&] {
     if (threadIdx.x < BM) row_table[threadIdx.x] = orow_v;
   };
-  kloop64<LPS, MI, NI, false, B_T, BM, BN, NW>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
+  kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
   // every wave is done with the operand stages (and has written its row-table entries)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,
@@ -1522,12 +1504,13 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   const int64_t r_end = p.offsets[e];
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   const int m0 = mt * BM, n0 = nt * BN;
-  const int wu = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));  // load slot
+  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
   const int nk = (nrows + KS - 1) / KS;
 
-  using LA = KLoad<BM>;
-  using LB = KLoad<BN>;
+  using LA = KLoad<BM, NW>;
+  using LB = KLoad<BN, NW>;
+  constexpr int KR = LB::KR;  // k-rows (gathered x rows) per wave per stage
   LA la;
   LB lb;
   la.init(m0, p.Ndy, p.lddy * 2);
@@ -1536,40 +1519,40 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   const char* dy_base = reinterpret_cast<const char*>(p.dy);
   const char* x_base = reinterpret_cast<const char*>(p.x);
 
-  // Gathered x rows: the wave's 16 k-rows of a stage come as byte offsets in scalar
+  // Gathered x rows: the wave's KR k-rows of a stage come as byte offsets in scalar
   // registers. Their indices are fetched one stage ahead with one vector load per wave
-  // (lanes 0..15, the low 32-bit words of the int64 entries) and moved to scalar
+  // (lanes 0..KR-1, the low 32-bit words of the int64 entries) and moved to scalar
   // registers with v_readlane when the stage's loads are set up. A vector load counts
   // on vmcnt, which the K loop only waits on at its barrier; scalar loads would count on
   // lgkmcnt and stall every fragment-read wait until they returned. Rows past the
   // expert's end get kOOBRow, which stays out of range after adding any column offset.
   constexpr uint32_t kOOBRow = 0x7ffffff0u;
   const uint32_t* xr32 = reinterpret_cast<const uint32_t*>(p.x_rows);
-  uint32_t src_off[16];
-  uint32_t pend = 0;  // this lane's index word for the next stage (lanes 0..15 hold the wave's 16 k-rows)
+  uint32_t src_off[KR];
+  uint32_t pend = 0;  // this lane's index word for the next stage (lanes 0..KR-1 hold the wave's k-rows)
   const int64_t ldx2 = p.ldx * 2;
   auto issue_idx = [&](int kt) -> uint32_t {
-    const int pos = kt * KS + 16 * wu + (int)(threadIdx.x & 15);
+    const int pos = kt * KS + KR * wu + (int)(threadIdx.x & (KR - 1));
     return xr32[2 * (r_begin + (pos < nrows ? pos : nrows - 1))];
   };
   // stage kt's indices (in pend) -> src_off, and the next stage's load issued; stages at or
   // past nk get kOOBRow everywhere and re-read the last valid index (no branch in the loop)
   auto fetch_src = [&](int kt) {
-    const int base = kt * KS + 16 * wu;
-    uint32_t v[16];  // gather indices are below 2^31 (R < 2^31)
+    const int base = kt * KS + KR * wu;
+    uint32_t v[KR];  // gather indices are below 2^31 (R < 2^31)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = (uint32_t)__builtin_amdgcn_readlane((int)pend, j);
+    for (int j = 0; j < KR; ++j) v[j] = (uint32_t)__builtin_amdgcn_readlane((int)pend, j);
     pend = issue_idx(kt + 1);
     if constexpr (GATHER == 1) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] >>= p.x_div_shift;
+      for (int j = 0; j < KR; ++j) v[j] >>= p.x_div_shift;
     } else {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] /= (uint32_t)p.x_div;
+      for (int j = 0; j < KR; ++j) v[j] /= (uint32_t)p.x_div;
     }
     // row byte offsets fit in 32 bits: x spans less than 2 GiB
 #pragma unroll
-    for (int j = 0; j < 16; ++j) src_off[j] = base + j < nrows ? v[j] * (uint32_t)ldx2 : kOOBRow;
+    for (int j = 0; j < KR; ++j) src_off[j] = base + j < nrows ? v[j] * (uint32_t)ldx2 : kOOBRow;
   };
   auto dma = [&](int q, int buf, int kt, bool on) {
     lds_char* sa = lds + buf * kStage;
@@ -1581,7 +1564,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
                wu);
     } else if constexpr (GATHER != 0) {
       const int qq = q - LA::NQ;
-      // this lane's k-row is qq * RPI + sub of the wave's 16; qq is a compile-time
+      // this lane's k-row is qq * RPI + sub of the wave's KR; qq is a compile-time
       // constant here (unrolled), so the pick indexes the array with constants only
       // (a select between array elements is turned back into a dynamically indexed
       // array, i.e. scratch memory; the masked XOR keeps every index constant)
@@ -1619,7 +1602,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   auto prefetch = [&](int kt) {
     if constexpr (GATHER != 0) fetch_src(kt);
   };
-  kloop64<LPS, MI, NI, true, true, BM, BN, NW>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
+  kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
   if constexpr (OUT_F32)
     wgrad_epilogue_f32(p, acc, e, m0, n0, wm0, wn0);
@@ -1673,7 +1656,7 @@ constexpr int rows_lds_bytes() {
 template <int BM, int BN, int NW = 4>
 constexpr int bf16_lds_bytes() {
   constexpr int main_loop = bf16_stage_bytes<BM, BN, NW>() + BM * 4;  // stages / staging + output-row table
-  constexpr int decode = (kGemmMaxE + 4 + 8) * 4;
+  constexpr int decode = (kGemmMaxE + 4 + 16) * 4;
   return main_loop > decode ? main_loop : decode;
 }
 
@@ -1709,10 +1692,14 @@ int launch_rows_f32(const RowsParams& p, int64_t R, hipStream_t s) {
 }
 
 // 256 x 256 tiles run with 8 waves (two per SIMD: while one wave is held issuing its
-// LDS-DMA loads, the other issues MFMAs), 128 x 128 tiles with 4.
+// LDS-DMA loads, the other issues MFMAs), 128 x 128 tiles with 4. (16 waves measured
+// slower: 64 x 64 per wave doubles the fragment reads per MFMA and leaves 128 registers
+// per wave.)
+constexpr int kBigWaves = 8;
+
 template <int BM, int BN, bool B_KN, int EPI>
 int launch_rows_bf16(const RowsParams& p, int64_t R, hipStream_t s) {
-  constexpr int NW = BM == 256 ? 8 : 4;
+  constexpr int NW = BM == 256 ? kBigWaves : 4;
   return launch_rows_kernel(rows_bf16_kernel<BM, BN, B_KN, EPI, NW>, bf16_lds_bytes<BM, BN, NW>(), BM, p, R, s,
                             NW * 64);
 }
@@ -1732,8 +1719,9 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
 
 template <int GATHER, bool OUT_F32>
 int launch_wgrad_big(const WgradParams& p, hipStream_t s) {
-  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, 8>, bf16_lds_bytes<256, 256, 8>(), 256, 256,
-                             p, s, 512);
+  constexpr int NW = kBigWaves;
+  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, NW>, bf16_lds_bytes<256, 256, NW>(), 256,
+                             256, p, s, NW * 64);
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
@@ -1748,10 +1736,134 @@ inline bool use_big_tiles(int64_t R, int E, int64_t N) {
   return R >= (int64_t)E * 256 && N >= 256;
 }
 
+// ==================================================================== small-M streaming path
+// Forward rows GEMMs when the experts hold few rows (the small-batch regime, e.g. a
+// decode step): the weights are then the only large operand and the GEMM is bound by
+// streaming them from HBM. Each wave owns 32 weight rows (16 SwiGLU pairs: their h and
+// gate rows) and streams them from HBM straight into MFMA operand registers (no LDS, no
+// barriers), kStreamDepth 64-deep stages ahead, multiplying them with up to 32 of the
+// expert's rows per pass, which come from L2. v_mfma_f32_32x32x16_bf16 takes the weight
+// fragment as its first operand, so lane (r, g) ends up with 4 consecutive output
+// columns (weight rows 8 q + 4 g .. + 3) of expert row r.
+// Measured at d = 2048, E = 128, k = 8 (W1 with SwiGLU + W2): 219 vs 237 us for the tiled
+// kernels at T = 32, even at T = 128, slower from T = 256 on; depths 2, 3 and 4 time the same.
+constexpr int kStreamDepth = 2;
+constexpr int kStreamRowsPerExpert = 8;  // dispatch bound on R / E
+
+template <int EPI>
+__global__ __launch_bounds__(256) void stream_rows_kernel(RowsParams p, int wtiles_per_e) {
+  const int lane = (int)(threadIdx.x & 63);
+  const int wpe = (wtiles_per_e + 3) / 4;  // workgroups per expert
+  const int e = (int)blockIdx.x / wpe;
+  const int wt = ((int)blockIdx.x % wpe) * 4 + (int)(threadIdx.x >> 6);
+  if (e >= p.E || wt >= wtiles_per_e) return;  // (waves are independent: no barriers)
+  const int64_t e_begin = e ? p.offsets[e - 1] : 0;
+  const int64_t count = p.offsets[e] - e_begin;
+  if (count <= 0) return;
+  const int r = lane & 31, g = lane >> 5;
+  int n;
+  bool nok;
+  if constexpr (EPI == EPI_SWIGLU) {
+    const int jj = wt * 16 + (r & 15);
+    nok = jj < p.half;
+    n = (r & 16) ? p.half + jj : jj;
+  } else {
+    n = wt * 32 + r;
+    nok = n < p.N;
+  }
+  const char* b_base = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride);
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(b_base, p.b_bytes);
+  const __amdgpu_buffer_rsrc_t ars = make_rsrc(p.a, p.a_bytes);
+  // offsets of this lane's 16 bytes at k = 0 (kOOB: reads zero); + 128 per 64-deep stage, + 32 per step
+  const uint32_t boff = nok ? (uint32_t)((int64_t)n * p.ldb * 2) + 16u * (uint32_t)g : kOOB;
+  const int nkc = p.K / 64;
+  uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+  for (int64_t mb = 0; mb < count; mb += 32) {
+    uint32_t aoff = kOOB;
+    if (mb + r < count) {
+      int64_t src = e_begin + mb + r;
+      if (p.a_rows != nullptr) src = reinterpret_cast<const int*>(p.a_rows)[2 * src] / p.a_div;
+      aoff = (uint32_t)(src * p.lda * 2) + 16u * (uint32_t)g;
+    }
+    f32x16_t acc;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+    v4i32_t wf[kStreamDepth][4], xf[kStreamDepth][4];
+    auto load = [&](int buf, int kc) __attribute__((always_inline)) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t ko = (uint32_t)kc * 128u + 32u * (uint32_t)s;
+        wf[buf][s] = __builtin_bit_cast(v4i32_t, __builtin_amdgcn_raw_buffer_load_b128(brs, boff + ko, 0, 0));
+        xf[buf][s] = __builtin_bit_cast(v4i32_t, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff + ko, 0, 0));
+      }
+    };
+#pragma unroll
+    for (int u = 0; u < kStreamDepth; ++u)
+      if (u < nkc) load(u, u);
+    for (int kc = 0; kc < nkc; kc += kStreamDepth) {
+#pragma unroll
+      for (int u = 0; u < kStreamDepth; ++u) {
+        if (kc + u < nkc) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, wf[u][s]),
+                                                          __builtin_bit_cast(bf16x8_t, xf[u][s]), acc, 0, 0, 0);
+          if (kc + u + kStreamDepth < nkc) load(u, kc + u + kStreamDepth);
+        }
+      }
+    }
+    if (mb + r >= count) continue;
+    const int64_t i = e_begin + mb + r;  // sorted row
+    const int64_t o = p.c_rows ? reinterpret_cast<const int*>(p.c_rows)[2 * i] : i;
+    if constexpr (EPI == EPI_SWIGLU) {
+      // acc[4 q + u]: h of pair wt 16 + 8 q + 4 g + u for q = 0, 1; its gate at q + 2
+      uint16_t* A2 = reinterpret_cast<uint16_t*>(p.c2);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int pr = wt * 16 + 8 * q + 4 * g;
+        if (pr >= p.half) continue;
+        float h[4], gt[4], a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          h[u] = to_f32(bf16_bits(acc[4 * q + u]));
+          gt[u] = to_f32(bf16_bits(acc[4 * (q + 2) + u]));
+          a[u] = silu_f(gt[u]) * h[u];
+        }
+        *reinterpret_cast<uint2*>(C + o * p.ldc + pr) = pack4_bf16(h);
+        *reinterpret_cast<uint2*>(C + o * p.ldc + p.half + pr) = pack4_bf16(gt);
+        *reinterpret_cast<uint2*>(A2 + o * p.ldc2 + pr) = pack4_bf16(a);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = wt * 32 + 8 * q + 4 * g;
+        if (c0 >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = acc[4 * q + u];
+        *reinterpret_cast<uint2*>(C + o * p.ldc + c0) = pack4_bf16(v);
+      }
+    }
+  }
+}
+
+template <int EPI>
+int launch_stream_rows(const RowsParams& p, hipStream_t s) {
+  const int wtiles = EPI == EPI_SWIGLU ? (int)cdiv(p.half, 16) : (int)cdiv(p.N, 32);
+  const int64_t blocks = (int64_t)p.E * cdiv(wtiles, 4);
+  ZMOE_REQUIRE(blocks < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "grouped gemm: too many tiles");
+  hipLaunchKernelGGL(stream_rows_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, p, wtiles);
+  return check_launch("grouped rows streaming kernel");
+}
+
 template <bool B_KN, int EPI>
 int dispatch_rows(int dtype, RowsParams p, int64_t R, int bn_for_tiles_div, hipStream_t s) {
   // n_tiles: along N (or along pair columns for SwiGLU, BN/2 pairs per tile)
   if (dtype == ZMOE_DTYPE_BF16) {
+    if constexpr (!B_KN && (EPI == EPI_STORE || EPI == EPI_SWIGLU)) {
+      // few rows per expert: stream the weights (the K loop takes whole 64-deep stages)
+      if (R <= (int64_t)kStreamRowsPerExpert * p.E && p.K % 64 == 0) return launch_stream_rows<EPI>(p, s);
+    }
     if (use_big_tiles(R, p.E, p.N)) {
       p.n_tiles = (int)cdiv(bn_for_tiles_div, EPI == EPI_SWIGLU ? 128 : 256);
       return launch_rows_bf16<256, 256, B_KN, EPI>(p, R, s);

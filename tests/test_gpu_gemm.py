@@ -23,6 +23,8 @@ SHAPES = [
     (600, 128, 128, 12, 3, 0.5),    # k = 3 with 128 tiles
     (1200, 200, 264, 4, 2, 0.3),    # 256 tiles with K and N tails (K % 64 = 8)
     (600, 64, 256, 2, 2, 0.0),      # 256 tiles, a single K stage
+    (120, 256, 80, 64, 4, 1.5),     # few rows per expert (weight streaming), skewed: experts past 32 rows
+    (32, 128, 256, 32, 8, 0.0),     # weight streaming, 8 rows per expert
 ]
 
 
@@ -82,7 +84,7 @@ def test_group_bwd_w(hip_device, dtype, T, K, N, E, k, skew, gather):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
                                             (1500, 256, 96, 16, 4, 1.5), (2, 64, 32, 8, 2, 0.0),
-                                            (1200, 200, 136, 4, 2, 0.3)])
+                                            (1200, 200, 136, 4, 2, 0.3), (128, 512, 136, 64, 4, 1.5)])
 def test_glu_fused_forward_and_backward_dh(hip_device, dtype, T, d, f, E, k, skew):
     from zmoe import ops
 
