@@ -25,6 +25,7 @@ SHAPES = [
     (600, 64, 256, 2, 2, 0.0),      # 256 tiles, a single K stage
     (120, 256, 80, 64, 4, 1.5),     # few rows per expert (weight streaming), skewed: experts past 32 rows
     (32, 128, 256, 32, 8, 0.0),     # weight streaming, 8 rows per expert
+    (6000, 64, 128, 1000, 2, 0.5),  # E = 1000: tile decode with 16 experts per lane, the last lanes partial
 ]
 
 
