@@ -224,7 +224,43 @@ def pmc_summary(path: str) -> int:
     for (kern, ctr), d in sorted(rows.items(), key=lambda kv: kv[1]["first"]):
         vals = list(d["v"].values())
         print(f"{ctr:12s} {len(vals):10d} {sum(vals) / len(vals):16.1f}  {kern[:110]}")
+    _pmc_clock_mfma(path, rows)
     return 0
+
+
+def _pmc_clock_mfma(path: str, rows: dict) -> None:
+    """With GRBM_GUI_ACTIVE and SQ_VALU_MFMA_BUSY_CYCLES collected beside --kernel-trace: the
+    core clock each kernel ran at (GRBM_GUI_ACTIVE is summed over the 8 XCDs) and the fraction
+    of the 1024 SIMDs' cycles in which the MFMA pipe was busy, at that clock."""
+    import csv
+    import glob
+
+    traces = sorted(glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True))
+    if not traces:
+        return
+    dur = {}
+    for fn in traces:
+        with open(fn) as fh:
+            for r in csv.DictReader(fh):
+                dur[(r["Kernel_Name"], r["Dispatch_Id"])] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    kernels = {k for k, c in rows if c == "SQ_VALU_MFMA_BUSY_CYCLES"}
+    out = []
+    for kern in kernels:
+        gui, busy = rows.get((kern, "GRBM_GUI_ACTIVE")), rows[(kern, "SQ_VALU_MFMA_BUSY_CYCLES")]
+        if gui is None:
+            continue
+        ids = [i for i in busy["v"] if (kern, i) in dur and i in gui["v"]]
+        if not ids or sum(busy["v"][i] for i in ids) < 1e6 * len(ids):
+            continue
+        ns = sum(dur[(kern, i)] for i in ids) / len(ids)
+        cyc = sum(gui["v"][i] for i in ids) / len(ids) / 8            # per XCD
+        mf = sum(busy["v"][i] for i in ids) / len(ids)
+        out.append((busy["first"], kern, len(ids), ns, cyc, mf))
+    if not out:
+        return
+    print(f"\n{'dispatches':>10s} {'avg ms':>8s} {'clock GHz':>9s} {'MFMA busy':>9s} {'MFMA ops/disp':>13s}  kernel")
+    for _, kern, n, ns, cyc, mf in sorted(out):
+        print(f"{n:10d} {ns / 1e6:8.3f} {cyc / ns:9.3f} {mf / (1024 * cyc):9.3f} {mf / 32:13.4g}  {kern[:90]}")
 
 
 def ns_flops(m: int, n: int, steps: int, executed: bool = False) -> float:
