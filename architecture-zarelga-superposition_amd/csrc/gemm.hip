@@ -317,6 +317,7 @@ struct WgradParams {
   int Ndy, Kx, E;
   int m_tiles, n_tiles;
   uint32_t dy_bytes, x_bytes;  // addressable bytes from p.dy / p.x
+  int rows_lo = 0, rows_hi = 0x7fffffff;  // bf16 kernels: only experts with rows_lo <= rows <= rows_hi
 };
 
 struct RowsTile {
@@ -1503,6 +1504,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   const int64_t r_begin = e ? p.offsets[e - 1] : 0;
   const int64_t r_end = p.offsets[e];
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
+  if (nrows < p.rows_lo || nrows > p.rows_hi) return;  // the other launch of a split covers this expert
   const int m0 = mt * BM, n0 = nt * BN;
   const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
@@ -1734,6 +1736,21 @@ inline bool use_big_tiles(int64_t R, int E, int64_t N) {
   if (forced == 128) return false;
   if (forced == 256) return N >= 256;
   return R >= (int64_t)E * 256 && N >= 256;
+}
+
+// Weight grads under a skewed routing: experts holding at most this many rows get a
+// launch of 128 x 128 tiles of their own (two workgroups per CU, so one's output writes
+// overlap the other's loads), the rest the 256 x 256 tiles; 0 = one launch. The row
+// counts stay on the device: each launch covers every expert's tiles and a workgroup
+// whose expert belongs to the other launch exits at once (~0.2-0.5 ns per workgroup).
+// ZMOE_WGRAD_SMALL_ROWS=n pins the bound (a tuning knob; unset = automatic).
+inline int wgrad_small_rows(int64_t R, int E) {
+  static const int forced = [] {
+    const char* v = getenv("ZMOE_WGRAD_SMALL_ROWS");
+    return v ? atoi(v) : -1;
+  }();
+  if (forced >= 0) return forced;
+  return R < (int64_t)E * 1024 ? 64 : 0;
 }
 
 // ==================================================================== small-M streaming path
@@ -2118,18 +2135,31 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   if (dtype == ZMOE_DTYPE_BF16) {
     const bool big = use_big_tiles(M, E, N) && K >= 256;
     const int gather = p.x_rows ? (p.x_div_shift >= 0 ? 1 : 2) : 0;
-    if (big && gather == 1)
-      rc = launch_wgrad_big<1, false>(p, s);
-    else if (big && gather == 2)
-      rc = launch_wgrad_big<2, false>(p, s);
-    else if (big)
-      rc = launch_wgrad_big<0, false>(p, s);
-    else if (gather == 1)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
-    else if (gather == 2)
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
-    else
-      rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
+    auto small_tiles = [&](const WgradParams& q) {
+      if (gather == 1)
+        return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
+      if (gather == 2)
+        return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
+    };
+    const int split = big ? wgrad_small_rows(M, E) : 0;
+    rc = 0;
+    if (split > 0) {  // experts of at most `split` rows on 128 x 128 tiles, the rest below
+      WgradParams q = p;
+      q.rows_hi = split;
+      rc = small_tiles(q);
+      p.rows_lo = split + 1;
+    }
+    if (rc == 0) {
+      if (!big)
+        rc = small_tiles(p);
+      else if (gather == 1)
+        rc = launch_wgrad_big<1, false>(p, s);
+      else if (gather == 2)
+        rc = launch_wgrad_big<2, false>(p, s);
+      else
+        rc = launch_wgrad_big<0, false>(p, s);
+    }
   } else {
     rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
                              s);

@@ -82,6 +82,34 @@ def test_group_bwd_w(hip_device, dtype, T, K, N, E, k, skew, gather):
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
 
 
+@pytest.mark.parametrize("gather", [False, True])
+def test_group_bwd_w_small_expert_split(hip_device, gather):
+    """bf16 weight grads with 256 x 256 tiles and fewer than 1024 rows per expert on average:
+    experts of at most 64 rows go to a separate launch of 128 x 128 tiles. Row counts on
+    both sides of that bound (0, 1, 64, 65) beside large experts."""
+    from zmoe import ops
+
+    counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0])
+    E, k, N, K = len(counts), 2, 256, 320
+    off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
+    R = int(counts.sum())
+    g = gen(R + N)
+    DY = torch.randn(R, N, generator=g).to(torch.bfloat16)
+    if gather:  # x rows of R / k tokens, each sorted row r reads token ss[r] // k
+        ss = torch.from_numpy(np.random.default_rng(7).permutation(R)).to(hip_device)
+        X = torch.randn(R // k + 1, K, generator=g).to(torch.bfloat16)
+        Xg = O.group(np64(X), ss.cpu().numpy(), fan_out=k)
+    else:
+        ss = None
+        X = torch.randn(R, K, generator=g).to(torch.bfloat16)
+        Xg = np64(X)
+    DWt, _ = ops.group_bwd_w(DY.to(hip_device), X.to(hip_device), off, E, x_gather=ss, x_div=k)
+    ref, _ = O.group_bwd_w(np64(DY), Xg, off.cpu().numpy(), E)
+    assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[torch.bfloat16], what="group_bwd_w split")
+    for e in np.nonzero(counts == 0)[0]:
+        assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
                                             (1500, 256, 96, 16, 4, 1.5), (2, 64, 32, 8, 2, 0.0),
