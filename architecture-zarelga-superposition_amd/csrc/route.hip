@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(const float* _
                                                                   const float* __restrict__ prob,
                                                                   const int64_t* __restrict__ idx,
                                                                   int64_t T, int E, int k,
-                                                                  GT* __restrict__ dlogits) {
+                                                                  GT* __restrict__ dlogits, int64_t ld) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(const float* _
   const float sgn = pj > 0.f ? 1.f : (pj < 0.f ? -1.f : 0.f);
   const float dp = S_raw > 1e-12f ? (dwj - inner * sgn) / S : dwj / S;
   const float dz = dp * pj * (1.f - pj);
-  GT* row = dlogits + t * (int64_t)E;
+  GT* row = dlogits + t * ld;
   for (int e0 = 0; e0 < E; e0 += 64) {
     const int e = e0 + lane;
     float v = 0.f;
@@ -183,19 +183,21 @@ extern "C" int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, 
 
 extern "C" int zmoe_route_topk_backward(const float* d_weight, const float* topk_prob,
                                         const int64_t* topk_idx, int64_t T, int E, int k, void* d_logits,
-                                        int d_logits_dtype, void* stream) {
+                                        int64_t ld_d_logits, int d_logits_dtype, void* stream) {
   ZMOE_REQUIRE(dtype_ok(d_logits_dtype), ZMOE_ERR_DTYPE, "route_topk_backward: dtype %d", d_logits_dtype);
   ZMOE_REQUIRE(T >= 0 && E >= 1 && k >= 1 && k <= E && k <= 64, ZMOE_ERR_SHAPE,
                "route_topk_backward: bad sizes (E=%d, k=%d)", E, k);
+  ZMOE_REQUIRE(ld_d_logits >= E, ZMOE_ERR_SHAPE, "route_topk_backward: row stride %lld below E=%d",
+               (long long)ld_d_logits, E);
   if (T == 0) return ZMOE_OK;
   ZMOE_REQUIRE(d_weight && topk_prob && topk_idx && d_logits, ZMOE_ERR_NULL, "route_topk_backward: null pointer");
   const dim3 grid((unsigned)cdiv(T, 4)), block(256);
   if (d_logits_dtype == ZMOE_DTYPE_BF16)
     hipLaunchKernelGGL(route_topk_backward_kernel<uint16_t>, grid, block, 0, as_stream(stream), d_weight,
-                       topk_prob, topk_idx, T, E, k, (uint16_t*)d_logits);
+                       topk_prob, topk_idx, T, E, k, (uint16_t*)d_logits, ld_d_logits);
   else
     hipLaunchKernelGGL(route_topk_backward_kernel<float>, grid, block, 0, as_stream(stream), d_weight,
-                       topk_prob, topk_idx, T, E, k, (float*)d_logits);
+                       topk_prob, topk_idx, T, E, k, (float*)d_logits, ld_d_logits);
   return check_launch("route_topk_backward");
 }
 

@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kRowThreads) void swiglu_kernel(const T* __restrict
 template <typename T>
 __global__ __launch_bounds__(kRowThreads) void swiglu_backward_kernel(const T* __restrict__ dA,
                                                                       const T* __restrict__ H, int64_t R,
-                                                                      int64_t f, T* __restrict__ dH) {
+                                                                      int64_t f, T* __restrict__ dH, int64_t ld) {
   constexpr int VN = V<T>::N;
   const int64_t nch = f / VN;
   const int64_t i = (int64_t)blockIdx.x * kRowThreads + threadIdx.x;
@@ -303,8 +303,8 @@ __global__ __launch_bounds__(kRowThreads) void swiglu_backward_kernel(const T* _
     dh[q] = da[q] * g[q] * s;
     dg[q] = da[q] * h[q] * s * (1.f + g[q] * (1.f - s));
   }
-  st16(dH + r * 2 * f + ch * VN, pack_chunk(dh, T{}));
-  st16(dH + r * 2 * f + f + ch * VN, pack_chunk(dg, T{}));
+  st16(dH + r * ld + ch * VN, pack_chunk(dh, T{}));
+  st16(dH + r * ld + f + ch * VN, pack_chunk(dg, T{}));
 }
 
 }  // namespace zmoe
@@ -511,20 +511,21 @@ extern "C" int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void*
 }
 
 extern "C" int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f, int dtype, void* dH,
-                                    void* stream) {
+                                    int64_t ld_dh, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "swiglu_backward: dtype");
-  ZMOE_REQUIRE(R >= 0 && f >= 0, ZMOE_ERR_SHAPE, "swiglu_backward: bad sizes");
+  ZMOE_REQUIRE(R >= 0 && f >= 0 && ld_dh >= 2 * f, ZMOE_ERR_SHAPE, "swiglu_backward: bad sizes");
   if (R == 0 || f == 0) return ZMOE_OK;
   ZMOE_REQUIRE(dA && H && dH, ZMOE_ERR_NULL, "swiglu_backward: null pointer");
-  ZMOE_REQUIRE(f % vec_of(dtype) == 0 && aligned16(H) && aligned16(dA) && aligned16(dH), ZMOE_ERR_ALIGN,
-               "swiglu_backward: f must be a multiple of %d", vec_of(dtype));
+  ZMOE_REQUIRE(f % vec_of(dtype) == 0 && ld_dh % vec_of(dtype) == 0 && aligned16(H) && aligned16(dA) &&
+                   aligned16(dH),
+               ZMOE_ERR_ALIGN, "swiglu_backward: f and the dH row stride must be multiples of %d", vec_of(dtype));
   const int64_t n = R * (f / vec_of(dtype));
   const dim3 grid((unsigned)cdiv(n, kRowThreads)), block(kRowThreads);
   if (dtype == ZMOE_DTYPE_BF16)
     hipLaunchKernelGGL(swiglu_backward_kernel<uint16_t>, grid, block, 0, as_stream(stream), (const uint16_t*)dA,
-                       (const uint16_t*)H, R, f, (uint16_t*)dH);
+                       (const uint16_t*)H, R, f, (uint16_t*)dH, ld_dh);
   else
     hipLaunchKernelGGL(swiglu_backward_kernel<float>, grid, block, 0, as_stream(stream), (const float*)dA,
-                       (const float*)H, R, f, (float*)dH);
+                       (const float*)H, R, f, (float*)dH, ld_dh);
   return check_launch("swiglu_backward");
 }

@@ -9,8 +9,10 @@ into the routed experts' combine pass, which writes the padded layout directly.
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from scattermoe.mlp import GLUMLP
+from zmoe import ops as _z
 
 from .expert_layer import ExpertMLP
 from .moe_gate import MoEGate
@@ -26,6 +28,73 @@ def pad_input(x: torch.Tensor, indices: torch.Tensor, batch: int, seqlen: int) -
     out = torch.zeros((batch * seqlen, *x.shape[1:]), dtype=x.dtype, device=x.device)
     out[indices] = x
     return out.view(batch, seqlen, *x.shape[1:])
+
+
+class _FusedMoELayer(torch.autograd.Function):
+    """The whole layer in one autograd function (bf16 on the device): gate projection and
+    routing, shared expert, routed GLU experts, combine. It runs the same kernels in the
+    same order as the module composition (MoEGate, ExpertMLP and GLUMLP's fused path) in
+    the forward, so the routing and output are the same values. The backward writes the
+    shared expert's dH and the gate's d_logits side by side into one [T, 2fs + E] buffer:
+    one GEMM against [W_up; W_gate; W_router] gives both of their input grads, one split-K
+    weight-grad launch all three weight grads, and the k-sum pass adds that input grad to
+    the routed experts' (one rounding; the composition runs two more GEMM launches and two
+    adds over [T, d]).
+
+    (x [T, d], gate weight, expert_biases, W1, W2, shared gate/up/down weights, k, E,
+    stash, pad_rows, pad_total) -> (out, topk_idx [T, k]); out is [T, d], or with pad_rows
+    (int64 [T]) the padded [pad_total, d] whose row pad_rows[t] is token t's.
+    """
+
+    @staticmethod
+    def forward(ctx, x, gate_w, expert_biases, W1, W2, Ws_gate, Ws_up, Ws_down, k: int, E: int, stash: dict,
+                pad_rows=None, pad_total=None):
+        logits = F.linear(x, gate_w)                                                 # moe_gate.py:26
+        idx, w, p = _z.route_topk(logits, expert_biases, k, round_probs_bf16=logits.dtype == torch.bfloat16)
+        fs = Ws_up.shape[0]
+        W3 = torch.cat([Ws_up, Ws_gate, gate_w], dim=0)     # [2fs + E, d]; rows :2fs = [up | gate]
+        Hs = F.linear(x, W3[:2 * fs])
+        As = _z.swiglu(Hs)
+        S = F.linear(As, Ws_down)                                                    # expert_layer.py:23-24
+        se, ss, off, inv = _z.flatten_sort_count(idx, E)                             # mlp.py:80-82
+        stash["expert_offsets"] = off
+        H, A = _z.glu_w1_forward(x, W1, se, ss, off, k)
+        Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
+                               expert_offsets=off)
+        out = _z.combine(Y, w, k, addend=S, out_rows=pad_rows, out_total=pad_total)  # moe_layer.py:48-56
+        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A, Y)
+        ctx.k, ctx.E, ctx.fs = k, E, fs
+        ctx.pad_rows = pad_rows
+        ctx.mark_non_differentiable(idx)
+        return out, idx
+
+    @staticmethod
+    def backward(ctx, dout, d_idx):
+        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A, Y = ctx.saved_tensors
+        k, E, fs = ctx.k, ctx.E, ctx.fs
+        need = ctx.needs_input_grad
+        dout = dout.to(x.dtype).contiguous()
+        pad_rows = ctx.pad_rows
+        # routed experts, as GLUExpertsFunction.backward (a padded grad is read in place)
+        d_gates, dYg = _z.combine_backward(Y, dout, w, inv, grad_rows=pad_rows)
+        dH = _z.glu_w2_backward_dh(dYg, W2, H, se, off)
+        dW2 = _z.group_bwd_w(dYg, A, off, E)[0] if need[4] else None
+        dW1 = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)[0] if need[3] else None
+        dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False, expert_offsets=off)
+        # shared expert (its output went into the combine as the addend: its grad is dout)
+        dS = dout if pad_rows is None else dout.index_select(0, pad_rows)
+        dAs = dS @ Ws_down
+        dWs_down = _z.dense_wgrad(dS, As) if need[7] else None
+        G = torch.empty((x.shape[0], 2 * fs + E), dtype=x.dtype, device=x.device)
+        _z.swiglu_backward(dAs, Hs, out=G[:, :2 * fs])                              # [d up | d gate]
+        # gate projection, through the routing's analytic backward
+        _z.route_topk_backward(d_gates, p, idx, E, x.dtype, out=G[:, 2 * fs:])     # d_logits
+        dx_dense = G @ W3                                   # shared expert + gate input grads
+        dW3 = _z.dense_wgrad(G, x) if need[1] or need[5] or need[6] else None
+        dx = _z.sum_k(dXe, k, add0=dx_dense)
+        part = (lambda a, b: None) if dW3 is None else (lambda a, b: dW3[a:b])
+        return (dx, part(2 * fs, 2 * fs + E), None, dW1, dW2, part(fs, 2 * fs), part(0, fs), dWs_down,
+                None, None, None, None, None)
 
 
 class MoELayer(nn.Module):
@@ -51,13 +120,42 @@ class MoELayer(nn.Module):
         # GLUMLP's ParallelExperts init at std 0.02; re-init at the config's 1/sqrt(d)
         # (moe_layer.py:27-36).
         self.reset_routed_expert_parameters()
+        # bf16 on the device: the whole layer as one autograd function (_FusedMoELayer);
+        # False runs the module composition (same forward values and weight grads)
+        self.fused_layer = True
 
     def reset_routed_expert_parameters(self):
         std = self.config.initializer_range
         nn.init.normal_(self.routed_experts.experts.weight, mean=0.0, std=std)
         nn.init.normal_(self.routed_experts.output_experts.weight, mean=0.0, std=std)
 
+    def _fused_weights(self, x):
+        """The layer's weights for _FusedMoELayer, or None where the module composition runs
+        (not bf16 on the device, autocast, the routed experts' unfused path)."""
+        se = self.shared_experts
+        ws = (self.gate.weight, self.routed_experts.experts.weight, self.routed_experts.output_experts.weight,
+              se.gate_proj.weight, se.up_proj.weight, se.down_proj.weight)
+        ok = (self.fused_layer and self.routed_experts.fused and not torch.is_autocast_enabled()
+              and x.dim() == 3 and x.is_cuda and x.dtype == torch.bfloat16
+              and all(w.is_cuda and w.dtype == torch.bfloat16 for w in ws)
+              and self.gate.top_k == self.routed_experts.top_k
+              and ws[4].shape[0] % 8 == 0 and ws[0].shape[0] % 8 == 0)    # 16-byte rows of the dH | d_logits buffer
+        return ws if ok else None
+
     def forward(self, hidden_states, unpad_indices=None):
+        ws = self._fused_weights(hidden_states)
+        if ws is not None:
+            bsz, seq_len, h = hidden_states.shape
+            flat = hidden_states.reshape(bsz * seq_len, h)
+            stash = {}
+            pad = () if unpad_indices is None else (unpad_indices, bsz * seq_len)
+            x = flat if unpad_indices is None else index_first_axis(flat, unpad_indices)
+            out, topk_idx = _FusedMoELayer.apply(x, ws[0], self.gate.expert_biases, *ws[1:], self.gate.top_k,
+                                                 self.routed_experts.num_experts, stash, *pad)
+            self.routed_experts.last_expert_offsets = stash["expert_offsets"]
+            if unpad_indices is None:
+                return out.view(bsz, seq_len, h), topk_idx.view(bsz, seq_len, -1)
+            return out.view(bsz, seq_len, h), pad_input(topk_idx, unpad_indices, bsz, seq_len)
         if unpad_indices is not None:
             bsz, seq_len = hidden_states.shape[:2]
             flat = hidden_states.reshape(bsz * seq_len, hidden_states.shape[-1])

@@ -37,7 +37,7 @@ SIGNATURES = {
     "zmoe_status_string": (ctypes.c_char_p, [I32]),
     "zmoe_last_error": (ctypes.c_char_p, []),
     "zmoe_route_topk": (I32, [P, I32, I64, I32, I32, P, I32, P, P, P, P]),
-    "zmoe_route_topk_backward": (I32, [P, P, P, I64, I32, I32, P, I32, P]),
+    "zmoe_route_topk_backward": (I32, [P, P, P, I64, I32, I32, P, I64, I32, P]),
     "zmoe_bincount": (I32, [P, I64, I32, P, P]),
     "zmoe_sort_workspace_bytes": (SZ, [I64, I32]),
     "zmoe_flatten_sort_count": (I32, [P, I64, I32, P, P, P, P, P, SZ, P]),
@@ -58,7 +58,7 @@ SIGNATURES = {
     "zmoe_combine_backward_rows": (I32, [P, P, P, I64, P, P, I64, I32, I64, I32, P, P, P]),
     "zmoe_sum_k": (I32, [P, I64, I32, I64, I32, P, P, P, P]),
     "zmoe_swiglu": (I32, [P, I64, I64, I32, P, P]),
-    "zmoe_swiglu_backward": (I32, [P, P, I64, I64, I32, P, P]),
+    "zmoe_swiglu_backward": (I32, [P, P, I64, I64, I32, P, I64, P]),
     "zmoe_bias_update": (I32, [P, I32, F32, P, P]),
     "zmoe_newton_schulz5_workspace_bytes": (SZ, [I64, I64, I64]),
     "zmoe_newton_schulz5": (I32, [P, I64, I64, I64, I32, F32, F32, F32, P, SZ, P]),
@@ -89,7 +89,7 @@ def load():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.zmoe_abi_version() != 1:
+        if lib.zmoe_abi_version() != 2:
             raise ImportError("libzmoe_hip.so ABI version mismatch")
         _lib = lib
     return _lib

@@ -80,13 +80,17 @@ def route_topk(logits: torch.Tensor, expert_biases: torch.Tensor, k: int, round_
 
 
 def route_topk_backward(d_weight: torch.Tensor, topk_prob: torch.Tensor, topk_idx: torch.Tensor, E: int,
-                        dtype: torch.dtype) -> torch.Tensor:
-    dev = _require_cuda(d_weight, topk_prob, topk_idx)
+                        dtype: torch.dtype, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """d_logits [T, E]; ``out`` may be a column slice of a wider row-major buffer."""
+    dev = _require_cuda(d_weight, topk_prob, topk_idx, out)
     T, k = topk_idx.shape
     dw = d_weight.to(torch.float32).contiguous()
-    out = torch.empty((T, E), dtype=dtype, device=dev)
+    if out is None:
+        out = torch.empty((T, E), dtype=dtype, device=dev)
+    elif out.shape != (T, E) or out.dtype != dtype or (T > 1 and out.stride(1) != 1):
+        raise ValueError("route_topk_backward: out must be [T, E] of the logits dtype with unit column stride")
     L.call("zmoe_route_topk_backward", _ptr(dw), _ptr(topk_prob.contiguous()), _ptr(topk_idx.contiguous()), T, E,
-           k, _ptr(out), _DT[dtype], _stream(dev))
+           k, _ptr(out), out.stride(0), _DT[dtype], _stream(dev))
     return out
 
 
@@ -408,14 +412,19 @@ def swiglu(H: torch.Tensor) -> torch.Tensor:
     return A
 
 
-def swiglu_backward(dA: torch.Tensor, H: torch.Tensor) -> torch.Tensor:
-    dev = _require_cuda(dA, H)
+def swiglu_backward(dA: torch.Tensor, H: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dH [R, 2f] from (dA [R, f], H [R, 2f]); ``out`` may be a column slice of a wider buffer."""
+    dev = _require_cuda(dA, H, out)
     H = H.contiguous()
     dA = dA.to(H.dtype).contiguous()
     R, two_f = H.shape
-    dH = torch.empty_like(H)
-    L.call("zmoe_swiglu_backward", _ptr(dA), _ptr(H), R, two_f // 2, _dtype_code(H), _ptr(dH), _stream(dev))
-    return dH
+    if out is None:
+        out = torch.empty_like(H)
+    elif out.shape != H.shape or out.dtype != H.dtype or (R > 1 and out.stride(1) != 1):
+        raise ValueError("swiglu_backward: out must be [R, 2f] of H's dtype with unit column stride")
+    L.call("zmoe_swiglu_backward", _ptr(dA), _ptr(H), R, two_f // 2, _dtype_code(H), _ptr(out), out.stride(0),
+           _stream(dev))
+    return out
 
 
 def bias_update_(expert_biases: torch.Tensor, expert_offsets: torch.Tensor, update_rate: float) -> torch.Tensor:

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define ZMOE_ABI_VERSION 1
+#define ZMOE_ABI_VERSION 2
 
 /* element types */
 enum { ZMOE_DTYPE_F32 = 0, ZMOE_DTYPE_BF16 = 1 };
@@ -61,10 +61,12 @@ int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, int E, int 
                     void* stream);
 
 /* Autograd of modeling/moe_gate.py:27,33-34: d_weight [T, k] f32 ->
- * d_logits [T, E] (dense, zeros off the selected experts), dtype F32/BF16. */
+ * d_logits [T, E] (dense, zeros off the selected experts), dtype F32/BF16,
+ * rows ld_d_logits >= E elements apart (E for a packed [T, E]). */
 int zmoe_route_topk_backward(const float* d_weight, const float* topk_prob,
                              const int64_t* topk_idx, int64_t T, int E, int k,
-                             void* d_logits, int d_logits_dtype, void* stream);
+                             void* d_logits, int64_t ld_d_logits, int d_logits_dtype,
+                             void* stream);
 
 /* ---------------------------------------------------------------------------
  * Counting and sorting — scattermoe/parallel_experts.py:6-28.
@@ -230,10 +232,11 @@ int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype,
                const void* add0, const void* add1, void* out, void* stream);
 
 /* scattermoe/mlp.py:101-102 stand-alone (shapes the fused kernels reject):
- * A = silu(H[:, f:]) * H[:, :f]; and its backward dH from (dA, H). */
+ * A = silu(H[:, f:]) * H[:, :f]; and its backward dH from (dA, H), rows of dH
+ * ld_dh >= 2f elements apart (2f for a packed [R, 2f]). */
 int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void* A, void* stream);
 int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f,
-                         int dtype, void* dH, void* stream);
+                         int dtype, void* dH, int64_t ld_dh, void* stream);
 
 /* main.py:161-175 (aux-loss-free bias update) from the sort's offsets:
  *   counts = diff(expert_offsets); b += rate * sign(mean(counts) - counts)    */

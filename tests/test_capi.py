@@ -43,7 +43,7 @@ def test_pure_host_entry_points():
     from zmoe import _lib
 
     lib = _lib.load()
-    assert lib.zmoe_abi_version() == 1
+    assert lib.zmoe_abi_version() == 2
     assert lib.zmoe_status_string(0) == b"ok"
     assert lib.zmoe_status_string(4) == b"misaligned pointer or stride"
     # workspace sizing is host arithmetic: header + one int32 per (tile, bucket)

@@ -96,6 +96,44 @@ def test_layer_fused_matches_composition_fp32(hip_device):
     run_and_compare(700, 128, 16, 4, 96, 1, torch.float32, hip_device, fused=False, seed=3)
 
 
+@pytest.mark.parametrize("unpad", [False, True])
+def test_fused_layer_matches_composition_bf16(hip_device, unpad):
+    """The layer as one autograd function (bf16) against the module composition: the same
+    routing and output bit for bit (same kernels, same order), and the same grads of the
+    routed experts' and the shared down projection's weights. The gate's and the shared
+    up/gate projections' weight grads come from one split-K launch over their
+    concatenated output grads (its split count may differ), and the hidden states' grad
+    sums its parts with one rounding: those within the bf16 tolerance."""
+    from modeling.model_config import ModelConfig
+    from modeling.moe_layer import MoELayer
+
+    torch.manual_seed(2)
+    cfg = ModelConfig(hidden_size=256, intermediate_size=128, n_experts=18, n_shared_experts=2,
+                      n_experts_per_token=4)
+    layer = MoELayer(cfg).to(hip_device).to(torch.bfloat16)
+    layer.gate.expert_biases.data = (0.1 * torch.randn(16)).to(hip_device)
+    B, S = 2, 300
+    valid = torch.tensor([i for i in range(B * S) if (i % 9) != 4], device=hip_device) if unpad else None
+    h = torch.randn(B, S, 256, device=hip_device).to(torch.bfloat16)
+    dout = torch.randn(B, S, 256, device=hip_device).to(torch.bfloat16)
+    runs = []
+    for fused in (True, False):
+        layer.fused_layer = fused
+        layer.zero_grad(set_to_none=True)
+        x = h.clone().requires_grad_(True)
+        out, idx = layer(x, unpad_indices=valid)
+        out.backward(dout)
+        runs.append((out, idx, x.grad, {n: p.grad for n, p in layer.named_parameters()}))
+    (o1, i1, g1, p1), (o0, i0, g0, p0) = runs
+    assert torch.equal(i1, i0) and torch.equal(o1, o0)
+    for n in p0:
+        if n.startswith("routed_experts.") or n == "shared_experts.down_proj.weight":
+            assert torch.equal(p1[n], p0[n]), n
+        else:
+            assert_close(np64(p1[n]), np64(p0[n]), **TOL[torch.bfloat16], what=n)
+    assert_close(np64(g1), np64(g0), **TOL[torch.bfloat16], what="dx fused vs composition")
+
+
 def test_layer_unpad_indices(hip_device):
     from modeling.model_config import ModelConfig
     from modeling.moe_layer import MoELayer

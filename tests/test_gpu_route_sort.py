@@ -66,6 +66,10 @@ def test_route_backward(hip_device, dtype):
     dz = ops.route_topk_backward(dw.to(hip_device), p, idx, E, torch.float32)
     ref = O.route_topk_backward(dw.numpy(), p.cpu().numpy(), idx.cpu().numpy(), E)
     assert_close(dz.cpu().numpy(), ref, rtol=1e-5, atol=1e-6, what="d_logits")
+    # into the trailing columns of a wider buffer (rows 40 + E apart); the rest is left alone
+    buf = torch.full((T, 40 + E), 7.0, device=hip_device)
+    ops.route_topk_backward(dw.to(hip_device), p, idx, E, torch.float32, out=buf[:, 40:])
+    assert torch.equal(buf[:, 40:], dz) and bool((buf[:, :40] == 7.0).all())
 
 
 @pytest.mark.parametrize("T,E,k,skew", [(2048, 8, 2, 0.0), (16384, 64, 8, 0.0), (32768, 128, 8, 0.0),

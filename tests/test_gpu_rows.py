@@ -85,6 +85,10 @@ def test_swiglu(hip_device, dtype):
     assert_close(np64(A), O.swiglu(np64(H)), **TOL[dtype], what="swiglu")
     dH = ops.swiglu_backward(dA.to(hip_device), H.to(hip_device))
     assert_close(np64(dH), O.swiglu_backward(np64(dA), np64(H)), **TOL[dtype], what="swiglu_backward")
+    # into the leading columns of a wider buffer: the rest of each row is left alone
+    buf = torch.full((333, 2 * 768 + 24), 7.0, dtype=dtype, device=hip_device)
+    ops.swiglu_backward(dA.to(hip_device), H.to(hip_device), out=buf[:, :2 * 768])
+    assert torch.equal(buf[:, :2 * 768], dH) and bool((buf[:, 2 * 768:] == 7.0).all())
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
