@@ -302,6 +302,12 @@ struct RowsParams {
   int n_tiles;
   uint32_t a_bytes;       // addressable bytes from p.a (buffer-resource range)
   uint32_t b_bytes;       // addressable bytes of one expert's weights
+  // EPI_SWIGLU_BWD (bf16), when A holds unscaled rows: row_scale[i] scales row i of dA
+  // after the GEMM, and row_dots[i * dots_ld + c / 64] receives sum_c dA_unscaled * A
+  // over each 64-column block c of row i (A = silu(gate) * h, as the forward stored it)
+  const float* row_scale;
+  float* row_dots;
+  int dots_ld;
 };
 
 struct WgradParams {
@@ -1089,7 +1095,8 @@ constexpr int EPI_BATCH = 8;
 template <int BM, int BN, int EPI, int MI, int NI>
 __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st, const int* row_table,
                                                    const f32x16_t (&acc)[MI][NI], int e, int64_t row0, int rows,
-                                                   int nt, int wm0, int wn0, int mt = 0) {
+                                                   int nt, int wm0, int wn0, int mt = 0,
+                                                   const float* scale_table = nullptr) {
   using S = WaveStage<NI * 32>;
   constexpr int VEC = 8;
   const int lane = threadIdx.x & 63;
@@ -1173,15 +1180,25 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
     }
   };
   if (has_g) load_globals(0, 0);
+  // SwiGLU backward of scaled rows: lanes 8 j .. 8 j + 7 of an item hold the 64 columns of
+  // one row (8 chunks of 8), so a row's partial dot product is a sum over 3 lane bits
+  const bool dots = EPI == EPI_SWIGLU_BWD && p.row_dots != nullptr;
+  static_assert(EPI != EPI_SWIGLU_BWD || S::CPR == 8, "one row per 8 lanes");
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int cur = i & 1;
     uint4 tv[B];
     int orow[B];
+    float rsc[B], dot[B];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       tv[u] = *reinterpret_cast<const uint4*>(st + (item_rl(i, u) - wm0) * S::PITCH + item_cc(i, u) * 16);
       orow[u] = row_table[item_rl(i, u)];
+      rsc[u] = 1.f;
+      dot[u] = 0.f;
+      if constexpr (EPI == EPI_SWIGLU_BWD) {
+        if (dots) rsc[u] = scale_table[item_rl(i, u)];
+      }
     }
     if (has_g && i + 1 < NB) load_globals(i + 1, cur ^ 1);
 #pragma unroll
@@ -1220,11 +1237,28 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           const float sg = sigmoid_fast(gt[v]);
+          if (dots) {  // dA = scale * (unscaled dA), stored in bf16; the dot uses the unscaled values
+            dot[u] += da[v] * to_f32(bf16_bits(gt[v] * sg * h[v]));  // A = silu(gate) * h in bf16
+            da[v] = to_f32(bf16_bits(rsc[u] * da[v]));
+          }
           dh[v] = da[v] * gt[v] * sg;
           dg[v] = da[v] * h[v] * sg * (1.f + gt[v] * (1.f - sg));
         }
         st_out(C + o * p.ldc + col, pack_chunk(dh, uint16_t{}));
         st_out(C + o * p.ldc + p.half + col, pack_chunk(dg, uint16_t{}));
+      }
+    }
+    if constexpr (EPI == EPI_SWIGLU_BWD) {
+      if (dots) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          float s = dot[u];
+          s += __shfl_xor(s, 1, 64);
+          s += __shfl_xor(s, 2, 64);
+          s += __shfl_xor(s, 4, 64);
+          if ((lane & 7) == 0 && item_rl(i, u) < rows && ncol0 < p.N)
+            p.row_dots[(row0 + item_rl(i, u)) * p.dots_ld + ncol0 / 64] = s;
+        }
       }
     }
   }
@@ -1444,20 +1478,28 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
   // (With 8 waves, the table is written by waves 0-3, which run the loads.)
   static_assert(BM <= 256, "row table written by the first 256 threads");
   int* row_table = reinterpret_cast<int*>(smem + bf16_stage_bytes<BM, BN, NW>());
+  float* scale_table = reinterpret_cast<float*>(row_table + BM);
   int orow_v = 0;
+  float scale_v = 1.f;
   if (threadIdx.x < BM) {
     const int rl = (int)threadIdx.x;
     const int64_t i = row0 + (rl < rows ? rl : 0);
     orow_v = p.c_rows ? reinterpret_cast<const int*>(p.c_rows)[2 * i] : (int)i;
+    if constexpr (EPI == EPI_SWIGLU_BWD) {
+      if (p.row_scale != nullptr) scale_v = p.row_scale[i];
+    }
   }
   auto hook = [&] {
-    if (threadIdx.x < BM) row_table[threadIdx.x] = orow_v;
+    if (threadIdx.x < BM) {
+      row_table[threadIdx.x] = orow_v;
+      if constexpr (EPI == EPI_SWIGLU_BWD) scale_table[threadIdx.x] = scale_v;
+    }
   };
   kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
   // every wave is done with the operand stages (and has written its row-table entries)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,
-                                  nt, wm0, wn0, tile.mt);
+                                  nt, wm0, wn0, tile.mt, scale_table);
 }
 
 // fp32 output straight from the accumulators (split-K partials; no rounding): lane
@@ -1657,7 +1699,7 @@ constexpr int rows_lds_bytes() {
 // the epilogue works from registers.
 template <int BM, int BN, int NW = 4>
 constexpr int bf16_lds_bytes() {
-  constexpr int main_loop = bf16_stage_bytes<BM, BN, NW>() + BM * 4;  // stages / staging + output-row table
+  constexpr int main_loop = bf16_stage_bytes<BM, BN, NW>() + BM * 8;  // stages / staging + row and scale tables
   constexpr int decode = (kGemmMaxE + 4 + 16) * 4;
   return main_loop > decode ? main_loop : decode;
 }
@@ -2095,6 +2137,92 @@ extern "C" int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const vo
   p.a_bytes = (uint32_t)a_span;
   p.b_bytes = (uint32_t)b_span;
   return dispatch_rows<true, EPI_SWIGLU_BWD>(dtype, p, R, (int)f, as_stream(stream));
+}
+
+namespace zmoe {
+// gates [R] in slot order -> sorted order (the row scales of the dA GEMM)
+__global__ __launch_bounds__(256) void gather_gates_kernel(const float* __restrict__ gates,
+                                                           const int64_t* __restrict__ ss, int64_t R,
+                                                           float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < R) out[i] = gates[ss[i]];
+}
+// d_gates[ss[i]] = sum of row i's partial dot products, in column-block order
+__global__ __launch_bounds__(256) void gate_dots_kernel(const float* __restrict__ dots, int P,
+                                                        const int64_t* __restrict__ ss, int64_t R,
+                                                        float* __restrict__ d_gates) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= R) return;
+  float s = 0.f;
+  for (int q = 0; q < P; ++q) s += dots[i * P + q];
+  d_gates[ss[i]] = s;
+}
+}  // namespace zmoe
+
+extern "C" size_t zmoe_glu_w2_backward_dh_gates_workspace_bytes(int64_t R, int64_t f) {
+  if (R < 0 || f < 1) return 0;
+  return (size_t)align_up(R * 4, 256) + (size_t)align_up(R * cdiv(f, 64) * 4, 256);
+}
+
+extern "C" int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k, const void* W2, const void* H,
+                                             const int64_t* sorted_expert_idxs,
+                                             const int64_t* sorted_scattered_idxs, const int64_t* expert_offsets,
+                                             const float* gates, int64_t d, int64_t f, int E, int dtype, void* dH,
+                                             float* d_gates, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  (void)sorted_expert_idxs;
+  ZMOE_REQUIRE(dtype == ZMOE_DTYPE_BF16, ZMOE_ERR_DTYPE, "glu_w2_backward_dh_gates: bf16 only (dtype %d)", dtype);
+  ZMOE_REQUIRE(T >= 0 && k >= 1 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE, ZMOE_ERR_SHAPE,
+               "glu_w2_backward_dh_gates: bad sizes");
+  ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w2_backward_dh_gates: d/f too large");
+  const int64_t R = T * k;
+  ZMOE_REQUIRE(R < kMaxRows, ZMOE_ERR_SHAPE, "glu_w2_backward_dh_gates: T * k must be below 2^31");
+  if (R == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(dout && W2 && H && dH && sorted_scattered_idxs && expert_offsets && gates && d_gates && workspace,
+               ZMOE_ERR_NULL, "glu_w2_backward_dh_gates: null pointer");
+  ZMOE_REQUIRE(workspace_bytes >= zmoe_glu_w2_backward_dh_gates_workspace_bytes(R, f), ZMOE_ERR_WORKSPACE,
+               "glu_w2_backward_dh_gates: workspace too small");
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(d % v == 0 && f % v == 0 && aligned16(dout) && aligned16(W2) && aligned16(H) && aligned16(dH) &&
+                   aligned16(workspace),
+               ZMOE_ERR_ALIGN, "glu_w2_backward_dh_gates: d and f must be multiples of %d elements", v);
+  float* scale = reinterpret_cast<float*>(workspace);
+  float* dots = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + align_up(R * 4, 256));
+  const int P = (int)cdiv(f, 64);
+  RowsParams p{};
+  p.a = dout;  // sorted row i reads token ss[i] / k
+  p.lda = d;
+  p.a_rows = sorted_scattered_idxs;
+  p.a_div = k;
+  p.b = W2;
+  p.b_estride = d * f;
+  p.ldb = f;
+  p.c = dH;
+  p.ldc = 2 * f;
+  p.aux = H;
+  p.ld_aux = 2 * f;
+  p.offsets = expert_offsets;
+  p.K = (int)d;
+  p.N = (int)f;
+  p.E = E;
+  p.half = (int)f;
+  p.row_scale = scale;
+  p.row_dots = dots;
+  p.dots_ld = P;
+  const int64_t a_span = span_bytes(T, d, d, dtype), b_span = span_bytes(d, f, f, dtype);
+  ZMOE_REQUIRE(a_span <= kMaxSpan && b_span <= kMaxSpan, ZMOE_ERR_SHAPE,
+               "glu_w2_backward_dh_gates: dout or one expert's W2 spans more than 2 GiB");
+  p.a_bytes = (uint32_t)a_span;
+  p.b_bytes = (uint32_t)b_span;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid((unsigned)cdiv(R, 256)), block(256);
+  hipLaunchKernelGGL(gather_gates_kernel, grid, block, 0, s, gates, sorted_scattered_idxs, R, scale);
+  int rc = check_launch("glu_w2_backward_dh_gates: gather");
+  if (rc) return rc;
+  rc = dispatch_rows<true, EPI_SWIGLU_BWD>(dtype, p, R, (int)f, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(gate_dots_kernel, grid, block, 0, s, dots, P, sorted_scattered_idxs, R, d_gates);
+  return check_launch("glu_w2_backward_dh_gates: gate sums");
 }
 
 extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m,

@@ -131,8 +131,8 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
 // d_gates[t,j] = <Y[t*k+j], dout[t]>; grouped[inverse[t*k+j]] = g[t,j] * dout[t].
 // KM: a compile-time bound on k (slot arrays sized KM; slots j >= k are skipped).
 // dout_rows (optional): token t's row of dout (the padded layout's gradient read in place);
-// a row outside [0, dout_total) reads as zero.
-template <typename T, int KM>
+// a row outside [0, dout_total) reads as zero. DOTS = false: the grouped rows only (no Y).
+template <typename T, int KM, bool DOTS>
 __global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
     const T* __restrict__ Y, const T* __restrict__ dout, const int64_t* __restrict__ dout_rows, int64_t dout_total,
     const float* __restrict__ g, const int32_t* __restrict__ inverse, int64_t T_, int k, int64_t d,
@@ -168,23 +168,28 @@ __global__ __launch_bounds__(kRowThreads) void combine_backward_kernel(
         for (int q = 0; q < VN; ++q) go[q] = 0.f;
       }
       uint4 yv[KM];
+      if constexpr (DOTS) {
 #pragma unroll
-      for (int j = 0; j < KM; ++j) yv[j] = ld16_stream(Y + (t * k + (j < k ? j : k - 1)) * d + ch * VN);
+        for (int j = 0; j < KM; ++j) yv[j] = ld16_stream(Y + (t * k + (j < k ? j : k - 1)) * d + ch * VN);
+      }
 #pragma unroll
       for (int j = 0; j < KM; ++j) {
-        float y[VN], sv[VN];
-        unpack_chunk(yv[j], y, T{});
-        float acc = 0.f;
+        float sv[VN];
 #pragma unroll
-        for (int q = 0; q < VN; ++q) {
-          acc = fmaf(y[q], go[q], acc);
-          sv[q] = w[j] * go[q];
+        for (int q = 0; q < VN; ++q) sv[q] = w[j] * go[q];
+        if constexpr (DOTS) {
+          float y[VN];
+          unpack_chunk(yv[j], y, T{});
+          float acc = 0.f;
+#pragma unroll
+          for (int q = 0; q < VN; ++q) acc = fmaf(y[q], go[q], acc);
+          dot[j] += acc;
         }
-        dot[j] += acc;
         if (j < k) st16(grouped + (int64_t)dst[j] * d + ch * VN, pack_chunk(sv, T{}));
       }
     }
   }
+  if constexpr (!DOTS) return;
   // reduce the partial dots over the row's threads (whole waves)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -385,9 +390,10 @@ int combine_backward_impl(const void* Y, const void* grad_out, const int64_t* gr
   ZMOE_REQUIRE(T >= 0 && k >= 1 && k <= kMaxFanOut && d >= 0, ZMOE_ERR_SHAPE,
                "combine_backward: need 1 <= k <= %d", kMaxFanOut);
   if (T == 0) return ZMOE_OK;
-  ZMOE_REQUIRE(Y && grad_out && gates && inverse && d_gates && grouped_grad_out, ZMOE_ERR_NULL,
-               "combine_backward: null pointer");
-  ZMOE_REQUIRE(d % vec_of(dtype) == 0 && rows_aligned(dtype, Y, d) && rows_aligned(dtype, grad_out, d) &&
+  ZMOE_REQUIRE(grad_out && gates && inverse && grouped_grad_out && (Y != nullptr) == (d_gates != nullptr),
+               ZMOE_ERR_NULL, "combine_backward: null pointer");
+  ZMOE_REQUIRE(d % vec_of(dtype) == 0 && (Y == nullptr || rows_aligned(dtype, Y, d)) &&
+                   rows_aligned(dtype, grad_out, d) &&
                    rows_aligned(dtype, grouped_grad_out, d),
                ZMOE_ERR_ALIGN, "combine_backward: d must be a multiple of %d, pointers 16-byte aligned",
                vec_of(dtype));
@@ -395,9 +401,14 @@ int combine_backward_impl(const void* Y, const void* grad_out, const int64_t* gr
   const dim3 grid((unsigned)cdiv(T, m.rpb)), block(kRowThreads);
   auto launch = [&](auto km, auto tt) {
     using TT = decltype(tt);
-    hipLaunchKernelGGL((combine_backward_kernel<TT, decltype(km)::value>), grid, block, 0, as_stream(stream),
-                       (const TT*)Y, (const TT*)grad_out, grad_rows, grad_total, gates, inverse, T, k, d,
-                       d_gates, (TT*)grouped_grad_out, m.tpr);
+    if (Y != nullptr)
+      hipLaunchKernelGGL((combine_backward_kernel<TT, decltype(km)::value, true>), grid, block, 0,
+                         as_stream(stream), (const TT*)Y, (const TT*)grad_out, grad_rows, grad_total, gates, inverse,
+                         T, k, d, d_gates, (TT*)grouped_grad_out, m.tpr);
+    else
+      hipLaunchKernelGGL((combine_backward_kernel<TT, decltype(km)::value, false>), grid, block, 0,
+                         as_stream(stream), (const TT*)Y, (const TT*)grad_out, grad_rows, grad_total, gates, inverse,
+                         T, k, d, d_gates, (TT*)grouped_grad_out, m.tpr);
   };
   auto by_k = [&](auto tt) {
     if (k <= 2) launch(std::integral_constant<int, 2>{}, tt);

@@ -128,6 +128,7 @@ inline int dtype_size(int dt) { return dt == ZMOE_DTYPE_BF16 ? 2 : 4; }
 inline bool dtype_ok(int dt) { return dt == ZMOE_DTYPE_BF16 || dt == ZMOE_DTYPE_F32; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t align_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 
 }  // namespace zmoe
 

@@ -34,7 +34,10 @@ class _FusedMoELayer(torch.autograd.Function):
     """The whole layer in one autograd function (bf16 on the device): gate projection and
     routing, shared expert, routed GLU experts, combine. It runs the same kernels in the
     same order as the module composition (MoEGate, ExpertMLP and GLUMLP's fused path) in
-    the forward, so the routing and output are the same values. The backward writes the
+    the forward, so the routing and output are the same values. The combine's backward is
+    folded into the dA GEMM (zmoe_glu_w2_backward_dh_gates: it reads the output grad's
+    rows in place and forms the gates' grad from its own products), so Y is not kept for
+    the backward and the only [T*k, d] pass left writes the gate-scaled rows for dW2. The backward writes the
     shared expert's dH and the gate's d_logits side by side into one [T, 2fs + E] buffer:
     one GEMM against [W_up; W_gate; W_router] gives both of their input grads, one split-K
     weight-grad launch all three weight grads, and the k-sum pass adds that input grad to
@@ -62,7 +65,7 @@ class _FusedMoELayer(torch.autograd.Function):
         Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
                                expert_offsets=off)
         out = _z.combine(Y, w, k, addend=S, out_rows=pad_rows, out_total=pad_total)  # moe_layer.py:48-56
-        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A, Y)
+        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A)
         ctx.k, ctx.E, ctx.fs = k, E, fs
         ctx.pad_rows = pad_rows
         ctx.mark_non_differentiable(idx)
@@ -70,19 +73,22 @@ class _FusedMoELayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, d_idx):
-        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A, Y = ctx.saved_tensors
+        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A = ctx.saved_tensors
         k, E, fs = ctx.k, ctx.E, ctx.fs
         need = ctx.needs_input_grad
         dout = dout.to(x.dtype).contiguous()
         pad_rows = ctx.pad_rows
-        # routed experts, as GLUExpertsFunction.backward (a padded grad is read in place)
-        d_gates, dYg = _z.combine_backward(Y, dout, w, inv, grad_rows=pad_rows)
-        dH = _z.glu_w2_backward_dh(dYg, W2, H, se, off)
-        dW2 = _z.group_bwd_w(dYg, A, off, E)[0] if need[4] else None
+        # the grad of the combine's inputs: dout for the shared expert's output (the addend),
+        # gates * dout[t] for the routed rows, <dout[t], Y> for the gates
+        dS = dout if pad_rows is None else dout.index_select(0, pad_rows)
+        # routed experts: the dA GEMM reads dS's rows in place and scales them by the gates
+        # after the product, from which it also forms d_gates (no pass over Y)
+        dH, d_gates = _z.glu_w2_backward_dh_gates(dS, W2, H, se, ss, off, k, w)
+        # gates * dout[t] in sorted order for dW2 (one read of each token's grad row)
+        dW2 = _z.group_bwd_w(_z.combine_backward(None, dS, w, inv)[1], A, off, E)[0] if need[4] else None
         dW1 = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)[0] if need[3] else None
         dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False, expert_offsets=off)
-        # shared expert (its output went into the combine as the addend: its grad is dout)
-        dS = dout if pad_rows is None else dout.index_select(0, pad_rows)
+        # shared expert
         dAs = dS @ Ws_down
         dWs_down = _z.dense_wgrad(dS, As) if need[7] else None
         G = torch.empty((x.shape[0], 2 * fs + E), dtype=x.dtype, device=x.device)

@@ -52,6 +52,8 @@ SIGNATURES = {
     "zmoe_rowwise_sum_product": (I32, [P, I32, P, I32, I64, I32, I64, P, I32, P]),
     "zmoe_glu_w1_forward": (I32, [P, I64, P, P, P, P, I64, I64, I64, I32, I32, I32, P, P, P]),
     "zmoe_glu_w2_backward_dh": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P, P]),
+    "zmoe_glu_w2_backward_dh_gates_workspace_bytes": (SZ, [I64, I64]),
+    "zmoe_glu_w2_backward_dh_gates": (I32, [P, I64, I32, P, P, P, P, P, P, I64, I64, I32, I32, P, P, P, SZ, P]),
     "zmoe_combine": (I32, [P, P, P, I64, I32, I64, I32, P, P]),
     "zmoe_combine_backward": (I32, [P, P, P, P, I64, I32, I64, I32, P, P, P]),
     "zmoe_combine_rows": (I32, [P, P, P, I64, I32, I64, I32, P, I64, P, P]),

@@ -313,6 +313,32 @@ def glu_w2_backward_dh(dYg: torch.Tensor, W2: torch.Tensor, H: torch.Tensor, sor
     return dH
 
 
+def glu_w2_backward_dh_gates(dout: torch.Tensor, W2: torch.Tensor, H: torch.Tensor, sorted_expert_idxs,
+                             sorted_scattered_idxs, expert_offsets, k: int, gates: torch.Tensor):
+    """glu_w2_backward_dh with the weighted combine's backward folded in (bf16): the A rows
+    are dout's rows read in place (sorted row i reads token s_i // k), scaled by gates[s_i]
+    after the GEMM, and the gates' grad <dout[t], Y[s]> is formed from the same products.
+    Returns (dH [T*k, 2f], d_gates [T, k] f32)."""
+    dev = _require_cuda(dout, W2, H, gates)
+    dout = _rows(dout).contiguous()
+    W2 = W2.contiguous()
+    E, d, f = W2.shape
+    T = dout.shape[0]
+    R = T * k
+    g = gates.reshape(-1).to(torch.float32).contiguous()
+    if g.numel() != R or H.shape != (R, 2 * f):
+        raise ValueError("glu_w2_backward_dh_gates: gates must hold T*k entries and H [T*k, 2f]")
+    dH = torch.empty((R, 2 * f), dtype=dout.dtype, device=dev)
+    d_gates = torch.empty((T, k), dtype=torch.float32, device=dev)
+    nbytes = L.load().zmoe_glu_w2_backward_dh_gates_workspace_bytes(R, f)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    with profiling.region("glu_w2_backward_dh", dev):
+        L.call("zmoe_glu_w2_backward_dh_gates", _ptr(dout), T, k, _ptr(W2), _ptr(H.contiguous()),
+               _ptr(sorted_expert_idxs), _ptr(_idx64(sorted_scattered_idxs)), _ptr(expert_offsets), _ptr(g), d, f,
+               E, _dtype_code(dout), _ptr(dH), _ptr(d_gates), _ptr(ws), nbytes, _stream(dev))
+    return dH, d_gates
+
+
 # --------------------------------------------------------------------- combine / reductions
 def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch.Tensor] = None,
             out_rows: Optional[torch.Tensor] = None, out_total: Optional[int] = None) -> torch.Tensor:
@@ -342,32 +368,33 @@ def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch
     return out
 
 
-def combine_backward(Y: torch.Tensor, grad_out: torch.Tensor, gates: torch.Tensor, inverse: torch.Tensor,
+def combine_backward(Y: Optional[torch.Tensor], grad_out: torch.Tensor, gates: torch.Tensor, inverse: torch.Tensor,
                      grad_rows: Optional[torch.Tensor] = None):
     """(d_gates [T, k] f32, grouped_grad_out [T*k, d] in sorted order).
 
     With ``grad_rows`` (int64 [T]) token t's gradient is row grad_rows[t] of the padded
-    ``grad_out`` [rows, d], read in place.
+    ``grad_out`` [rows, d], read in place. ``Y = None``: only the grouped rows (d_gates None).
     """
     dev = _require_cuda(Y, grad_out, gates, inverse, grad_rows)
-    Y = Y.contiguous()
-    d = Y.shape[-1]
+    Y = None if Y is None else Y.contiguous()
+    d = grad_out.shape[-1]
+    dt = grad_out.dtype if Y is None else Y.dtype
     T, k = gates.shape
     g = gates.to(torch.float32).contiguous()
-    d_gates = torch.empty((T, k), dtype=torch.float32, device=dev)
-    grouped = torch.empty((T * k, d), dtype=Y.dtype, device=dev)
-    with profiling.region("combine_backward", dev):
+    d_gates = None if Y is None else torch.empty((T, k), dtype=torch.float32, device=dev)
+    grouped = torch.empty((T * k, d), dtype=dt, device=dev)
+    with profiling.region("combine_backward" if Y is not None else "combine_backward_scale", dev):
         if grad_rows is None:
-            go = grad_out.reshape(T, d).to(Y.dtype).contiguous()
-            L.call("zmoe_combine_backward", _ptr(Y), _ptr(go), _ptr(g), _ptr(inverse), T, k, d, _dtype_code(Y),
+            go = grad_out.reshape(T, d).to(dt).contiguous()
+            L.call("zmoe_combine_backward", _ptr(Y), _ptr(go), _ptr(g), _ptr(inverse), T, k, d, _dtype_code(grouped),
                    _ptr(d_gates), _ptr(grouped), _stream(dev))
         else:
-            go = grad_out.reshape(-1, d).to(Y.dtype).contiguous()
+            go = grad_out.reshape(-1, d).to(dt).contiguous()
             rows = _idx64(grad_rows)
             if rows.numel() != T:
                 raise ValueError("combine_backward: grad_rows must hold one row per token")
             L.call("zmoe_combine_backward_rows", _ptr(Y), _ptr(go), _ptr(rows), go.shape[0], _ptr(g), _ptr(inverse),
-                   T, k, d, _dtype_code(Y), _ptr(d_gates), _ptr(grouped), _stream(dev))
+                   T, k, d, _dtype_code(grouped), _ptr(d_gates), _ptr(grouped), _stream(dev))
     return d_gates, grouped
 
 

@@ -56,7 +56,7 @@ TRAFFIC_C3 = {
     "group_bwd_w#0": 2200162099,
     "group_bwd_w#1": 3903050547,
 }
-ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "sum_k")
+ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale", "sum_k")
 
 
 def gemm_flops(name: str, launch: int, T, d, k, f) -> float:
@@ -82,6 +82,7 @@ def row_bytes(name: str, T, d, E, k) -> float:
         "flatten_sort_count": R * 8 * 2 + R * 8 * 2 + R * 4,
         "combine": R * d * 2 + R * 4 + T * d * 2 + T * d * 2,
         "combine_backward": R * d * 2 + T * d * 2 + R * (4 + 4 + 4) + R * d * 2,
+        "combine_backward_scale": T * d * 2 + R * (4 + 4) + R * d * 2,   # without Y: no gate dots
         "sum_k": R * d * 2 + T * d * 2,
     }[name]
 

@@ -196,6 +196,24 @@ int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const void* H,
                             const int64_t* expert_offsets, int64_t R, int64_t d,
                             int64_t f, int E, int dtype, void* dH, void* stream);
 
+/* The same with the weighted combine's backward folded in (parallel_experts.py:
+ * 191-208 and the gate grads of :161-163 via ops.py:9-80, rowwise_sum_product),
+ * bf16 only. The A rows are the output grad's rows, read in place:
+ *   dYg[i] = gates[s_i] * dout[s_i / k]   (s_i = sorted_scattered_idxs[i]), so
+ *   dA[i]  = gates[s_i] * (dout[s_i / k] @ W2[e])   -> dH as above, and
+ *   d_gates[s_i] = <dout[s_i / k], Y[s_i]> = <dout[s_i / k] @ W2[e], A_i>,
+ * with A_i = silu(g) * h from H (as the forward stored it). dout [T, d], gates and
+ * d_gates [T * k] f32 in slot order; d_gates is written (not accumulated), in a
+ * fixed summation order. Workspace: zmoe_glu_w2_backward_dh_gates_workspace_bytes. */
+size_t zmoe_glu_w2_backward_dh_gates_workspace_bytes(int64_t R, int64_t f);
+int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k, const void* W2,
+                                  const void* H, const int64_t* sorted_expert_idxs,
+                                  const int64_t* sorted_scattered_idxs,
+                                  const int64_t* expert_offsets, const float* gates,
+                                  int64_t d, int64_t f, int E, int dtype, void* dH,
+                                  float* d_gates, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* scattermoe/parallel_experts.py:161-163 (gates @ output_expanded) plus the
  * residual sum of modeling/moe_layer.py:53:
  *   out[t, :] = addend[t, :] + sum_j gates[t, j] * Y[t * k + j, :]
@@ -206,7 +224,9 @@ int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t 
 /* scattermoe/parallel_experts.py:191-208 (rowwise_sum_product + group with
  * coeff=gates) in one pass over grad_out:
  *   d_gates[t, j] = sum_h Y[t*k+j, h] * grad_out[t, h]
- *   grouped_grad_out[inverse[t*k+j], :] = gates[t, j] * grad_out[t, :]       */
+ *   grouped_grad_out[inverse[t*k+j], :] = gates[t, j] * grad_out[t, :]
+ * Y and d_gates may both be NULL: then only grouped_grad_out is written (the
+ * gates' grad formed elsewhere, e.g. by zmoe_glu_w2_backward_dh_gates).       */
 int zmoe_combine_backward(const void* Y, const void* grad_out, const float* gates,
                           const int32_t* inverse, int64_t T, int k, int64_t d,
                           int dtype, float* d_gates, void* grouped_grad_out,

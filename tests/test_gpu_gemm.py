@@ -139,6 +139,37 @@ def test_glu_fused_forward_and_backward_dh(hip_device, dtype, T, d, f, E, k, ske
     assert_close(np64(dH), O.swiglu_backward(dA, np64(H)), **tol, what="dH")
 
 
+@pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
+                                            (1500, 256, 96, 16, 4, 1.5), (2, 64, 32, 8, 2, 0.0),
+                                            (1200, 200, 136, 4, 2, 0.3), (128, 512, 136, 64, 4, 1.5)])
+def test_glu_w2_backward_dh_gates(hip_device, T, d, f, E, k, skew):
+    """The dA GEMM with the combine's backward folded in (bf16): dH from dA = gates[s] *
+    (dout[s // k] @ W2[e]) and d_gates[s] = <dout[s // k], Y[s]>, Y = A W2^T, against the
+    float64 oracle on the device's H and A."""
+    from zmoe import ops
+
+    idx, se, ss, off, _ = _routing(T, E, k, skew, hip_device, seed=T + 3 * f)
+    g = gen(T + 2 * d + f)
+    dt = torch.bfloat16
+    x = torch.randn(T, d, generator=g).to(dt)
+    W1 = (torch.randn(E, 2 * f, d, generator=g) / d ** 0.5).to(dt)
+    W2 = (torch.randn(E, d, f, generator=g) / f ** 0.5).to(dt)
+    dout = torch.randn(T, d, generator=g).to(dt)
+    gates = torch.rand(T, k, generator=g) + 0.05
+    H, A = ops.glu_w1_forward(x.to(hip_device), W1.to(hip_device), se, ss, off, k)
+    dH, d_gates = ops.glu_w2_backward_dh_gates(dout.to(hip_device), W2.to(hip_device), H, se, ss, off, k,
+                                               gates.to(hip_device))
+    se_n, ss_n = se.cpu().numpy(), ss.cpu().numpy()
+    dYg = O.group(np64(dout), ss_n, coeff=gates.numpy().astype(np.float64), fan_out=k)
+    dA = O.scatter2scatter(dYg, np64(W2), se_n, ss_n, 1, x_grouped=True, y_grouped=True)
+    dA = O.bf16_round(dA.astype(np.float32)).astype(np.float64)  # dA is stored in bf16 before the epilogue
+    tol = TOL[dt]
+    assert_close(np64(dH), O.swiglu_backward(dA, np64(H)), **tol, what="dH")
+    Y = O.scatter2scatter(np64(A), np64(W2).transpose(0, 2, 1), se_n, ss_n, 1, x_grouped=True, y_grouped=False)
+    ref = O.rowwise_sum_product(Y.reshape(T, k, d), np64(dout))
+    assert_close(d_gates.cpu().numpy().astype(np.float64), ref, **tol, what="d_gates")
+
+
 @pytest.mark.parametrize("M,N,K,splits", [(1000, 128, 256, None), (1000, 128, 256, 3), (4100, 256, 512, 7),
                                           (4096, 136, 264, 1), (0, 128, 128, 4), (20000, 1536, 512, None)])
 def test_dense_wgrad_bf16(hip_device, M, N, K, splits):

@@ -54,6 +54,9 @@ def test_combine_and_backward(hip_device, dtype, T, d, k):
     assert_close(d_gates.cpu().numpy(), ref_dg, rtol=1e-5, atol=1e-4, what="d_gates")
     ref_grouped = O.group(np64(dout), ss.cpu().numpy(), coeff=gates.double().numpy().reshape(-1), fan_out=k)
     assert_close(np64(grouped), ref_grouped, **tol, what="grouped_grad_out")
+    # without Y: the same grouped rows, no gate grads
+    no_dg, grouped2 = ops.combine_backward(None, dout.to(hip_device), gates.to(hip_device), inv)
+    assert no_dg is None and torch.equal(grouped2, grouped)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
