@@ -35,6 +35,7 @@
 // The f32 kernels use the same tiling with VGPR-staged loads, 32-deep stages and
 // v_mfma_f32_32x32x2f32 (four per 16-byte fragment).
 #include <cstdlib>
+#include <type_traits>
 
 #include "zmoe_internal.h"
 
@@ -302,9 +303,10 @@ struct RowsParams {
   int n_tiles;
   uint32_t a_bytes;       // addressable bytes from p.a (buffer-resource range)
   uint32_t b_bytes;       // addressable bytes of one expert's weights
-  // EPI_SWIGLU_BWD (bf16), when A holds unscaled rows: row_scale[i] scales row i of dA
-  // after the GEMM, and row_dots[i * dots_ld + c / 64] receives sum_c dA_unscaled * A
-  // over each 64-column block c of row i (A = silu(gate) * h, as the forward stored it)
+  // bf16, per sorted row i (null: none). EPI_SWIGLU: the activation output is
+  // row_scale[i] * silu(gate) * h. EPI_SWIGLU_BWD, when A holds unscaled rows:
+  // row_scale[i] scales row i of dA after the GEMM, and row_dots[i * dots_ld + c / 64]
+  // receives sum_c dA_unscaled * silu(gate) * h over each 64-column block c of row i
   const float* row_scale;
   float* row_dots;
   int dots_ld;
@@ -315,7 +317,7 @@ struct WgradParams {
   int64_t lddy;
   const void* x;
   int64_t ldx;
-  const int64_t* x_rows;
+  const int64_t* x_rows;  // gather: source row of sorted row i = x_rows[i] / x_div (of DY with the DY gather)
   int x_div;
   int x_div_shift;  // log2(x_div) when x_div is a power of two, else -1
   void* dw;  // [E, Ndy, Kx]
@@ -1138,8 +1140,9 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
             float h[VEC], gt[VEC], a[VEC];
             unpack_chunk(hv[u], h, uint16_t{});
             unpack_chunk(gv[u], gt, uint16_t{});
+            const float rs = p.row_scale != nullptr ? scale_table[rl] : 1.f;
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) a[q] = silu_f(gt[q]) * h[q];
+            for (int q = 0; q < VEC; ++q) a[q] = rs * (silu_f(gt[q]) * h[q]);
             const int64_t o = orow[u];
             st_out(C + o * p.ldc + jj, hv[u]);
             st_out(C + o * p.ldc + p.half + jj, gv[u]);
@@ -1485,14 +1488,14 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
     const int rl = (int)threadIdx.x;
     const int64_t i = row0 + (rl < rows ? rl : 0);
     orow_v = p.c_rows ? reinterpret_cast<const int*>(p.c_rows)[2 * i] : (int)i;
-    if constexpr (EPI == EPI_SWIGLU_BWD) {
+    if constexpr (EPI == EPI_SWIGLU_BWD || EPI == EPI_SWIGLU) {
       if (p.row_scale != nullptr) scale_v = p.row_scale[i];
     }
   }
   auto hook = [&] {
     if (threadIdx.x < BM) {
       row_table[threadIdx.x] = orow_v;
-      if constexpr (EPI == EPI_SWIGLU_BWD) scale_table[threadIdx.x] = scale_v;
+      if constexpr (EPI == EPI_SWIGLU_BWD || EPI == EPI_SWIGLU) scale_table[threadIdx.x] = scale_v;
     }
   };
   kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
@@ -1527,9 +1530,11 @@ __device__ __forceinline__ void wgrad_epilogue_f32(const WgradParams& p, const f
 }
 
 // GATHER: 0 = x rows in sorted order; 1 = gathered, row = index >> shift; 2 = gathered,
-// row = index / x_div. Both gathered forms keep the K loop free of branches.
-template <int BM, int BN, int GATHER, bool OUT_F32 = false, int NW = 4>
+// row = index / x_div. Both gathered forms keep the K loop free of branches. DYG: the
+// gather applies to the DY rows instead (x rows then in sorted order).
+template <int BM, int BN, int GATHER, bool OUT_F32 = false, int NW = 4, bool DYG = false>
 __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
+  static_assert(!DYG || GATHER != 0, "a DY gather needs a gather mode");
   extern __shared__ __align__(16) char smem[];
   constexpr int KS = 64;
   using WG = WaveGrid<BM, BN, NW>;
@@ -1575,6 +1580,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   uint32_t src_off[KR];
   uint32_t pend = 0;  // this lane's index word for the next stage (lanes 0..KR-1 hold the wave's k-rows)
   const int64_t ldx2 = p.ldx * 2;
+  const int64_t ldg2 = DYG ? p.lddy * 2 : ldx2;  // row pitch of the gathered operand
   auto issue_idx = [&](int kt) -> uint32_t {
     const int pos = kt * KS + KR * wu + (int)(threadIdx.x & (KR - 1));
     return xr32[2 * (r_begin + (pos < nrows ? pos : nrows - 1))];
@@ -1594,35 +1600,45 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
 #pragma unroll
       for (int j = 0; j < KR; ++j) v[j] /= (uint32_t)p.x_div;
     }
-    // row byte offsets fit in 32 bits: x spans less than 2 GiB
+    // row byte offsets fit in 32 bits: the gathered operand spans less than 2 GiB
 #pragma unroll
-    for (int j = 0; j < KR; ++j) src_off[j] = base + j < nrows ? v[j] * (uint32_t)ldx2 : kOOBRow;
+    for (int j = 0; j < KR; ++j) src_off[j] = base + j < nrows ? v[j] * (uint32_t)ldg2 : kOOBRow;
+  };
+  // the gathered row offset of this lane's k-row for instruction qq of loader L: k-row
+  // qq * RPI + sub() of the wave's KR; qq is a compile-time constant here (unrolled), so
+  // the pick indexes the array with constants only (a select between array elements is
+  // turned back into a dynamically indexed array, i.e. scratch memory; the masked XOR
+  // keeps every index constant)
+  auto pick = [&](auto* loader_tag, int qq) -> uint32_t {
+    using L = typename std::remove_pointer<decltype(loader_tag)>::type;
+    static_assert(L::RPI == 2 || L::RPI == 4, "two or four k-rows per load instruction");
+    const int sub = L::sub();
+    const uint32_t m1 = 0u - (uint32_t)(sub & 1);
+    const uint32_t s0 = src_off[qq * L::RPI], s1 = src_off[qq * L::RPI + 1];
+    uint32_t v = s0 ^ ((s0 ^ s1) & m1);
+    if constexpr (L::RPI == 4) {
+      const uint32_t s2 = src_off[qq * L::RPI + 2], s3 = src_off[qq * L::RPI + 3];
+      const uint32_t hi = s2 ^ ((s2 ^ s3) & m1);
+      v = v ^ ((v ^ hi) & (0u - (uint32_t)((sub >> 1) & 1)));
+    }
+    return v;
   };
   auto dma = [&](int q, int buf, int kt, bool on) {
     lds_char* sa = lds + buf * kStage;
     lds_char* sb = sa + BM * KS * 2;
     const int64_t k0 = (int64_t)kt * KS;
     if (q < LA::NQ) {
-      const int64_t pitch = p.lddy * 2;
-      la.issue(q, stage_rsrc(dy_base, p.dy_bytes, (r_begin + k0) * pitch, ((int64_t)nrows - k0) * pitch, on), sa,
-               wu);
-    } else if constexpr (GATHER != 0) {
-      const int qq = q - LA::NQ;
-      // this lane's k-row is qq * RPI + sub of the wave's KR; qq is a compile-time
-      // constant here (unrolled), so the pick indexes the array with constants only
-      // (a select between array elements is turned back into a dynamically indexed
-      // array, i.e. scratch memory; the masked XOR keeps every index constant)
-      const int sub = LB::sub();
-      const uint32_t m1 = 0u - (uint32_t)(sub & 1);
-      const uint32_t s0 = src_off[qq * LB::RPI], s1 = src_off[qq * LB::RPI + 1];
-      uint32_t v = s0 ^ ((s0 ^ s1) & m1);
-      if constexpr (LB::RPI == 4) {
-        const uint32_t s2 = src_off[qq * LB::RPI + 2], s3 = src_off[qq * LB::RPI + 3];
-        const uint32_t hi = s2 ^ ((s2 ^ s3) & m1);
-        v = v ^ ((v ^ hi) & (0u - (uint32_t)((sub >> 1) & 1)));
+      if constexpr (DYG) {
+        // kOOBRow + coff and v + kOOB both stay below 2^32 and at or above 2^31 - 16
+        la.issue_at(q, make_rsrc(dy_base, on ? p.dy_bytes : 0u), sa, wu, pick((LA*)nullptr, q) + la.coff[q]);
+      } else {
+        const int64_t pitch = p.lddy * 2;
+        la.issue(q, stage_rsrc(dy_base, p.dy_bytes, (r_begin + k0) * pitch, ((int64_t)nrows - k0) * pitch, on),
+                 sa, wu);
       }
-      // kOOBRow + coff and v + kOOB both stay below 2^32 and at or above 2^31 - 16
-      lb.issue_at(qq, make_rsrc(x_base, on ? p.x_bytes : 0u), sb, wu, v + lb.coff[qq]);
+    } else if constexpr (GATHER != 0 && !DYG) {
+      const int qq = q - LA::NQ;
+      lb.issue_at(qq, make_rsrc(x_base, on ? p.x_bytes : 0u), sb, wu, pick((LB*)nullptr, qq) + lb.coff[qq]);
     } else {
       const int64_t pitch = ldx2;
       lb.issue(q - LA::NQ, stage_rsrc(x_base, p.x_bytes, (r_begin + k0) * pitch, ((int64_t)nrows - k0) * pitch, on),
@@ -1761,11 +1777,11 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   return check_launch("grouped wgrad kernel");
 }
 
-template <int GATHER, bool OUT_F32>
+template <int GATHER, bool OUT_F32, bool DYG = false>
 int launch_wgrad_big(const WgradParams& p, hipStream_t s) {
   constexpr int NW = kBigWaves;
-  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, NW>, bf16_lds_bytes<256, 256, NW>(), 256,
-                             256, p, s, NW * 64);
+  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, NW, DYG>, bf16_lds_bytes<256, 256, NW>(),
+                             256, 256, p, s, NW * 64);
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
@@ -1877,6 +1893,7 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(RowsParams p, int wtil
     if constexpr (EPI == EPI_SWIGLU) {
       // acc[4 q + u]: h of pair wt 16 + 8 q + 4 g + u for q = 0, 1; its gate at q + 2
       uint16_t* A2 = reinterpret_cast<uint16_t*>(p.c2);
+      const float rs = p.row_scale != nullptr ? p.row_scale[i] : 1.f;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int pr = wt * 16 + 8 * q + 4 * g;
@@ -1886,7 +1903,7 @@ __global__ __launch_bounds__(256) void stream_rows_kernel(RowsParams p, int wtil
         for (int u = 0; u < 4; ++u) {
           h[u] = to_f32(bf16_bits(acc[4 * q + u]));
           gt[u] = to_f32(bf16_bits(acc[4 * (q + 2) + u]));
-          a[u] = silu_f(gt[u]) * h[u];
+          a[u] = rs * (silu_f(gt[u]) * h[u]);
         }
         *reinterpret_cast<uint2*>(C + o * p.ldc + pr) = pack4_bf16(h);
         *reinterpret_cast<uint2*>(C + o * p.ldc + p.half + pr) = pack4_bf16(gt);
@@ -2057,11 +2074,10 @@ extern "C" int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const voi
            : dispatch_rows<true, EPI_STORE>(dtype, p, R, (int)N, s);
 }
 
-extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
-                                   const int64_t* sorted_expert_idxs, const int64_t* sorted_scattered_idxs,
-                                   const int64_t* expert_offsets, int64_t T, int64_t d, int64_t f, int E, int k,
-                                   int dtype, void* H, void* A, void* stream) {
-  (void)sorted_expert_idxs;
+namespace {
+int glu_w1_forward_impl(const void* X, int64_t x_stride_m, const void* W1, const int64_t* sorted_scattered_idxs,
+                        const int64_t* expert_offsets, int64_t T, int64_t d, int64_t f, int E, int k, int dtype,
+                        const float* row_scale, void* H, void* A, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "glu_w1_forward: dtype %d", dtype);
   ZMOE_REQUIRE(T >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE && k >= 1, ZMOE_ERR_SHAPE,
                "glu_w1_forward: bad sizes");
@@ -2097,7 +2113,30 @@ extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void
                "glu_w1_forward: X or one expert's W1 spans more than 2 GiB");
   p.a_bytes = (uint32_t)a_span;
   p.b_bytes = (uint32_t)b_span;
+  p.row_scale = row_scale;
   return dispatch_rows<false, EPI_SWIGLU>(dtype, p, R, (int)f, as_stream(stream));
+}
+}  // namespace
+
+extern "C" int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
+                                   const int64_t* sorted_expert_idxs, const int64_t* sorted_scattered_idxs,
+                                   const int64_t* expert_offsets, int64_t T, int64_t d, int64_t f, int E, int k,
+                                   int dtype, void* H, void* A, void* stream) {
+  (void)sorted_expert_idxs;
+  return glu_w1_forward_impl(X, x_stride_m, W1, sorted_scattered_idxs, expert_offsets, T, d, f, E, k, dtype, nullptr,
+                             H, A, stream);
+}
+
+extern "C" int zmoe_glu_w1_forward_scaled(const void* X, int64_t x_stride_m, const void* W1,
+                                          const int64_t* sorted_expert_idxs, const int64_t* sorted_scattered_idxs,
+                                          const int64_t* expert_offsets, int64_t T, int64_t d, int64_t f, int E,
+                                          int k, int dtype, const float* row_scale, void* H, void* A,
+                                          void* stream) {
+  (void)sorted_expert_idxs;
+  ZMOE_REQUIRE(dtype == ZMOE_DTYPE_BF16, ZMOE_ERR_DTYPE, "glu_w1_forward_scaled: bf16 only (dtype %d)", dtype);
+  ZMOE_REQUIRE(T * k == 0 || row_scale != nullptr, ZMOE_ERR_NULL, "glu_w1_forward_scaled: null row_scale");
+  return glu_w1_forward_impl(X, x_stride_m, W1, sorted_scattered_idxs, expert_offsets, T, d, f, E, k, dtype,
+                             row_scale, H, A, stream);
 }
 
 extern "C" int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const void* H,
@@ -2225,6 +2264,81 @@ extern "C" int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k,
   return check_launch("glu_w2_backward_dh_gates: gate sums");
 }
 
+namespace {
+// bf16 weight grads: 256 x 256 tiles when the experts are large enough, 128 x 128 otherwise,
+// and the small experts split off under a skewed routing. DYG: the gather is on DY's rows.
+template <bool DYG>
+int group_bwd_w_bf16(WgradParams p, int64_t M, int E, int64_t N, int64_t K, hipStream_t s) {
+  const bool big = use_big_tiles(M, E, N) && K >= 256;
+  const int gather = p.x_rows ? (p.x_div_shift >= 0 ? 1 : 2) : 0;
+  if (DYG && gather == 0) return zmoe::set_error(ZMOE_ERR_NULL, "group_bwd_w: the DY gather needs indices");
+  auto small_tiles = [&](const WgradParams& q) -> int {
+    if (gather == 1)
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1, false, 4, DYG>, bf16_lds_bytes<128, 128>(), 128, 128,
+                                 q, s);
+    if (gather == 2)
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2, false, 4, DYG>, bf16_lds_bytes<128, 128>(), 128, 128,
+                                 q, s);
+    if constexpr (!DYG)
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
+    return (int)ZMOE_ERR_NULL;  // not reached (checked above)
+  };
+  const int split = big ? wgrad_small_rows(M, E) : 0;
+  int rc = 0;
+  if (split > 0) {  // experts of at most `split` rows on 128 x 128 tiles, the rest below
+    WgradParams q = p;
+    q.rows_hi = split;
+    rc = small_tiles(q);
+    p.rows_lo = split + 1;
+  }
+  if (rc) return rc;
+  if (!big) return small_tiles(p);
+  if (gather == 1) return launch_wgrad_big<1, false, DYG>(p, s);
+  if (gather == 2) return launch_wgrad_big<2, false, DYG>(p, s);
+  if constexpr (!DYG) return launch_wgrad_big<0, false>(p, s);
+  return (int)ZMOE_ERR_NULL;  // not reached
+}
+}  // namespace
+
+extern "C" int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m, const int64_t* dy_gather_idxs,
+                                          int dy_gather_div, const void* X, int64_t x_stride_m,
+                                          const int64_t* expert_offsets, int64_t M, int64_t N, int64_t K, int E,
+                                          int dtype, void* DWt, void* stream) {
+  ZMOE_REQUIRE(dtype == ZMOE_DTYPE_BF16, ZMOE_ERR_DTYPE, "group_bwd_w_gather_dy: bf16 only (dtype %d)", dtype);
+  ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && E >= 1 && E <= kGemmMaxE && dy_gather_div >= 1, ZMOE_ERR_SHAPE,
+               "group_bwd_w_gather_dy: bad sizes");
+  ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30), ZMOE_ERR_SHAPE, "group_bwd_w_gather_dy: N/K too large");
+  ZMOE_REQUIRE(M < kMaxRows, ZMOE_ERR_SHAPE, "group_bwd_w_gather_dy: M must be below 2^31");
+  ZMOE_REQUIRE(DWt && expert_offsets, ZMOE_ERR_NULL, "group_bwd_w_gather_dy: null pointer");
+  ZMOE_REQUIRE(M == 0 || (DY && X && dy_gather_idxs), ZMOE_ERR_NULL, "group_bwd_w_gather_dy: null operand");
+  const int v = vec_elems(dtype);
+  ZMOE_REQUIRE(N % v == 0 && K % v == 0 && aligned16(DWt) && (M == 0 || (ok_rows(dtype, DY, dy_stride_m) &&
+                                                                          ok_rows(dtype, X, x_stride_m))),
+               ZMOE_ERR_ALIGN, "group_bwd_w_gather_dy: N, K and strides must be multiples of %d elements", v);
+  WgradParams p{};
+  p.dy = DY;
+  p.lddy = dy_stride_m;
+  p.x = X;
+  p.ldx = x_stride_m;
+  p.x_rows = dy_gather_idxs;
+  p.x_div = dy_gather_div;
+  p.x_div_shift = (dy_gather_div & (dy_gather_div - 1)) == 0 ? __builtin_ctz(dy_gather_div) : -1;
+  p.dw = DWt;
+  p.offsets = expert_offsets;
+  p.Ndy = (int)N;
+  p.Kx = (int)K;
+  p.E = E;
+  const int64_t dy_span = span_bytes(cdiv(M, dy_gather_div), dy_stride_m, N, dtype);
+  const int64_t x_span = span_bytes(M, x_stride_m, K, dtype);
+  ZMOE_REQUIRE(dy_span <= kMaxSpan && x_span <= kMaxSpan, ZMOE_ERR_SHAPE,
+               "group_bwd_w_gather_dy: DY or X spans more than 2 GiB");
+  p.dy_bytes = (uint32_t)dy_span;
+  p.x_bytes = (uint32_t)x_span;
+  if (M == 0) p.x_rows = nullptr;  // no rows: every expert's tiles write zeros (no gather)
+  return M == 0 ? group_bwd_w_bf16<false>(p, M, E, N, K, as_stream(stream))
+                : group_bwd_w_bf16<true>(p, M, E, N, K, as_stream(stream));
+}
+
 extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m,
                                 const int64_t* x_gather_idxs, int x_gather_div, const int64_t* expert_offsets,
                                 int64_t M, int64_t N, int64_t K, int E, int dtype, void* DWt, void* Db,
@@ -2261,33 +2375,7 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   hipStream_t s = as_stream(stream);
   int rc;
   if (dtype == ZMOE_DTYPE_BF16) {
-    const bool big = use_big_tiles(M, E, N) && K >= 256;
-    const int gather = p.x_rows ? (p.x_div_shift >= 0 ? 1 : 2) : 0;
-    auto small_tiles = [&](const WgradParams& q) {
-      if (gather == 1)
-        return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
-      if (gather == 2)
-        return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
-      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
-    };
-    const int split = big ? wgrad_small_rows(M, E) : 0;
-    rc = 0;
-    if (split > 0) {  // experts of at most `split` rows on 128 x 128 tiles, the rest below
-      WgradParams q = p;
-      q.rows_hi = split;
-      rc = small_tiles(q);
-      p.rows_lo = split + 1;
-    }
-    if (rc == 0) {
-      if (!big)
-        rc = small_tiles(p);
-      else if (gather == 1)
-        rc = launch_wgrad_big<1, false>(p, s);
-      else if (gather == 2)
-        rc = launch_wgrad_big<2, false>(p, s);
-      else
-        rc = launch_wgrad_big<0, false>(p, s);
-    }
+    rc = group_bwd_w_bf16<false>(p, M, E, N, K, s);
   } else {
     rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
                              s);

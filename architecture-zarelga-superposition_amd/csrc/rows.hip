@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
       for (int j = 0; j < KF; ++j) yv[j] = ld16_stream(Y + (t * KF + j) * d + ch * VN);
 #pragma unroll
       for (int j = 0; j < KF; ++j) {
-        const float w = g[t * KF + j];
+        const float w = g ? g[t * KF + j] : 1.f;
         float y[VN];
         unpack_chunk(yv[j], y, T{});
 #pragma unroll
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_kernel(const T* __restric
       }
     } else {
       for (int j = 0; j < k; ++j) {
-        const float w = g[t * k + j];
+        const float w = g ? g[t * k + j] : 1.f;
         float y[VN];
         unpack_chunk(ld16_stream(Y + (t * k + j) * d + ch * VN), y, T{});
 #pragma unroll
@@ -360,7 +360,7 @@ int combine_impl(const void* Y, const float* gates, const void* addend, int64_t 
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "combine: dtype");
   ZMOE_REQUIRE(T >= 0 && k >= 1 && d >= 0, ZMOE_ERR_SHAPE, "combine: bad sizes");
   if (T == 0 || d == 0) return ZMOE_OK;
-  ZMOE_REQUIRE(Y && gates && out, ZMOE_ERR_NULL, "combine: null pointer");
+  ZMOE_REQUIRE(Y && out, ZMOE_ERR_NULL, "combine: null pointer");
   ZMOE_REQUIRE(d % vec_of(dtype) == 0 && rows_aligned(dtype, Y, d) && rows_aligned(dtype, out, d) &&
                    rows_aligned(dtype, addend, d),
                ZMOE_ERR_ALIGN, "combine: d must be a multiple of %d, pointers 16-byte aligned", vec_of(dtype));

@@ -32,12 +32,15 @@ def pad_input(x: torch.Tensor, indices: torch.Tensor, batch: int, seqlen: int) -
 
 class _FusedMoELayer(torch.autograd.Function):
     """The whole layer in one autograd function (bf16 on the device): gate projection and
-    routing, shared expert, routed GLU experts, combine. It runs the same kernels in the
-    same order as the module composition (MoEGate, ExpertMLP and GLUMLP's fused path) in
-    the forward, so the routing and output are the same values. The combine's backward is
-    folded into the dA GEMM (zmoe_glu_w2_backward_dh_gates: it reads the output grad's
-    rows in place and forms the gates' grad from its own products), so Y is not kept for
-    the backward and the only [T*k, d] pass left writes the gate-scaled rows for dW2. The backward writes the
+    routing, shared expert, routed GLU experts, combine. The routing is computed as in the
+    module composition (MoEGate, ExpertMLP and GLUMLP's fused path), with the same values.
+    The routing weights are applied to the activations A instead of to the W2 outputs
+    (w (A W2) = (w A) W2): the W1 epilogue writes A_s = w * silu(gate) * h and the combine
+    sums unweighted rows. In the backward, the W2 input-grad GEMM reads the output grad's
+    rows in place, scales its product by w and forms the gates' grad <dout[t], Y> =
+    <dout[t] W2^T, A> from H (zmoe_glu_w2_backward_dh_gates); the W2 grad is dout[t]^T A_s
+    with dout's rows gathered in the weight-grad kernel. No [T*k, d] pass is left besides
+    the forward combine, and Y is not kept. The backward writes the
     shared expert's dH and the gate's d_logits side by side into one [T, 2fs + E] buffer:
     one GEMM against [W_up; W_gate; W_router] gives both of their input grads, one split-K
     weight-grad launch all three weight grads, and the k-sum pass adds that input grad to
@@ -61,11 +64,12 @@ class _FusedMoELayer(torch.autograd.Function):
         S = F.linear(As, Ws_down)                                                    # expert_layer.py:23-24
         se, ss, off, inv = _z.flatten_sort_count(idx, E)                             # mlp.py:80-82
         stash["expert_offsets"] = off
-        H, A = _z.glu_w1_forward(x, W1, se, ss, off, k)
-        Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
-                               expert_offsets=off)
-        out = _z.combine(Y, w, k, addend=S, out_rows=pad_rows, out_total=pad_total)  # moe_layer.py:48-56
-        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A)
+        w_sorted = w.reshape(-1).index_select(0, ss)
+        H, A_s = _z.glu_w1_forward(x, W1, se, ss, off, k, row_scale=w_sorted)        # A_s = w * A
+        Y_s = _z.scatter2scatter(A_s, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
+                                 expert_offsets=off)                                 # = w * Y
+        out = _z.combine(Y_s, None, k, addend=S, out_rows=pad_rows, out_total=pad_total)  # moe_layer.py:48-56
+        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, H, A_s)
         ctx.k, ctx.E, ctx.fs = k, E, fs
         ctx.pad_rows = pad_rows
         ctx.mark_non_differentiable(idx)
@@ -73,7 +77,7 @@ class _FusedMoELayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, d_idx):
-        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, inv, H, A = ctx.saved_tensors
+        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, H, A_s = ctx.saved_tensors
         k, E, fs = ctx.k, ctx.E, ctx.fs
         need = ctx.needs_input_grad
         dout = dout.to(x.dtype).contiguous()
@@ -84,8 +88,7 @@ class _FusedMoELayer(torch.autograd.Function):
         # routed experts: the dA GEMM reads dS's rows in place and scales them by the gates
         # after the product, from which it also forms d_gates (no pass over Y)
         dH, d_gates = _z.glu_w2_backward_dh_gates(dS, W2, H, se, ss, off, k, w)
-        # gates * dout[t] in sorted order for dW2 (one read of each token's grad row)
-        dW2 = _z.group_bwd_w(_z.combine_backward(None, dS, w, inv)[1], A, off, E)[0] if need[4] else None
+        dW2 = _z.group_bwd_w_gather_dy(dS, ss, k, A_s, off, E) if need[4] else None        # sum dout[t]^T (w A)
         dW1 = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)[0] if need[3] else None
         dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False, expert_offsets=off)
         # shared expert

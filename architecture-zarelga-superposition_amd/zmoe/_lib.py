@@ -47,10 +47,12 @@ SIGNATURES = {
     "zmoe_scatter2scatter": (I32, [P, I64, P, I64, I64, I64, P, I64, P, P, P, I64, I64, I64, I32, I32, I32, I32,
                                    I32, P, I64, P]),
     "zmoe_group_bwd_w": (I32, [P, I64, P, I64, P, I32, P, I64, I64, I64, I32, I32, P, P, P]),
+    "zmoe_group_bwd_w_gather_dy": (I32, [P, I64, P, I32, P, I64, P, I64, I64, I64, I32, I32, P, P]),
     "zmoe_dense_wgrad_workspace_bytes": (SZ, [I64, I64, I32]),
     "zmoe_dense_wgrad": (I32, [P, I64, P, I64, I64, I64, I64, I32, I32, P, P, SZ, P]),
     "zmoe_rowwise_sum_product": (I32, [P, I32, P, I32, I64, I32, I64, P, I32, P]),
     "zmoe_glu_w1_forward": (I32, [P, I64, P, P, P, P, I64, I64, I64, I32, I32, I32, P, P, P]),
+    "zmoe_glu_w1_forward_scaled": (I32, [P, I64, P, P, P, P, I64, I64, I64, I32, I32, I32, P, P, P, P]),
     "zmoe_glu_w2_backward_dh": (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P, P]),
     "zmoe_glu_w2_backward_dh_gates_workspace_bytes": (SZ, [I64, I64]),
     "zmoe_glu_w2_backward_dh_gates": (I32, [P, I64, I32, P, P, P, P, P, P, I64, I64, I32, I32, P, P, P, SZ, P]),

@@ -238,6 +238,30 @@ def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor,
     return DWt, Db
 
 
+def group_bwd_w_gather_dy(DY: torch.Tensor, dy_gather: torch.Tensor, dy_div: int, X: torch.Tensor,
+                          expert_offsets: torch.Tensor, E: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """group_bwd_w with the gather on DY (bf16): sorted row i of DY is DY[dy_gather[i] // dy_div],
+    X [R, K] in sorted order. Returns DWt [E, N, K]."""
+    dev = _require_cuda(DY, dy_gather, X, expert_offsets)
+    DY = _rows(DY)
+    X = _rows(X)
+    if DY.dtype != torch.bfloat16 or X.dtype != torch.bfloat16:
+        raise ValueError("group_bwd_w_gather_dy: bf16 operands only")
+    g = _idx64(dy_gather)
+    M, K = X.shape
+    N = DY.shape[1]
+    if g.numel() != M or DY.shape[0] * dy_div < M:
+        raise ValueError("group_bwd_w_gather_dy: dy_gather must have X.size(0) entries, into DY's rows")
+    DWt = torch.empty((E, N, K), dtype=DY.dtype, device=dev) if out is None else out
+    if DWt.shape != (E, N, K) or DWt.dtype != DY.dtype or not DWt.is_contiguous():
+        raise ValueError("group_bwd_w_gather_dy: bad out tensor")
+    off = _idx64(expert_offsets)
+    with profiling.region("group_bwd_w", dev):
+        L.call("zmoe_group_bwd_w_gather_dy", _ptr(DY), DY.stride(0), _ptr(g), int(dy_div), _ptr(X), X.stride(0),
+               _ptr(off), M, N, K, E, _dtype_code(DY), _ptr(DWt), _stream(dev))
+    return DWt
+
+
 def dense_wgrad_splits(M: int, N: int, K: int, cus: int = 256) -> int:
     """Row splits for the dense weight-grad GEMM: the split count minimising
     (waves of tiles over the CUs) x (rows per split), plus the fp32 partials' extra
@@ -281,9 +305,11 @@ def dense_wgrad(DY: torch.Tensor, X: torch.Tensor, splits: Optional[int] = None,
 
 
 def glu_w1_forward(x: torch.Tensor, W1: torch.Tensor, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets,
-                   k: int):
-    """W1 grouped GEMM with fused SwiGLU: returns H [R, 2f] and A [R, f] in sorted order."""
-    dev = _require_cuda(x, W1)
+                   k: int, row_scale: Optional[torch.Tensor] = None):
+    """W1 grouped GEMM with fused SwiGLU: returns H [R, 2f] and A [R, f] in sorted order.
+
+    ``row_scale`` (f32 [R], sorted order; bf16 only): A[i] = row_scale[i] * silu(gate) * h."""
+    dev = _require_cuda(x, W1, row_scale)
     x = _rows(x)
     W1 = W1.contiguous()
     E, two_f, d = W1.shape
@@ -293,9 +319,17 @@ def glu_w1_forward(x: torch.Tensor, W1: torch.Tensor, sorted_expert_idxs, sorted
     H = torch.empty((R, two_f), dtype=x.dtype, device=dev)
     A = torch.empty((R, f), dtype=x.dtype, device=dev)
     with profiling.region("glu_w1_forward", dev):
-        L.call("zmoe_glu_w1_forward", _ptr(x), x.stride(0), _ptr(W1), _ptr(sorted_expert_idxs),
-               _ptr(sorted_scattered_idxs), _ptr(expert_offsets), T, d, f, E, k, _dtype_code(x), _ptr(H), _ptr(A),
-               _stream(dev))
+        if row_scale is None:
+            L.call("zmoe_glu_w1_forward", _ptr(x), x.stride(0), _ptr(W1), _ptr(sorted_expert_idxs),
+                   _ptr(sorted_scattered_idxs), _ptr(expert_offsets), T, d, f, E, k, _dtype_code(x), _ptr(H), _ptr(A),
+                   _stream(dev))
+        else:
+            rs = row_scale.reshape(-1)
+            if rs.dtype != torch.float32 or rs.numel() != R:
+                raise ValueError("glu_w1_forward: row_scale must be float32 with T*k entries")
+            L.call("zmoe_glu_w1_forward_scaled", _ptr(x), x.stride(0), _ptr(W1), _ptr(sorted_expert_idxs),
+                   _ptr(sorted_scattered_idxs), _ptr(expert_offsets), T, d, f, E, k, _dtype_code(x),
+                   _ptr(rs.contiguous()), _ptr(H), _ptr(A), _stream(dev))
     return H, A
 
 
@@ -340,9 +374,9 @@ def glu_w2_backward_dh_gates(dout: torch.Tensor, W2: torch.Tensor, H: torch.Tens
 
 
 # --------------------------------------------------------------------- combine / reductions
-def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch.Tensor] = None,
+def combine(Y: torch.Tensor, gates: Optional[torch.Tensor], k: int, addend: Optional[torch.Tensor] = None,
             out_rows: Optional[torch.Tensor] = None, out_total: Optional[int] = None) -> torch.Tensor:
-    """out[t] = addend[t] + sum_j gates[t, j] * Y[t*k + j].
+    """out[t] = addend[t] + sum_j gates[t, j] * Y[t*k + j] (``gates = None``: all 1).
 
     With ``out_rows`` (int64 [T]) the result is the padded [out_total, d] tensor whose row
     out_rows[t] is token t's output and whose other rows are zero (moe_layer.py:55-56).
@@ -351,7 +385,7 @@ def combine(Y: torch.Tensor, gates: torch.Tensor, k: int, addend: Optional[torch
     Y = Y.contiguous()
     d = Y.shape[-1]
     T = Y.numel() // (d * k)
-    g = gates.reshape(T, k).to(torch.float32).contiguous()
+    g = None if gates is None else gates.reshape(T, k).to(torch.float32).contiguous()
     if addend is not None:
         addend = addend.reshape(T, d).to(Y.dtype).contiguous()
     with profiling.region("combine", dev):

@@ -144,6 +144,16 @@ int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X,
                      int64_t N, int64_t K, int E, int dtype, void* DWt, void* Db,
                      void* stream);
 
+/* The same with the gather on DY's rows instead (parallel_experts.py:102 applied to
+ * the output grad; bf16 only): DYrow(i) = DY[dy_gather_idxs[i] / dy_gather_div],
+ * X rows in sorted order. With X the gate-scaled activations this is the W2 grad
+ * straight from the output grad's rows (no grouped copy of them). */
+int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m,
+                               const int64_t* dy_gather_idxs, int dy_gather_div,
+                               const void* X, int64_t x_stride_m,
+                               const int64_t* expert_offsets, int64_t M, int64_t N,
+                               int64_t K, int E, int dtype, void* DWt, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Dense weight gradient DW[N, K] = DY^T X over M rows (DY [M, N], X [M, K]), for
  * the nn.Linear weights around the routed experts: the shared expert's
@@ -186,6 +196,18 @@ int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
                         int64_t f, int E, int k, int dtype, void* H, void* A,
                         void* stream);
 
+/* The same with each activation row scaled by its routing weight (bf16 only):
+ *   A[i, j] = row_scale[i] * silu(H[i, f + j]) * H[i, j]   (one rounding)
+ * row_scale [R] f32 in sorted order (gates[sorted_scattered_idxs[i]]). The W2
+ * product of these rows is then already gate-weighted, so the combine sums the k
+ * rows of a token with unit weights (parallel_experts.py:161-163 reassociated). */
+int zmoe_glu_w1_forward_scaled(const void* X, int64_t x_stride_m, const void* W1,
+                               const int64_t* sorted_expert_idxs,
+                               const int64_t* sorted_scattered_idxs,
+                               const int64_t* expert_offsets, int64_t T, int64_t d,
+                               int64_t f, int E, int k, int dtype, const float* row_scale,
+                               void* H, void* A, void* stream);
+
 /* scattermoe/parallel_experts.py:112-120 (W2 input grad, x_grouped and
  * y_grouped) fused with the backward of silu(gates) * h (mlp.py:102):
  *   dA[i, :] = dYg[i, :] @ W2[e]                 (W2 [E, d, f] contiguous)
@@ -217,7 +239,8 @@ int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k, const void
 /* scattermoe/parallel_experts.py:161-163 (gates @ output_expanded) plus the
  * residual sum of modeling/moe_layer.py:53:
  *   out[t, :] = addend[t, :] + sum_j gates[t, j] * Y[t * k + j, :]
- * Y [T*k, d] in slot order; addend may be NULL; fp32 accumulation in j order. */
+ * Y [T*k, d] in slot order; addend may be NULL; gates may be NULL (all 1: rows
+ * already scaled, e.g. by the W1 forward's row_gates); fp32 accumulation in j order. */
 int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t T,
                  int k, int64_t d, int dtype, void* out, void* stream);
 

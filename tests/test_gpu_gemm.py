@@ -82,6 +82,64 @@ def test_group_bwd_w(hip_device, dtype, T, K, N, E, k, skew, gather):
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
 
 
+@pytest.mark.parametrize("T,K,N,E,k,skew", SHAPES[:10])
+def test_group_bwd_w_gather_dy(hip_device, T, K, N, E, k, skew):
+    """bf16 weight grads with the gather on DY's rows: sorted row i of DY is
+    DY[ss[i] // k] (the output grad's rows read in place), X in sorted order."""
+    from zmoe import ops
+
+    idx, se, ss, off, _ = _routing(T, E, k, skew, hip_device, seed=T + 5 * N)
+    g = gen(T * 5 + K)
+    dt = torch.bfloat16
+    DY = torch.randn(T, N, generator=g).to(dt)
+    X = torch.randn(T * k, K, generator=g).to(dt)
+    DWt = ops.group_bwd_w_gather_dy(DY.to(hip_device), ss, k, X.to(hip_device), off, E)
+    ref, _ = O.group_bwd_w(O.group(np64(DY), ss.cpu().numpy(), fan_out=k), np64(X), off.cpu().numpy(), E)
+    assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[dt], what="group_bwd_w_gather_dy")
+    counts = np.diff(np.concatenate([[0], off.cpu().numpy()]))
+    for e in np.nonzero(counts == 0)[0]:
+        assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
+
+
+def test_group_bwd_w_gather_dy_small_expert_split(hip_device):
+    """The DY gather on both sides of the small-expert split (0, 1, 64, 65 rows)."""
+    from zmoe import ops
+
+    counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0])
+    E, k, N, K = len(counts), 2, 256, 320
+    off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
+    R = int(counts.sum())
+    g = gen(R + K)
+    ss = torch.from_numpy(np.random.default_rng(8).permutation(R)).to(hip_device)
+    DY = torch.randn(R // k + 1, N, generator=g).to(torch.bfloat16)
+    X = torch.randn(R, K, generator=g).to(torch.bfloat16)
+    DWt = ops.group_bwd_w_gather_dy(DY.to(hip_device), ss, k, X.to(hip_device), off, E)
+    ref, _ = O.group_bwd_w(O.group(np64(DY), ss.cpu().numpy(), fan_out=k), np64(X), off.cpu().numpy(), E)
+    assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[torch.bfloat16], what="group_bwd_w_gather_dy split")
+    for e in np.nonzero(counts == 0)[0]:
+        assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
+
+
+@pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
+                                            (1200, 200, 136, 4, 2, 0.3), (128, 512, 136, 64, 4, 1.5),
+                                            (32, 256, 256, 32, 8, 0.0)])
+def test_glu_w1_forward_scaled(hip_device, T, d, f, E, k, skew):
+    """A = row_scale * silu(gate) * h from the W1 epilogue (tiled and weight-streaming paths),
+    H unchanged."""
+    from zmoe import ops
+
+    idx, se, ss, off, _ = _routing(T, E, k, skew, hip_device, seed=T + 7 * f)
+    g = gen(T + 3 * d + f)
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16).to(hip_device)
+    W1 = (torch.randn(E, 2 * f, d, generator=g) / d ** 0.5).to(torch.bfloat16).to(hip_device)
+    rs = (torch.rand(T * k, generator=g) + 0.05).to(hip_device)
+    H0, A0 = ops.glu_w1_forward(x, W1, se, ss, off, k)
+    H, A = ops.glu_w1_forward(x, W1, se, ss, off, k, row_scale=rs)
+    assert torch.equal(H, H0)
+    ref = O.bf16_round((rs.double().cpu().numpy()[:, None] * O.swiglu(np64(H))).astype(np.float32))
+    assert_close(np64(A), ref.astype(np.float64), **TOL[torch.bfloat16], what="scaled A")
+
+
 @pytest.mark.parametrize("gather", [False, True])
 def test_group_bwd_w_small_expert_split(hip_device, gather):
     """bf16 weight grads with 256 x 256 tiles and fewer than 1024 rows per expert on average:

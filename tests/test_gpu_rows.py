@@ -54,6 +54,10 @@ def test_combine_and_backward(hip_device, dtype, T, d, k):
     assert_close(d_gates.cpu().numpy(), ref_dg, rtol=1e-5, atol=1e-4, what="d_gates")
     ref_grouped = O.group(np64(dout), ss.cpu().numpy(), coeff=gates.double().numpy().reshape(-1), fan_out=k)
     assert_close(np64(grouped), ref_grouped, **tol, what="grouped_grad_out")
+    # unit gates (gates = None): the plain k-sum plus the addend
+    out1 = ops.combine(Y.to(hip_device), None, k, addend=add.to(hip_device))
+    ref1 = np64(Y).reshape(T, k, d).sum(1) + np64(add)
+    assert_close(np64(out1), ref1, **tol, what="combine without gates")
     # without Y: the same grouped rows, no gate grads
     no_dg, grouped2 = ops.combine_backward(None, dout.to(hip_device), gates.to(hip_device), inv)
     assert no_dg is None and torch.equal(grouped2, grouped)
