@@ -1240,9 +1240,9 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           const float sg = sigmoid_fast(gt[v]);
-          if (dots) {  // dA = scale * (unscaled dA), stored in bf16; the dot uses the unscaled values
-            dot[u] += da[v] * to_f32(bf16_bits(gt[v] * sg * h[v]));  // A = silu(gate) * h in bf16
-            da[v] = to_f32(bf16_bits(rsc[u] * da[v]));
+          if (dots) {  // dA = scale * (unscaled dA, bf16); the dot uses the unscaled values
+            dot[u] += da[v] * (gt[v] * sg * h[v]);  // A = silu(gate) * h
+            da[v] *= rsc[u];
           }
           dh[v] = da[v] * gt[v] * sg;
           dg[v] = da[v] * h[v] * sg * (1.f + gt[v] * (1.f - sg));
