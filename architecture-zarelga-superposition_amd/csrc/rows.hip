@@ -312,6 +312,40 @@ __global__ __launch_bounds__(kRowThreads) void swiglu_backward_kernel(const T* _
   st16(dH + r * ld + f + ch * VN, pack_chunk(dg, T{}));
 }
 
+// SwiGLU backward of gate-scaled rows with the gates' grad: one wave per sorted row r,
+//   dA = row_scale[r] * dAu[r];  dH[r] = [dA * g * s | dA * h * s * (1 + g (1 - s))];
+//   d_gates[slot[r]] = sum_c dAu[r, c] * silu(g) * h      (s = sigmoid(g), [h | g] = H[r])
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void swiglu_backward_gates_kernel(
+    const T* __restrict__ dAu, const T* __restrict__ H, int64_t R, int64_t f, const float* __restrict__ row_scale,
+    const int64_t* __restrict__ slot, T* __restrict__ dH, float* __restrict__ d_gates) {
+  constexpr int VN = V<T>::N;
+  const int64_t r = (int64_t)blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
+  if (r >= R) return;  // whole waves
+  const int lane = threadIdx.x & 63;
+  const int64_t nch = f / VN;
+  const float sc = row_scale[r];
+  float dot = 0.f;
+  for (int64_t ch = lane; ch < nch; ch += 64) {
+    float da[VN], h[VN], g[VN], dh[VN], dg[VN];
+    unpack_chunk(ld16_stream(dAu + r * f + ch * VN), da, T{});
+    unpack_chunk(ld16_stream(H + r * 2 * f + ch * VN), h, T{});
+    unpack_chunk(ld16_stream(H + r * 2 * f + f + ch * VN), g, T{});
+#pragma unroll
+    for (int q = 0; q < VN; ++q) {
+      const float s = sigmoid_fast(g[q]);
+      dot = fmaf(da[q], g[q] * s * h[q], dot);
+      const float d = sc * da[q];
+      dh[q] = d * g[q] * s;
+      dg[q] = d * h[q] * s * (1.f + g[q] * (1.f - s));
+    }
+    st16(dH + r * 2 * f + ch * VN, pack_chunk(dh, T{}));
+    st16(dH + r * 2 * f + f + ch * VN, pack_chunk(dg, T{}));
+  }
+  dot = wave_sum(dot);
+  if (lane == 0) d_gates[slot[r]] = dot;
+}
+
 }  // namespace zmoe
 
 using namespace zmoe;
@@ -519,6 +553,26 @@ extern "C" int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void*
   else
     hipLaunchKernelGGL(swiglu_kernel<float>, grid, block, 0, as_stream(stream), (const float*)H, R, f, (float*)A);
   return check_launch("swiglu");
+}
+
+extern "C" int zmoe_swiglu_backward_gates(const void* dA, const void* H, int64_t R, int64_t f, const float* row_scale,
+                                          const int64_t* slot_of_row, int dtype, void* dH, float* d_gates,
+                                          void* stream) {
+  ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "swiglu_backward_gates: dtype");
+  ZMOE_REQUIRE(R >= 0 && f >= 1, ZMOE_ERR_SHAPE, "swiglu_backward_gates: bad sizes");
+  if (R == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(dA && H && dH && row_scale && slot_of_row && d_gates, ZMOE_ERR_NULL,
+               "swiglu_backward_gates: null pointer");
+  ZMOE_REQUIRE(f % vec_of(dtype) == 0 && aligned16(H) && aligned16(dA) && aligned16(dH), ZMOE_ERR_ALIGN,
+               "swiglu_backward_gates: f must be a multiple of %d", vec_of(dtype));
+  const dim3 grid((unsigned)cdiv(R, kRowThreads / 64)), block(kRowThreads);
+  if (dtype == ZMOE_DTYPE_BF16)
+    hipLaunchKernelGGL(swiglu_backward_gates_kernel<uint16_t>, grid, block, 0, as_stream(stream),
+                       (const uint16_t*)dA, (const uint16_t*)H, R, f, row_scale, slot_of_row, (uint16_t*)dH, d_gates);
+  else
+    hipLaunchKernelGGL(swiglu_backward_gates_kernel<float>, grid, block, 0, as_stream(stream), (const float*)dA,
+                       (const float*)H, R, f, row_scale, slot_of_row, (float*)dH, d_gates);
+  return check_launch("swiglu_backward_gates");
 }
 
 extern "C" int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f, int dtype, void* dH,

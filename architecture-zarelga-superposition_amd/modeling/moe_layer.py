@@ -37,8 +37,9 @@ class _FusedMoELayer(torch.autograd.Function):
     The routing weights are applied to the activations A instead of to the W2 outputs
     (w (A W2) = (w A) W2): the W1 epilogue writes A_s = w * silu(gate) * h and the combine
     sums unweighted rows. In the backward, the W2 input-grad GEMM reads the output grad's
-    rows in place, scales its product by w and forms the gates' grad <dout[t], Y> =
-    <dout[t] W2^T, A> from H (zmoe_glu_w2_backward_dh_gates); the W2 grad is dout[t]^T A_s
+    rows in place, and one row pass (zmoe_swiglu_backward_gates) scales its product by w,
+    runs the SwiGLU backward and forms the gates' grad <dout[t], Y> = <dout[t] W2^T, A>
+    from H; the W2 grad is dout[t]^T A_s
     with dout's rows gathered in the weight-grad kernel. No [T*k, d] pass is left besides
     the forward combine, and Y is not kept. The backward writes the
     shared expert's dH and the gate's d_logits side by side into one [T, 2fs + E] buffer:
@@ -69,7 +70,7 @@ class _FusedMoELayer(torch.autograd.Function):
         Y_s = _z.scatter2scatter(A_s, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
                                  expert_offsets=off)                                 # = w * Y
         out = _z.combine(Y_s, None, k, addend=S, out_rows=pad_rows, out_total=pad_total)  # moe_layer.py:48-56
-        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, H, A_s)
+        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s)
         ctx.k, ctx.E, ctx.fs = k, E, fs
         ctx.pad_rows = pad_rows
         ctx.mark_non_differentiable(idx)
@@ -77,7 +78,7 @@ class _FusedMoELayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, d_idx):
-        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w, se, ss, off, H, A_s = ctx.saved_tensors
+        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s = ctx.saved_tensors
         k, E, fs = ctx.k, ctx.E, ctx.fs
         need = ctx.needs_input_grad
         dout = dout.to(x.dtype).contiguous()
@@ -85,9 +86,13 @@ class _FusedMoELayer(torch.autograd.Function):
         # the grad of the combine's inputs: dout for the shared expert's output (the addend),
         # gates * dout[t] for the routed rows, <dout[t], Y> for the gates
         dS = dout if pad_rows is None else dout.index_select(0, pad_rows)
-        # routed experts: the dA GEMM reads dS's rows in place and scales them by the gates
-        # after the product, from which it also forms d_gates (no pass over Y)
-        dH, d_gates = _z.glu_w2_backward_dh_gates(dS, W2, H, se, ss, off, k, w)
+        # routed experts: dA = dout[t] W2_e^T as a plain grouped GEMM on dS's rows read in
+        # place, then one row pass for the SwiGLU backward of w * dA and the gates' grad (no
+        # pass over Y; an epilogue that reads H inside the GEMM measured slower)
+        dA = _z.scatter2scatter(dS, W2, se, ss, k, x_grouped=False, y_grouped=True, expert_offsets=off,
+                                region="glu_w2_backward_dh")
+        dH, d_gates = _z.swiglu_backward_gates(dA, H, w_sorted, ss)
+        d_gates = d_gates.view(-1, k)
         dW2 = _z.group_bwd_w_gather_dy(dS, ss, k, A_s, off, E) if need[4] else None        # sum dout[t]^T (w A)
         dW1 = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)[0] if need[3] else None
         dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False, expert_offsets=off)

@@ -63,6 +63,7 @@ SIGNATURES = {
     "zmoe_sum_k": (I32, [P, I64, I32, I64, I32, P, P, P, P]),
     "zmoe_swiglu": (I32, [P, I64, I64, I32, P, P]),
     "zmoe_swiglu_backward": (I32, [P, P, I64, I64, I32, P, I64, P]),
+    "zmoe_swiglu_backward_gates": (I32, [P, P, I64, I64, P, P, I32, P, P, P]),
     "zmoe_bias_update": (I32, [P, I32, F32, P, P]),
     "zmoe_newton_schulz5_workspace_bytes": (SZ, [I64, I64, I64]),
     "zmoe_newton_schulz5": (I32, [P, I64, I64, I64, I32, F32, F32, F32, P, SZ, P]),

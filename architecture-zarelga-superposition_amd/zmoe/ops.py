@@ -168,8 +168,9 @@ def group(A: torch.Tensor, sorted_idxs: torch.Tensor, coeff: Optional[torch.Tens
 def scatter2scatter(X: torch.Tensor, W: torch.Tensor, sorted_expert_idxs: torch.Tensor,
                     sorted_scattered_idxs: torch.Tensor, k: int, b: Optional[torch.Tensor] = None,
                     x_grouped: bool = False, y_grouped: bool = False, out: Optional[torch.Tensor] = None,
-                    expert_offsets: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """scattermoe/kernels/ops.py:192-209. W is the logical [E, K, N] operand."""
+                    expert_offsets: Optional[torch.Tensor] = None, region: str = "scatter2scatter") -> torch.Tensor:
+    """scattermoe/kernels/ops.py:192-209. W is the logical [E, K, N] operand (``region``: the
+    profiling name of the launch)."""
     dev = _require_cuda(X, W, sorted_expert_idxs, sorted_scattered_idxs, b, out, expert_offsets)
     X = _rows(X)
     if W.dim() != 3:
@@ -194,7 +195,7 @@ def scatter2scatter(X: torch.Tensor, W: torch.Tensor, sorted_expert_idxs: torch.
     if b is not None:
         b = b.to(X.dtype).contiguous()
     M = X.shape[0]
-    with profiling.region("scatter2scatter", dev):
+    with profiling.region(region, dev):
         L.call("zmoe_scatter2scatter", _ptr(X), X.stride(0), _ptr(W), W.stride(0), W.stride(1), W.stride(2),
                _ptr(b), b.stride(0) if b is not None else 0, _ptr(se), _ptr(ss), _ptr(off), M, K, N, E, k,
                int(x_grouped), int(y_grouped), _dtype_code(X), _ptr(out), out.stride(0), _stream(dev))
@@ -471,6 +472,27 @@ def swiglu(H: torch.Tensor) -> torch.Tensor:
     A = torch.empty((R, two_f // 2), dtype=H.dtype, device=dev)
     L.call("zmoe_swiglu", _ptr(H), R, two_f // 2, _dtype_code(H), _ptr(A), _stream(dev))
     return A
+
+
+def swiglu_backward_gates(dA: torch.Tensor, H: torch.Tensor, row_scale: torch.Tensor, slot_of_row: torch.Tensor):
+    """SwiGLU backward of gate-scaled rows with the gates' grad, per sorted row r:
+    dH[r] = swiglu_backward(row_scale[r] * dA[r], H[r]) and
+    d_gates[slot_of_row[r]] = sum_c dA[r, c] * silu(H[r, f + c]) * H[r, c].
+    Returns (dH [R, 2f], d_gates [R] f32 in slot order)."""
+    dev = _require_cuda(dA, H, row_scale, slot_of_row)
+    H = H.contiguous()
+    dA = dA.to(H.dtype).contiguous()
+    R, two_f = H.shape
+    rs = row_scale.reshape(-1).to(torch.float32).contiguous()
+    slots = _idx64(slot_of_row)
+    if dA.shape != (R, two_f // 2) or rs.numel() != R or slots.numel() != R:
+        raise ValueError("swiglu_backward_gates: dA [R, f], H [R, 2f], row_scale and slot_of_row [R]")
+    dH = torch.empty_like(H)
+    d_gates = torch.empty(R, dtype=torch.float32, device=dev)
+    with profiling.region("swiglu_backward_gates", dev):
+        L.call("zmoe_swiglu_backward_gates", _ptr(dA), _ptr(H), R, two_f // 2, _ptr(rs), _ptr(slots), _dtype_code(H),
+               _ptr(dH), _ptr(d_gates), _stream(dev))
+    return dH, d_gates
 
 
 def swiglu_backward(dA: torch.Tensor, H: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -56,7 +56,8 @@ TRAFFIC_C3 = {
     "group_bwd_w#0": 2188436906,
     "group_bwd_w#1": 3906568874,
 }
-ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale", "sum_k")
+ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
+           "swiglu_backward_gates", "sum_k")
 
 
 def gemm_flops(name: str, launch: int, T, d, k, f) -> float:
@@ -71,7 +72,7 @@ def gemm_flops(name: str, launch: int, T, d, k, f) -> float:
     return small if launch % 2 == 0 else big
 
 
-def row_bytes(name: str, T, d, E, k) -> float:
+def row_bytes(name: str, T, d, E, k, f=0) -> float:
     """Algorithmic HBM bytes of one launch (bf16 rows, fp32 gates, int64 ids).
 
     The layer's combine also reads the shared expert's output [T, d] as its addend.
@@ -83,6 +84,7 @@ def row_bytes(name: str, T, d, E, k) -> float:
         "combine": R * d * 2 + R * 4 + T * d * 2 + T * d * 2,
         "combine_backward": R * d * 2 + T * d * 2 + R * (4 + 4 + 4) + R * d * 2,
         "combine_backward_scale": T * d * 2 + R * (4 + 4) + R * d * 2,   # without Y: no gate dots
+        "swiglu_backward_gates": R * f * 2 + 2 * R * 2 * f * 2 + R * (4 + 8 + 4),  # dA, H, dH; scales, slots, d_gates
         "sum_k": R * d * 2 + T * d * 2,
     }[name]
 
@@ -433,7 +435,7 @@ def main(argv=None):
         if not durs:
             continue
         avg = sum(durs) / len(durs)
-        by = row_bytes(name, T, d, E, k)
+        by = row_bytes(name, T, d, E, k, f)
         kernels[name] = dict(avg_ms=avg, gbs=by / (avg * 1e-3) / 1e9, bytes=by)
     gemm = {n: v for n, v in kernels.items() if "tflops" in v}
     dom_name = max(gemm, key=lambda n: gemm[n]["avg_ms"])

@@ -281,6 +281,16 @@ int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void* A, void* s
 int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f,
                          int dtype, void* dH, int64_t ld_dh, void* stream);
 
+/* The SwiGLU backward of gate-scaled rows with the gates' grad (the combine backward
+ * of parallel_experts.py:191-208 reassociated, as in zmoe_glu_w2_backward_dh_gates,
+ * after a plain dA GEMM on the output grad's rows), per sorted row r:
+ *   dH[r] = swiglu_backward(row_scale[r] * dA[r], H[r])
+ *   d_gates[slot_of_row[r]] = sum_j dA[r, j] * silu(H[r, f + j]) * H[r, j]
+ * dA [R, f], H and dH [R, 2f] packed; d_gates [R] f32 written in slot order. */
+int zmoe_swiglu_backward_gates(const void* dA, const void* H, int64_t R, int64_t f,
+                               const float* row_scale, const int64_t* slot_of_row,
+                               int dtype, void* dH, float* d_gates, void* stream);
+
 /* main.py:161-175 (aux-loss-free bias update) from the sort's offsets:
  *   counts = diff(expert_offsets); b += rate * sign(mean(counts) - counts)    */
 int zmoe_bias_update(const int64_t* expert_offsets, int E, float update_rate,

@@ -98,6 +98,25 @@ def test_swiglu(hip_device, dtype):
     assert torch.equal(buf[:, :2 * 768], dH) and bool((buf[:, 2 * 768:] == 7.0).all())
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("R,f", [(333, 768), (64, 136), (1, 8), (5, 264)])
+def test_swiglu_backward_gates(hip_device, dtype, R, f):
+    """dH = swiglu_backward(row_scale * dA, H) and d_gates[slot] = <dA, silu(g) * h> per row."""
+    from zmoe import ops
+
+    g = gen(R + f)
+    H = torch.randn(R, 2 * f, generator=g).to(dtype)
+    dA = torch.randn(R, f, generator=g).to(dtype)
+    rs = torch.rand(R, generator=g) + 0.05
+    slots = torch.from_numpy(np.random.default_rng(R).permutation(R))
+    dH, dg = ops.swiglu_backward_gates(dA.to(hip_device), H.to(hip_device), rs.to(hip_device), slots.to(hip_device))
+    ref_dH = O.swiglu_backward(rs.double().numpy()[:, None] * np64(dA), np64(H))
+    assert_close(np64(dH), ref_dH, **TOL[dtype], what="dH")
+    ref_dg = np.empty(R)
+    ref_dg[slots.numpy()] = (np64(dA) * O.swiglu(np64(H))).sum(1)
+    assert_close(dg.cpu().numpy().astype(np.float64), ref_dg, **TOL[dtype], what="d_gates")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_combine_rows_writes_padded_layout(hip_device, dtype):
     """zmoe_combine_rows / zmoe_combine_backward_rows (the re-pad of moe_layer.py:55-56 folded
