@@ -49,12 +49,12 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # the same counter reads for a plain 1 GiB copy (reads x 2.000, writes x 1.000); the
 # commands and raw counts are in profiles/grouped_gemm_c3_hbm_bytes.md.
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6009356949,
-    "scatter2scatter#0": 2736196778,
-    "glu_w2_backward_dh#0": 3800921386,
-    "scatter2scatter#1": 5119116416,
-    "group_bwd_w#0": 2188436906,
-    "group_bwd_w#1": 3906568874,
+    "glu_w1_forward#0": 6014018560,
+    "scatter2scatter#0": 2750119936,
+    "glu_w2_backward_dh#0": 2388471808,
+    "scatter2scatter#1": 5074219008,
+    "group_bwd_w#0": 2234429440,
+    "group_bwd_w#1": 3897198592,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
