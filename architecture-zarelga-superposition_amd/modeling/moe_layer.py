@@ -36,13 +36,13 @@ class _FusedMoELayer(torch.autograd.Function):
     module composition (MoEGate, ExpertMLP and GLUMLP's fused path), with the same values.
     The routing weights are applied to the activations A instead of to the W2 outputs
     (w (A W2) = (w A) W2): the W1 epilogue writes A_s = w * silu(gate) * h and the combine
-    sums unweighted rows. In the backward, the W2 input-grad GEMM reads the output grad's
-    rows in place, and one row pass (zmoe_swiglu_backward_gates) scales its product by w,
-    runs the SwiGLU backward and forms the gates' grad <dout[t], Y> = <dout[t] W2^T, A>
-    from H; the W2 grad is dout[t]^T A_s
-    with dout's rows gathered in the weight-grad kernel. No [T*k, d] pass is left besides
-    the forward combine, and Y is not kept. The backward writes the
-    shared expert's dH and the gate's d_logits side by side into one [T, 2fs + E] buffer:
+    sums unweighted rows. In the backward, the W2 input-grad GEMM (dA = dout[t] W2_e, W2_e
+    the [d, f] weight of expert e) reads the output grad's rows in place, and one row pass
+    (zmoe_swiglu_backward_gates) scales dA by w, runs the SwiGLU backward and forms the
+    gates' grad <dout[t], Y> = <dout[t] W2_e, A> with A from H. The W2 grad is the sum of
+    dout[t]^T A_s, dout's rows gathered in the weight-grad kernel. No [T*k, d] pass is left
+    besides the forward combine, and Y is not kept. The backward also writes the shared
+    expert's dH and the gate's d_logits side by side into one [T, 2fs + E] buffer:
     one GEMM against [W_up; W_gate; W_router] gives both of their input grads, one split-K
     weight-grad launch all three weight grads, and the k-sum pass adds that input grad to
     the routed experts' (one rounding; the composition runs two more GEMM launches and two
@@ -86,7 +86,7 @@ class _FusedMoELayer(torch.autograd.Function):
         # the grad of the combine's inputs: dout for the shared expert's output (the addend),
         # gates * dout[t] for the routed rows, <dout[t], Y> for the gates
         dS = dout if pad_rows is None else dout.index_select(0, pad_rows)
-        # routed experts: dA = dout[t] W2_e^T as a plain grouped GEMM on dS's rows read in
+        # routed experts: dA = dout[t] W2_e as a plain grouped GEMM on dS's rows read in
         # place, then one row pass for the SwiGLU backward of w * dA and the gates' grad (no
         # pass over Y; an epilogue that reads H inside the GEMM measured slower)
         dA = _z.scatter2scatter(dS, W2, se, ss, k, x_grouped=False, y_grouped=True, expert_offsets=off,
