@@ -38,7 +38,10 @@ __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(const int64_t* 
   for (int e = threadIdx.x; e <= E; e += kSortThreads) out[e] = h[e];
 }
 
-// Single block of 1024 threads; buckets are strided over the threads.
+// Single block of 1024 threads; buckets are strided over the threads. A bucket's column
+// is walked kScanBatch tiles at a time, all of a batch's loads issued before any is used
+// (one memory round trip per batch instead of per tile).
+constexpr int kScanBatch = 16;
 __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ tile_hist, int ntiles, int E,
                                                          int64_t* __restrict__ offsets,
                                                          int32_t* __restrict__ flag) {
@@ -46,7 +49,14 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ t
   __shared__ int64_t start[kSortMaxE + 1];
   for (int e = threadIdx.x; e <= E; e += blockDim.x) {
     int64_t total = 0;
-    for (int b = 0; b < ntiles; ++b) total += tile_hist[(int64_t)b * (E + 1) + e];
+    for (int b0 = 0; b0 < ntiles; b0 += kScanBatch) {
+      int32_t c[kScanBatch];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j)
+        c[j] = b0 + j < ntiles ? tile_hist[(int64_t)(b0 + j) * (E + 1) + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j) total += c[j];
+    }
     tot[e] = total;
   }
   __syncthreads();
@@ -62,11 +72,16 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ t
   for (int e = threadIdx.x; e <= E; e += blockDim.x) {
     if (e < E) offsets[e] = start[e] + tot[e];
     int64_t run = start[e];
-    for (int b = 0; b < ntiles; ++b) {
-      const int64_t o = (int64_t)b * (E + 1) + e;
-      const int32_t c = tile_hist[o];
-      tile_hist[o] = (int32_t)run;
-      run += c;
+    for (int b0 = 0; b0 < ntiles; b0 += kScanBatch) {
+      int32_t c[kScanBatch];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j)
+        c[j] = b0 + j < ntiles ? tile_hist[(int64_t)(b0 + j) * (E + 1) + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j) {
+        if (b0 + j < ntiles) tile_hist[(int64_t)(b0 + j) * (E + 1) + e] = (int32_t)run;
+        run += c[j];
+      }
     }
   }
 }
