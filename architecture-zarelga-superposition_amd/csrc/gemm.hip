@@ -2391,17 +2391,21 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   return check_launch("bias_grad_kernel");
 }
 
-// Workspace: split offsets (256 bytes) + S fp32 partials of [N, K].
+// Workspace: the split offsets (one int64 per split, kDenseMaxSplits of them: 512 bytes, which
+// keeps the partials 256-byte aligned) + S fp32 partials of [N, K].
+constexpr int kDenseMaxSplits = 64;
+constexpr size_t kDenseHeaderBytes = kDenseMaxSplits * sizeof(int64_t);
+
 extern "C" size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int splits) {
-  if (N < 1 || K < 1 || splits < 1) return 256;
-  return 256 + (size_t)splits * (size_t)N * (size_t)K * 4u;
+  if (N < 1 || K < 1 || splits < 1) return kDenseHeaderBytes;
+  return kDenseHeaderBytes + (size_t)splits * (size_t)N * (size_t)K * 4u;
 }
 
 extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m, int64_t M,
                                 int64_t N, int64_t K, int dtype, int splits, void* DW, void* workspace,
                                 size_t workspace_bytes, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "dense_wgrad: dtype %d", dtype);
-  ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && splits >= 1 && splits <= 64, ZMOE_ERR_SHAPE,
+  ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && splits >= 1 && splits <= kDenseMaxSplits, ZMOE_ERR_SHAPE,
                "dense_wgrad: bad sizes (M=%lld N=%lld K=%lld splits=%d)", (long long)M, (long long)N, (long long)K,
                splits);
   ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30) && M < kMaxRows, ZMOE_ERR_SHAPE, "dense_wgrad: sizes too large");
@@ -2429,7 +2433,7 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
   p.x_rows = nullptr;
   p.x_div = 1;
   p.x_div_shift = 0;
-  p.dw = reinterpret_cast<char*>(workspace) + 256;
+  p.dw = reinterpret_cast<char*>(workspace) + kDenseHeaderBytes;
   p.offsets = off;
   p.Ndy = (int)N;
   p.Kx = (int)K;

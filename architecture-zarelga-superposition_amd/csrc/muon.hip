@@ -117,46 +117,48 @@ NsLayout ns_layout(int64_t E, int64_t m, int64_t n) {
   return L;
 }
 
+// Matrices per pass: the grouped GEMMs address a pass's whole X (and A, B) stack as one
+// buffer resource of at most kNsMaxSpan bytes, and take at most 1024 "experts". Larger
+// stacks run as consecutive passes of this many matrices over one pass-sized workspace;
+// every matrix is independent, so the result does not depend on the split.
+constexpr int64_t kNsMaxSpan = 0x7fff0000LL;
+
+int64_t ns_chunk(int64_t E, int64_t m, int64_t n) {
+  int64_t c = kNsMaxSpan / (m * n * 2);
+  c = c < 1024 ? c : 1024;
+  return c < E ? c : E;
+}
+
 }  // namespace zmoe
 
 using namespace zmoe;
 
 extern "C" size_t zmoe_newton_schulz5_workspace_bytes(int64_t E, int64_t m, int64_t n) {
-  if (E < 1 || m < 1 || n < 1) return 0;
-  return ns_layout(E, m, n).total;
+  if (E < 1 || m < 1 || n < 1 || m * n * 2 > kNsMaxSpan) return 0;
+  return ns_layout(ns_chunk(E, m, n), m, n).total;
 }
 
-extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int steps, float a, float b, float c,
-                                   void* workspace, size_t workspace_bytes, void* stream) {
-  ZMOE_REQUIRE(E >= 1 && E <= 1024 && m >= 8 && n >= 8 && m <= n && steps >= 0, ZMOE_ERR_SHAPE,
-               "newton_schulz5: need 1 <= E <= 1024, 8 <= m <= n, steps >= 0 (E=%lld m=%lld n=%lld)",
-               (long long)E, (long long)m, (long long)n);
-  ZMOE_REQUIRE(m % 8 == 0 && n % 8 == 0, ZMOE_ERR_ALIGN, "newton_schulz5: m and n must be multiples of 8");
-  ZMOE_REQUIRE(m < (1 << 20) && n < (1 << 20) && E * m < 0x7fffffffLL, ZMOE_ERR_SHAPE, "newton_schulz5: too large");
-  ZMOE_REQUIRE(X && workspace, ZMOE_ERR_NULL, "newton_schulz5: null pointer");
-  ZMOE_REQUIRE(aligned16(X) && (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, ZMOE_ERR_ALIGN,
-               "newton_schulz5: X must be 16-byte and the workspace 256-byte aligned");
-  const NsLayout L = ns_layout(E, m, n);
-  ZMOE_REQUIRE(workspace_bytes >= L.total, ZMOE_ERR_WORKSPACE, "newton_schulz5: workspace %zu < %zu bytes",
-               workspace_bytes, L.total);
-  hipStream_t s = as_stream(stream);
-  char* ws = static_cast<char*>(workspace);
+namespace {
+
+// One pass over Ec matrices at Xuser (workspace laid out for Ec).
+int ns_pass(uint16_t* Xuser, int64_t Ec, int64_t m, int64_t n, int steps, float a, float b, float c, char* ws,
+            hipStream_t s) {
+  const NsLayout L = ns_layout(Ec, m, n);
   int64_t* offsets = reinterpret_cast<int64_t*>(ws + L.off_offsets);
   float* partial = reinterpret_cast<float*>(ws + L.off_partial);
   uint16_t* Abuf = reinterpret_cast<uint16_t*>(ws + L.off_a);
   uint16_t* Pbuf = reinterpret_cast<uint16_t*>(ws + L.off_p);
   uint16_t* Bbuf = reinterpret_cast<uint16_t*>(ws + L.off_b);
-  uint16_t* Xuser = static_cast<uint16_t*>(X);
   uint16_t* Xtmp = reinterpret_cast<uint16_t*>(ws + L.off_x);
 
-  hipLaunchKernelGGL(ns_offsets_kernel, dim3((unsigned)cdiv(E, 256)), dim3(256), 0, s, offsets, (int)E, m);
+  hipLaunchKernelGGL(ns_offsets_kernel, dim3((unsigned)cdiv(Ec, 256)), dim3(256), 0, s, offsets, (int)Ec, m);
   int rc = check_launch("newton_schulz5 offsets");
   if (rc) return rc;
   // the normalised X goes where the step count makes the last step land in X
   uint16_t* cur = (steps % 2 == 1) ? Xtmp : Xuser;
   uint16_t* nxt = (steps % 2 == 1) ? Xuser : Xtmp;
   const int64_t per_chunks = m * n / 8;
-  const dim3 grid((unsigned)L.P, (unsigned)E);
+  const dim3 grid((unsigned)L.P, (unsigned)Ec);
   hipLaunchKernelGGL(ns_sumsq_kernel, grid, dim3(kNsThreads), 0, s, Xuser, per_chunks, L.slice_chunks, L.P,
                      partial);
   rc = check_launch("newton_schulz5 norm");
@@ -166,13 +168,13 @@ extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int
   rc = check_launch("newton_schulz5 scale");
   if (rc) return rc;
 
-  const int64_t R = E * m;
+  const int64_t R = Ec * m;
   for (int it = 0; it < steps; ++it) {
     // A = X X^T, and cA as a second output
     NsGemm g1{};
     g1.A = cur; g1.lda = n;
     g1.B = cur; g1.b_estride = m * n; g1.ldb = n; g1.b_kn = false;
-    g1.offsets = offsets; g1.R = R; g1.K = (int)n; g1.N = (int)m; g1.E = (int)E;
+    g1.offsets = offsets; g1.R = R; g1.K = (int)n; g1.N = (int)m; g1.E = (int)Ec;
     g1.C = Abuf; g1.ldc = m;
     g1.C2 = Pbuf; g1.ldc2 = m; g1.gamma = c;
     g1.sym_m = (int)m;  // X X^T is symmetric: upper-triangle tiles plus their mirror
@@ -183,7 +185,7 @@ extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int
     NsGemm g2{};
     g2.A = Pbuf; g2.lda = m;
     g2.B = Abuf; g2.b_estride = m * m; g2.ldb = m; g2.b_kn = true;
-    g2.offsets = offsets; g2.R = R; g2.K = (int)m; g2.N = (int)m; g2.E = (int)E;
+    g2.offsets = offsets; g2.R = R; g2.K = (int)m; g2.N = (int)m; g2.E = (int)Ec;
     g2.C = Bbuf; g2.ldc = m;
     g2.D = Abuf; g2.ldd = m; g2.beta = b;
     g2.sym_m = (int)m;  // (cA) A + bA is symmetric (polynomial in the symmetric A)
@@ -193,7 +195,7 @@ extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int
     NsGemm g3{};
     g3.A = Bbuf; g3.lda = m;
     g3.B = cur; g3.b_estride = m * n; g3.ldb = n; g3.b_kn = true;
-    g3.offsets = offsets; g3.R = R; g3.K = (int)m; g3.N = (int)n; g3.E = (int)E;
+    g3.offsets = offsets; g3.R = R; g3.K = (int)m; g3.N = (int)n; g3.E = (int)Ec;
     g3.C = nxt; g3.ldc = n;
     g3.D = cur; g3.ldd = n; g3.beta = a;
     rc = ns_gemm(g3, s);
@@ -201,6 +203,33 @@ extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int
     uint16_t* t = cur;
     cur = nxt;
     nxt = t;
+  }
+  return ZMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int steps, float a, float b, float c,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  ZMOE_REQUIRE(E >= 1 && m >= 8 && n >= 8 && m <= n && steps >= 0, ZMOE_ERR_SHAPE,
+               "newton_schulz5: need E >= 1, 8 <= m <= n, steps >= 0 (E=%lld m=%lld n=%lld)", (long long)E,
+               (long long)m, (long long)n);
+  ZMOE_REQUIRE(m % 8 == 0 && n % 8 == 0, ZMOE_ERR_ALIGN, "newton_schulz5: m and n must be multiples of 8");
+  ZMOE_REQUIRE(m < (1 << 20) && n < (1 << 20) && m * n * 2 <= kNsMaxSpan, ZMOE_ERR_SHAPE,
+               "newton_schulz5: one matrix spans more than 2 GiB");
+  ZMOE_REQUIRE(X && workspace, ZMOE_ERR_NULL, "newton_schulz5: null pointer");
+  ZMOE_REQUIRE(aligned16(X) && (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, ZMOE_ERR_ALIGN,
+               "newton_schulz5: X must be 16-byte and the workspace 256-byte aligned");
+  const int64_t chunk = ns_chunk(E, m, n);
+  const size_t need = ns_layout(chunk, m, n).total;
+  ZMOE_REQUIRE(workspace_bytes >= need, ZMOE_ERR_WORKSPACE, "newton_schulz5: workspace %zu < %zu bytes",
+               workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  uint16_t* Xs = static_cast<uint16_t*>(X);
+  for (int64_t e0 = 0; e0 < E; e0 += chunk) {
+    const int64_t Ec = E - e0 < chunk ? E - e0 : chunk;
+    const int rc = ns_pass(Xs + e0 * m * n, Ec, m, n, steps, a, b, c, static_cast<char*>(workspace), s);
+    if (rc) return rc;
   }
   return ZMOE_OK;
 }

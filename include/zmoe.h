@@ -302,6 +302,8 @@ int zmoe_bias_update(const int64_t* expert_offsets, int E, float update_rate,
  * caller transposes a tall stack first, as muon.py:18-19 does), updated in place:
  *   X = X / (||X||_F + 1e-7);  repeat steps: A = X X^T; B = b A + (c A) A; X = a X + B X
  * with bf16 rounding after every product and sum, as in bf16 tensor arithmetic.
+ * Any E: the stack runs in passes of at most min(1024, (2 GiB - 64 KiB) / (2 m n))
+ * matrices over one pass-sized workspace (one matrix must span less than that).
  * Workspace: zmoe_newton_schulz5_workspace_bytes(E, m, n), 256-byte aligned.      */
 size_t zmoe_newton_schulz5_workspace_bytes(int64_t E, int64_t m, int64_t n);
 int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int steps, float a, float b, float c,

@@ -70,6 +70,8 @@ __all__ = [
     "glu_mlp_backward",
     "swiglu",
     "swiglu_backward",
+    "storage_rounder",
+    "summand_rss",
     "shared_expert_forward",
     "shared_expert_backward",
     "MoELayerOracle",
@@ -368,65 +370,161 @@ def swiglu_backward(dA, H):
     return np.concatenate([dh, dg], axis=-1)
 
 
-def glu_mlp_forward(x, expert_p, expert_idxs, W1, W2):
+def storage_rounder(store):
+    """The rounding applied where the path stores a tensor.
+
+    ``None``: exact (no rounding; the float64 restatement). ``"bf16"``: a value is
+    formed in this module's float type, rounded to float32 (the fp32 accumulator or
+    elementwise result) and then to bfloat16 (the stored activation), as every bf16
+    tensor the path writes is produced: GEMM outputs (scattermoe/kernels/ops.py:202,
+    :434 store in the operand dtype), elementwise results and the combine/k-sum rows.
+    """
+    if store is None:
+        return lambda a: a
+    if store == "bf16":
+        return lambda a: bf16_round(np.asarray(a, dtype=np.float32)).astype(_f())
+    raise ValueError(f"unknown store {store!r}")
+
+
+def glu_mlp_forward(x, expert_p, expert_idxs, W1, W2, store=None, gate_scale_on="Y", residual=None):
     """GLUMLP.forward (mlp.py:74-95).
 
     x [T, d]; expert_p, expert_idxs [T, k]; W1 [E, 2f, d] and W2 [E, d, f] in
     ``nn.Parameter`` storage (the reference permutes them to [E, in, out]).
-    Returns (y [T, d], cache) with the tensors the reference saves.
+
+    ``store`` rounds at the stored tensors (see ``storage_rounder``): H (:79-84), the
+    activation A (:85-87), the per-slot W2 outputs Y (:88-93) and the combined output.
+    ``gate_scale_on`` says where the routing weights multiply: ``"Y"`` on the W2 outputs
+    as the reference does (parallel_experts.py:50-52), ``"A"`` on the activations before
+    the W2 product (w (A W2) = (w A) W2, equal in exact arithmetic; the rounding points
+    differ). ``residual`` [T, d] (the shared expert's output, moe_layer.py:53) is added
+    before the output is rounded, as one pass forms both sums.
+    Returns (y [T, d], cache) with the tensors the backward needs.
     """
+    r = storage_rounder(store)
     x = np.asarray(x, dtype=_f())
     T, k = np.asarray(expert_idxs).shape
     E = np.asarray(W1).shape[0]
     se, ss, off = flatten_sort_count(expert_idxs, E)                          # :77-78
     W1l = np.transpose(np.asarray(W1, dtype=_f()), (0, 2, 1))
     W2l = np.transpose(np.asarray(W2, dtype=_f()), (0, 2, 1))
-    H, _ = parallel_linear_forward(x, W1l, k, se, ss, off, grouped_out=True)  # :79-84
-    A = swiglu(H)                                                             # :85-87
-    y, y_exp = parallel_linear_forward(A, W2l, 1, se, ss, off, gates=expert_p,  # :88-93
-                                       grouped_in=True)
-    cache = dict(x=x, se=se, ss=ss, off=off, H=H, A=A, y_exp=y_exp,
-                 gates=np.asarray(expert_p, dtype=_f()), k=k, W1l=W1l, W2l=W2l)
+    gates = np.asarray(expert_p, dtype=_f())
+    w_sorted = gates.reshape(-1)[ss]
+    H = r(scatter2scatter(x, W1l, se, ss, k, y_grouped=True))                 # :79-84
+    if gate_scale_on == "Y":
+        A = r(swiglu(H))                                                      # :85-87
+    elif gate_scale_on == "A":
+        A = r(w_sorted[:, None] * swiglu(H))
+    else:
+        raise ValueError("gate_scale_on must be 'Y' or 'A'")
+    Y = r(scatter2scatter(A, W2l, se, ss, 1, x_grouped=True, y_grouped=False))  # :88-93, slot order
+    Y3 = Y.reshape(T, k, -1)
+    y = np.einsum("tj,tjn->tn", gates, Y3) if gate_scale_on == "Y" else Y3.sum(axis=1)  # parallel_experts.py:50-52
+    if residual is not None:
+        y = np.asarray(residual, dtype=_f()) + y
+    y = r(y)
+    cache = dict(x=x, se=se, ss=ss, off=off, H=H, A=A, y_exp=Y3, gates=gates, w_sorted=w_sorted, k=k,
+                 W1l=W1l, W2l=W2l, store=store, gate_scale_on=gate_scale_on)
     return y, cache
 
 
-def glu_mlp_backward(dy, cache):
-    """Autograd of GLUMLP: returns (dx [T, d], dW1 [E, 2f, d], dW2 [E, d, f], d_gates [T, k])."""
+def summand_rss(sum_of_products, a, b):
+    """Root-sum-square of the summands of every element of a product-sum: the same
+    reduction ``sum_of_products(a, b)`` applied to a**2 and b**2, square-rooted.
+
+    It bounds the largest summand (max |a_r b_r| <= rss), so one bf16 ulp of any single
+    stored summand moves the sum by at most 2**-8 * rss: the scale of the rounding flips
+    that accumulation order alone causes in bf16 reductions (see tests/helpers.py)."""
+    return np.sqrt(sum_of_products(np.asarray(a, dtype=_f()) ** 2, np.asarray(b, dtype=_f()) ** 2))
+
+
+def glu_mlp_backward(dy, cache, rss=False):
+    """Autograd of GLUMLP (mlp.py:74-95 through parallel_experts.py:70-135), at the
+    rounding points of ``glu_mlp_forward``'s ``store``.
+
+    Returns (dx [T, d], dW1 [E, 2f, d], dW2 [E, d, f], d_gates [T, k]). dx (the k-sum of
+    the per-slot input grads, parallel_experts.py:125) and d_gates (fp32 in the path) are
+    not rounded: the caller adds its other input-grad terms before the one rounding.
+    With ``rss=True`` a fifth item maps "W1", "W2", "d_gates" to the root-sum-square of
+    each element's summands (``summand_rss``).
+    """
     c = cache
-    dA, dW2l, _, d_gates = parallel_linear_backward(
-        dy, c["A"], c["W2l"], 1, c["se"], c["ss"], c["off"], gates=c["gates"],
-        output_expanded=c["y_exp"], grouped_in=True)
-    dH = swiglu_backward(dA, c["H"])
-    dx, dW1l, _, _ = parallel_linear_backward(
-        dH, c["x"], c["W1l"], c["k"], c["se"], c["ss"], c["off"], grouped_out=True)
-    return dx, np.transpose(dW1l, (0, 2, 1)), np.transpose(dW2l, (0, 2, 1)), d_gates
+    r = storage_rounder(c["store"])
+    dy = np.asarray(dy, dtype=_f())
+    se, ss, off, k = c["se"], c["ss"], c["off"], c["k"]
+    E = c["W1l"].shape[0]
+    T = dy.shape[0]
+    W2t = np.transpose(c["W2l"], (0, 2, 1))
+    if c["gate_scale_on"] == "Y":
+        d_gates = rowwise_sum_product(c["y_exp"], dy)                         # :82
+        G = r(group(dy, ss, coeff=c["gates"].reshape(-1), fan_out=k))          # :95-97
+        dA = r(scatter2scatter(G, W2t, se, ss, 1, x_grouped=True, y_grouped=True))  # :112-120
+        dH = r(swiglu_backward(dA, c["H"]))
+    else:
+        # dout[t]'s rows unscaled; the gates' grad <dout[t], Y> = <dout[t] W2_e, A / w>
+        G = group(dy, ss, fan_out=k)
+        dA = r(scatter2scatter(G, W2t, se, ss, 1, x_grouped=True, y_grouped=True))
+        d_sorted = (dA * swiglu(c["H"])).sum(axis=1)
+        d_gates = np.empty(T * k, dtype=_f())
+        d_gates[ss] = d_sorted
+        d_gates = d_gates.reshape(T, k)
+        dH = r(swiglu_backward(c["w_sorted"][:, None] * dA, c["H"]))
+    dW2l, _ = group_bwd_w(G, c["A"], off, E)                                    # :105-110
+    grouped_x = group(c["x"], ss, fan_out=k)                                   # :98-103
+    dW1l, _ = group_bwd_w(dH, grouped_x, off, E)
+    W1t = np.transpose(c["W1l"], (0, 2, 1))
+    dXe = r(scatter2scatter(dH, W1t, se, ss, 1, x_grouped=True, y_grouped=False))
+    dx = dXe.reshape(T, k, -1).sum(axis=1)                                     # :125
+    out = (dx, r(np.transpose(dW1l, (0, 2, 1))), r(np.transpose(dW2l, (0, 2, 1))), d_gates)
+    if not rss:
+        return out
+    wsum = lambda a, b: group_bwd_w(a, b, off, E)[0]  # noqa: E731
+    if c["gate_scale_on"] == "Y":
+        g_rss = summand_rss(rowwise_sum_product, c["y_exp"], dy)
+    else:
+        g_rss = np.empty(T * k, dtype=_f())
+        g_rss[ss] = np.sqrt(((dA * swiglu(c["H"])) ** 2).sum(axis=1))
+        g_rss = g_rss.reshape(T, k)
+    return out + ({"W1": np.transpose(summand_rss(wsum, dH, grouped_x), (0, 2, 1)),
+                   "W2": np.transpose(summand_rss(wsum, G, c["A"]), (0, 2, 1)), "d_gates": g_rss},)
 
 
 # --------------------------------------------------------------------------- #
 # a14: shared expert (modeling/expert_layer.py:23-24)
 # --------------------------------------------------------------------------- #
-def shared_expert_forward(x, Wg, Wu, Wd):
-    """down(silu(gate(x)) * up(x)) with nn.Linear weights [out, in]."""
+def shared_expert_forward(x, Wg, Wu, Wd, store=None):
+    """down(silu(gate(x)) * up(x)) with nn.Linear weights [out, in]; ``store`` rounds
+    the two projections, the activation and the output."""
+    r = storage_rounder(store)
     x = np.asarray(x, dtype=_f())
-    g = x @ np.asarray(Wg, dtype=_f()).T
-    u = x @ np.asarray(Wu, dtype=_f()).T
-    a = _silu(g) * u
-    return a @ np.asarray(Wd, dtype=_f()).T, (x, g, u, a)
+    g = r(x @ np.asarray(Wg, dtype=_f()).T)
+    u = r(x @ np.asarray(Wu, dtype=_f()).T)
+    a = r(_silu(g) * u)
+    return r(a @ np.asarray(Wd, dtype=_f()).T), (x, g, u, a)
 
 
-def shared_expert_backward(dy, cache, Wg, Wu, Wd):
+def shared_expert_backward(dy, cache, Wg, Wu, Wd, store=None, rss=False):
+    """Returns (dx, dWg, dWu, dWd); dx is not rounded (the caller adds its other terms).
+    With ``rss=True`` a fifth item maps "gate", "up", "down" to the weight grads'
+    summand root-sum-squares."""
+    r = storage_rounder(store)
     x, g, u, a = cache
     dy = np.asarray(dy, dtype=_f())
     Wg = np.asarray(Wg, dtype=_f())
     Wu = np.asarray(Wu, dtype=_f())
     Wd = np.asarray(Wd, dtype=_f())
-    dWd = dy.T @ a
-    da = dy @ Wd
+    dWd = r(dy.T @ a)
+    da = r(dy @ Wd)
     s = 1.0 / (1.0 + np.exp(-g))
-    du = da * g * s
-    dg = da * u * s * (1.0 + g * (1.0 - s))
+    du = r(da * g * s)
+    dg = r(da * u * s * (1.0 + g * (1.0 - s)))
     dx = dg @ Wg + du @ Wu
-    return dx, dg.T @ x, du.T @ x, dWd
+    out = (dx, r(dg.T @ x), r(du.T @ x), dWd)
+    if not rss:
+        return out
+    tsum = lambda a, b: a.T @ b  # noqa: E731
+    return out + ({"gate": summand_rss(tsum, dg, x), "up": summand_rss(tsum, du, x),
+                   "down": summand_rss(tsum, dy, a)},)
 
 
 # --------------------------------------------------------------------------- #
@@ -443,9 +541,23 @@ class MoELayerOracle:
     ``logits`` may be supplied to forward() so the routing starts from exactly the
     gate projection the device computed (the projection itself is checked with a
     tolerance; routing from given logits is checked bit-exactly).
+
+    ``store`` / ``gate_scale_on``: as in ``glu_mlp_forward``. With ``store="bf16"`` the
+    gate's logits grad is rounded (it is stored in the logits dtype), and so is the
+    hidden states' grad: with ``gate_scale_on="A"`` (the layer as one function) the gate
+    and shared-expert input grads are formed by one product and rounded, then added to
+    the routed k-sum and rounded once more; with ``"Y"`` (the module composition) the
+    three terms are summed and rounded once (autograd's accumulation order is not
+    modelled; it moves the result by at most an ulp or two).
     """
 
-    def __init__(self, Wgate, expert_biases, W1, W2, k, shared=None, round_probs_bf16=False):
+    def __init__(self, Wgate, expert_biases, W1, W2, k, shared=None, round_probs_bf16=False, store=None,
+                 gate_scale_on="Y", expert_ids=None):
+        """``expert_ids`` (sorted, optional): W1 and W2 hold only these experts' weights
+        (a compact stack for checks on a few tokens of a wide layer); the routing still
+        runs over all gate rows, and tokens must select only these experts. dW1 / dW2
+        then cover the same experts."""
+        self.expert_ids = None if expert_ids is None else np.asarray(expert_ids, dtype=np.int64)
         self.Wgate = np.asarray(Wgate, dtype=_f())
         self.bias = np.asarray(expert_biases, dtype=np.float32)
         self.W1 = np.asarray(W1, dtype=_f())
@@ -453,36 +565,53 @@ class MoELayerOracle:
         self.k = int(k)
         self.shared = None if shared is None else tuple(np.asarray(w, dtype=_f()) for w in shared)
         self.round_probs_bf16 = round_probs_bf16
+        self.store = store
+        self.gate_scale_on = gate_scale_on
 
     def forward(self, x, logits=None):
         x = np.asarray(x, dtype=_f())
         if logits is None:
             logits = (x @ self.Wgate.T).astype(np.float32)                    # moe_gate.py:26
         idx, w, p_sel = route_topk(logits, self.bias, self.k, self.round_probs_bf16)
-        y, mcache = glu_mlp_forward(x, w, idx, self.W1, self.W2)               # moe_layer.py:51
-        out = y
-        scache = None
+        scache, ys = None, None
         if self.shared is not None:
-            ys, scache = shared_expert_forward(x, *self.shared)                # moe_layer.py:47
-            out = ys + y                                                       # moe_layer.py:53
+            ys, scache = shared_expert_forward(x, *self.shared, store=self.store)   # moe_layer.py:47
+        local = idx
+        if self.expert_ids is not None:
+            local = np.searchsorted(self.expert_ids, idx)
+            if np.any(local >= self.expert_ids.size) or np.any(self.expert_ids[np.minimum(
+                    local, self.expert_ids.size - 1)] != idx):
+                raise ValueError("a token selected an expert outside expert_ids")
+        out, mcache = glu_mlp_forward(x, w, local, self.W1, self.W2, store=self.store,  # moe_layer.py:51-53
+                                      gate_scale_on=self.gate_scale_on, residual=ys)
         self._cache = dict(x=x, idx=idx, w=w, p_sel=p_sel, mcache=mcache, scache=scache)
         return out, idx, w
 
-    def backward(self, dout):
-        """Returns dict of float64 grads: x, gate_weight, W1, W2 (+ shared_*)."""
+    def backward(self, dout, rss=False):
+        """Returns dict of grads: x, gate_weight, W1, W2 (+ shared_*), d_gates, d_logits.
+        With ``rss=True`` also "rss": the summand root-sum-square of every weight grad and
+        of d_gates, keyed like the grads."""
+        r = storage_rounder(self.store)
         c = self._cache
         dout = np.asarray(dout, dtype=_f())
-        dx, dW1, dW2, d_gates = glu_mlp_backward(dout, c["mcache"])
+        res = glu_mlp_backward(dout, c["mcache"], rss=rss)
+        dx_routed, dW1, dW2, d_gates = res[:4]
         E = self.Wgate.shape[0]
-        dz = route_topk_backward(d_gates, c["p_sel"], c["idx"], E)
-        grads = {}
-        dx = dx + dz @ self.Wgate
-        grads["gate_weight"] = dz.T @ c["x"]
+        dz = r(route_topk_backward(d_gates, c["p_sel"], c["idx"], E))
+        grads = {"gate_weight": r(dz.T @ c["x"])}
+        if rss:
+            grads["rss"] = dict(res[4], gate_weight=summand_rss(lambda a, b: a.T @ b, dz, c["x"]))
+        dx_dense = dz @ self.Wgate
         if self.shared is not None:
-            dxs, dWg, dWu, dWd = shared_expert_backward(dout, c["scache"], *self.shared)
-            dx = dx + dxs
+            sres = shared_expert_backward(dout, c["scache"], *self.shared, store=self.store, rss=rss)
+            dxs, dWg, dWu, dWd = sres[:4]
+            dx_dense = dx_dense + dxs
             grads.update(shared_gate=dWg, shared_up=dWu, shared_down=dWd)
-        grads.update(x=dx, W1=dW1, W2=dW2, d_gates=d_gates, d_logits=dz)
+            if rss:
+                grads["rss"].update({"shared_" + n: v for n, v in sres[4].items()})
+        if self.gate_scale_on == "A":
+            dx_dense = r(dx_dense)
+        grads.update(x=r(dx_routed + dx_dense), W1=dW1, W2=dW2, d_gates=d_gates, d_logits=dz)
         return grads
 
 

@@ -72,3 +72,37 @@ def test_argument_errors_are_reported_without_a_gpu():
     p = ctypes.c_void_p(256)
     rc = lib.zmoe_scatter2scatter(p, 12, p, 12 * 16, 16, 1, None, 0, p, p, p, 4, 12, 16, 2, 1, 0, 0, 1, p, 16, None)
     assert rc == 4
+
+
+def test_dense_wgrad_workspace_holds_every_split_offset():
+    """The split offsets (one int64 per split, up to 64 splits) sit in a header ahead of the
+    fp32 partials; the header must hold all 64 so that the offsets of splits 32..63 do not
+    land in split 0's partials. The automatic choice reaches 64 splits."""
+    from zmoe import _lib, ops
+
+    lib = _lib.load()
+    assert ops.dense_wgrad_splits(65536, 8, 256) == 64
+    assert all(1 <= ops.dense_wgrad_splits(M, 2048, 2176) <= 64 for M in (0, 1000, 32768, 1 << 20))
+    hdr = lib.zmoe_dense_wgrad_workspace_bytes(8, 256, 0)
+    assert hdr >= 64 * 8 and hdr % 256 == 0
+    assert lib.zmoe_dense_wgrad_workspace_bytes(8, 256, 64) == hdr + 64 * 8 * 256 * 4
+    # more than 64 splits is refused before any launch
+    p = ctypes.c_void_p(256)
+    rc = lib.zmoe_dense_wgrad(p, 8, p, 256, 65536, 8, 256, 1, 65, p, p, 1 << 30, None)
+    assert rc == 2
+
+
+def test_newton_schulz_workspace_is_sized_for_one_pass():
+    """Stacks of any length run in passes of at most 1024 matrices spanning under 2 GiB,
+    so the workspace of a long stack equals that of one full pass."""
+    from zmoe import _lib
+
+    lib = _lib.load()
+    one = lib.zmoe_newton_schulz5_workspace_bytes(1023, 256, 4096)     # 1023 x 2 MiB fills one pass
+    assert one > 0
+    assert lib.zmoe_newton_schulz5_workspace_bytes(1100, 256, 4096) == one
+    assert lib.zmoe_newton_schulz5_workspace_bytes(5000, 256, 4096) == one
+    # C4's W1 stack [256, 4096, 7168] (15 GB) runs in passes of 36 matrices
+    c4 = lib.zmoe_newton_schulz5_workspace_bytes(256, 4096, 7168)
+    assert c4 == lib.zmoe_newton_schulz5_workspace_bytes(36, 4096, 7168)
+    assert lib.zmoe_newton_schulz5_workspace_bytes(1, 65536, 65536) == 0  # one matrix above 2 GiB

@@ -40,14 +40,15 @@ def test_glumlp_reference_call_forward_backward(hip_device):
 
     xr = np64(x.to(torch.bfloat16))
     W1r, W2r = np64(W1.to(torch.bfloat16)), np64(W2.to(torch.bfloat16))
-    ry, cache = O.glu_mlp_forward(xr, np64(p), idx.numpy(), W1r, W2r)
-    rdx, rdW1, rdW2, rdg = O.glu_mlp_backward(np64(dy.to(torch.bfloat16)), cache)
+    # bf16 storage model of this path (routing weights on the W2 outputs)
+    ry, cache = O.glu_mlp_forward(xr, np64(p), idx.numpy(), W1r, W2r, store="bf16", gate_scale_on="Y")
+    rdx, rdW1, rdW2, rdg, rss = O.glu_mlp_backward(np64(dy.to(torch.bfloat16)), cache, rss=True)
     tol = TOL[torch.bfloat16]
     assert_close(np64(y), ry, **tol, what="y")
     assert_close(np64(xd.grad), rdx, **tol, what="dx")
-    assert_close(np64(pd.grad), rdg, **tol, what="d expert_p")
-    assert_close(np64(mlp.experts.weight.grad), rdW1, **tol, what="dW1")
-    assert_close(np64(mlp.output_experts.weight.grad), rdW2, **tol, what="dW2")
+    assert_close(np64(pd.grad), rdg, **tol, what="d expert_p", rss=rss["d_gates"])
+    assert_close(np64(mlp.experts.weight.grad), rdW1, **tol, what="dW1", rss=rss["W1"])
+    assert_close(np64(mlp.output_experts.weight.grad), rdW2, **tol, what="dW2", rss=rss["W2"])
     # the sort's offsets of this forward are kept on the module
     counts = np.bincount(idx.numpy().reshape(-1), minlength=E)
     np.testing.assert_array_equal(mlp.last_expert_offsets.cpu().numpy(), np.cumsum(counts))

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import TOL, assert_close, gen, np64, random_topk
+from helpers import TOL, assert_close, assert_close_fro, gen, np64, random_topk
 
 pytestmark = pytest.mark.gpu
 
@@ -76,7 +76,10 @@ def test_group_bwd_w(hip_device, dtype, T, K, N, E, k, skew, gather):
                              x_gather=ss if gather else None, x_div=k)
     Xg = O.group(np64(X), ss.cpu().numpy(), fan_out=k) if gather else np64(X)
     ref, _ = O.group_bwd_w(np64(DY), Xg, off.cpu().numpy(), E)  # [E, K, N]
-    assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[dtype], what="group_bwd_w")
+    if dtype == torch.float32:  # fp32 sums over up to ~2000 rows: the norm-wise fp32 bound
+        assert_close_fro(np64(DWt), ref.transpose(0, 2, 1), what="group_bwd_w f32")
+    else:
+        assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[dtype], what="group_bwd_w")
     counts = np.diff(np.concatenate([[0], off.cpu().numpy()]))
     for e in np.nonzero(counts == 0)[0]:
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
@@ -225,11 +228,19 @@ def test_glu_w2_backward_dh_gates(hip_device, T, d, f, E, k, skew):
     assert_close(np64(dH), O.swiglu_backward(dA, np64(H)), **tol, what="dH")
     Y = O.scatter2scatter(np64(A), np64(W2).transpose(0, 2, 1), se_n, ss_n, 1, x_grouped=True, y_grouped=False)
     ref = O.rowwise_sum_product(Y.reshape(T, k, d), np64(dout))
-    assert_close(d_gates.cpu().numpy().astype(np.float64), ref, **tol, what="d_gates")
+    # the kernel forms <dout[t], Y> as sum_c (dout[t] W2_e)_c A_c from its staged bf16 dA:
+    # bound by the root-sum-square of those f summands (see helpers.TOL)
+    dAu = O.scatter2scatter(O.group(np64(dout), ss_n, fan_out=k), np64(W2), se_n, ss_n, 1, x_grouped=True,
+                            y_grouped=True)
+    rss = np.empty(T * k)
+    rss[ss_n] = np.sqrt(((dAu * np64(A)) ** 2).sum(axis=1))
+    assert_close(d_gates.cpu().numpy().astype(np.float64), ref, **tol, what="d_gates", rss=rss.reshape(T, k))
 
 
 @pytest.mark.parametrize("M,N,K,splits", [(1000, 128, 256, None), (1000, 128, 256, 3), (4100, 256, 512, 7),
-                                          (4096, 136, 264, 1), (0, 128, 128, 4), (20000, 1536, 512, None)])
+                                          (4096, 136, 264, 1), (0, 128, 128, 4), (20000, 1536, 512, None),
+                                          # 33..64 splits, more tiles than the GPU has CUs
+                                          (40000, 512, 768, 48), (70000, 512, 768, 64), (65536, 8, 256, None)])
 def test_dense_wgrad_bf16(hip_device, M, N, K, splits):
     """DW = DY^T X with split-K fp32 partials (the nn.Linear weight grads of the shared
     expert and gate projection) against float64."""
@@ -250,4 +261,4 @@ def test_dense_wgrad_f32(hip_device):
     DY = torch.randn(777, 64, generator=g)
     X = torch.randn(777, 96, generator=g)
     DW = ops.dense_wgrad(DY.to(hip_device), X.to(hip_device), splits=4)
-    assert_close(np64(DW), np64(DY).T @ np64(X), **TOL[torch.float32], what="dense_wgrad f32")
+    assert_close_fro(np64(DW), np64(DY).T @ np64(X), what="dense_wgrad f32")  # 777-row fp32 sums

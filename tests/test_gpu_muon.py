@@ -105,3 +105,26 @@ def test_c3_expert_stack(hip_device, name, shape):
             s = a * s + b * s**3 + c * s**5
         s_exact = np.sort(s)[::-1]
         assert np.max(np.abs(s_got - s_exact)) < 0.1, (name, e, np.max(np.abs(s_got - s_exact)))
+
+
+@pytest.mark.parametrize("shape", [(1100, 256, 4096),   # 2.3 GB: passes of 1023 and 77 matrices
+                                   (1030, 64, 64)])     # more than 1024 matrices of one tile
+def test_stack_beyond_one_pass(hip_device, shape):
+    """Stacks that span more than 2 GiB or hold more than 1024 matrices run in passes over
+    one pass-sized workspace. Each matrix is independent, so every matrix of the whole
+    stack equals, bit for bit, the same matrix run in a small stack of its own; sampled
+    matrices on both sides of a pass boundary are also checked against the oracle."""
+    from zmoe import ops
+
+    E, m, n = shape
+    G = make_stack(shape, 21, hip_device).to(torch.bfloat16)
+    out = ops.newton_schulz5(G, 5)
+    torch.cuda.synchronize()
+    chunk = min(1024, (0x7FFF0000) // (m * n * 2))
+    picks = sorted({0, chunk - 1, min(chunk, E - 1), E - 1})
+    alone = ops.newton_schulz5(G[picks].contiguous(), 5)
+    assert torch.equal(out[picks], alone), (shape, picks)
+    for e in picks[:2] + picks[-1:]:
+        got = out[e].float().cpu().numpy()
+        ref = O.newton_schulz5(G[e].float().cpu().numpy()[None], 5)[0]
+        assert rel_fro(got, ref) <= REL_FRO[5], (shape, e, rel_fro(got, ref))
