@@ -12,6 +12,8 @@
 //      keep slot order (stable).
 // Out-of-range ids land after every valid slot (bucket E) with their original
 // value, so every output stays a permutation; the scan raises a flag.
+#include <mutex>
+
 #include "zmoe_internal.h"
 
 namespace zmoe {
@@ -189,21 +191,27 @@ extern "C" const int32_t* zmoe_sort_error_flag(const void* workspace) {
   return reinterpret_cast<const int32_t*>(workspace);
 }
 
-extern "C" int zmoe_flatten_sort_count(const int64_t* expert_idxs, int64_t R, int E, int64_t* sorted_expert_idxs,
-                                       int64_t* sorted_scattered_idxs, int64_t* expert_offsets, int32_t* inverse,
-                                       void* workspace, size_t workspace_bytes, void* stream) {
-  ZMOE_REQUIRE(E >= 1 && E <= kSortMaxE, ZMOE_ERR_SHAPE, "flatten_sort_count: need 1 <= E <= %d (E=%d)",
-               kSortMaxE, E);
-  ZMOE_REQUIRE(R >= 0 && R < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "flatten_sort_count: R=%lld out of range",
-               (long long)R);
-  ZMOE_REQUIRE(expert_offsets && workspace, ZMOE_ERR_NULL, "flatten_sort_count: null offsets/workspace");
-  ZMOE_REQUIRE(workspace_bytes >= zmoe_sort_workspace_bytes(R, E), ZMOE_ERR_WORKSPACE,
-               "flatten_sort_count: workspace %zu < %zu bytes", workspace_bytes, zmoe_sort_workspace_bytes(R, E));
+namespace {
+
+int sort_shape_checks(int64_t R, int E, int64_t* expert_offsets, const char* name) {
+  ZMOE_REQUIRE(E >= 1 && E <= kSortMaxE, ZMOE_ERR_SHAPE, "%s: need 1 <= E <= %d (E=%d)", name, kSortMaxE, E);
+  ZMOE_REQUIRE(R >= 0 && R < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "%s: R=%lld out of range", name, (long long)R);
+  ZMOE_REQUIRE(expert_offsets, ZMOE_ERR_NULL, "%s: null expert_offsets", name);
+  return ZMOE_OK;
+}
+
+int sort_pointer_checks(const int64_t* expert_idxs, int64_t R, int64_t* sorted_expert_idxs,
+                        int64_t* sorted_scattered_idxs, const char* name) {
   ZMOE_REQUIRE(R == 0 || (expert_idxs && sorted_expert_idxs && sorted_scattered_idxs), ZMOE_ERR_NULL,
-               "flatten_sort_count: null pointer");
-  hipStream_t s = as_stream(stream);
-  int32_t* flag = reinterpret_cast<int32_t*>(workspace);
-  int32_t* tile_hist = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kSortHeader);
+               "%s: null pointer", name);
+  return ZMOE_OK;
+}
+
+// The three launches over a workspace laid out as [flag | header padding | tile table];
+// every byte they read is written earlier in the same call, so nothing needs clearing.
+int sort_launch(const int64_t* expert_idxs, int64_t R, int E, int64_t* sorted_expert_idxs,
+                int64_t* sorted_scattered_idxs, int64_t* expert_offsets, int32_t* inverse, int32_t* flag,
+                int32_t* tile_hist, hipStream_t s, const char* name) {
   const int ntiles = (int)cdiv(R, kSortTile);
   if (ntiles > 0)
     hipLaunchKernelGGL(sort_hist_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, tile_hist);
@@ -211,7 +219,81 @@ extern "C" int zmoe_flatten_sort_count(const int64_t* expert_idxs, int64_t R, in
   if (ntiles > 0)
     hipLaunchKernelGGL(sort_scatter_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, tile_hist,
                        sorted_expert_idxs, sorted_scattered_idxs, inverse);
-  return check_launch("flatten_sort_count");
+  return check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int zmoe_flatten_sort_count(const int64_t* expert_idxs, int64_t R, int E, int64_t* sorted_expert_idxs,
+                                       int64_t* sorted_scattered_idxs, int64_t* expert_offsets, int32_t* inverse,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = sort_shape_checks(R, E, expert_offsets, "flatten_sort_count");
+  if (rc) return rc;
+  ZMOE_REQUIRE(workspace, ZMOE_ERR_NULL, "flatten_sort_count: null workspace");
+  ZMOE_REQUIRE(workspace_bytes >= zmoe_sort_workspace_bytes(R, E), ZMOE_ERR_WORKSPACE,
+               "flatten_sort_count: workspace %zu < %zu bytes", workspace_bytes, zmoe_sort_workspace_bytes(R, E));
+  rc = sort_pointer_checks(expert_idxs, R, sorted_expert_idxs, sorted_scattered_idxs, "flatten_sort_count");
+  if (rc) return rc;
+  int32_t* flag = reinterpret_cast<int32_t*>(workspace);
+  int32_t* tile_hist = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kSortHeader);
+  return sort_launch(expert_idxs, R, E, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets, inverse, flag,
+                     tile_hist, as_stream(stream), "flatten_sort_count");
+}
+
+// ------------------------------------------------------------------ no-allocation variant
+// The sort's workspace as a file-scope device array, for callers that cannot allocate.
+// Every GPU the library runs on holds one copy, at its own address, until the process
+// ends. In host code the array's name is not a device address: kernels get the pointer
+// that hipGetSymbolAddress returns for the current device (looked up once per device).
+constexpr size_t kSortScratchBytes = ZMOE_SORT_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kSortScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  ZMOE_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices, ZMOE_ERR_HIP,
+               "flatten_sort_count_noalloc: hipGetDevice failed (%s, device %d)", hipGetErrorString(e), dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    ZMOE_REQUIRE(e == hipSuccess && ptr != nullptr, ZMOE_ERR_HIP,
+                 "flatten_sort_count_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                 hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ZMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int zmoe_flatten_sort_count_noalloc(const int64_t* expert_idxs, int64_t R, int E,
+                                               int64_t* sorted_expert_idxs, int64_t* sorted_scattered_idxs,
+                                               int64_t* expert_offsets, int32_t* inverse, int32_t* error_flag,
+                                               void* stream) {
+  int rc = sort_shape_checks(R, E, expert_offsets, "flatten_sort_count_noalloc");
+  if (rc) return rc;
+  const size_t need = zmoe_sort_workspace_bytes(R, E);
+  ZMOE_REQUIRE(need <= kSortScratchBytes, ZMOE_ERR_WORKSPACE,
+               "flatten_sort_count_noalloc: R=%lld slots over E=%d experts need %zu bytes of scratch, above its "
+               "%zu-byte maximum (ceil(R / %d) * (E + 1) * 4 + %zu); use zmoe_flatten_sort_count with a workspace",
+               (long long)R, E, need, kSortScratchBytes, kSortTile, kSortHeader);
+  rc = sort_pointer_checks(expert_idxs, R, sorted_expert_idxs, sorted_scattered_idxs, "flatten_sort_count_noalloc");
+  if (rc) return rc;
+  void* base = nullptr;
+  rc = scratch_for_current_device(&base);
+  if (rc) return rc;
+  int32_t* flag = error_flag ? error_flag : reinterpret_cast<int32_t*>(base);
+  int32_t* tile_hist = reinterpret_cast<int32_t*>(static_cast<char*>(base) + kSortHeader);
+  return sort_launch(expert_idxs, R, E, sorted_expert_idxs, sorted_scattered_idxs, expert_offsets, inverse, flag,
+                     tile_hist, as_stream(stream), "flatten_sort_count_noalloc");
 }
 
 extern "C" int zmoe_bincount(const int64_t* expert_idxs, int64_t R, int E, int64_t* counts, void* stream) {

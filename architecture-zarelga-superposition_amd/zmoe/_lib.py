@@ -42,6 +42,7 @@ SIGNATURES = {
     "zmoe_sort_workspace_bytes": (SZ, [I64, I32]),
     "zmoe_flatten_sort_count": (I32, [P, I64, I32, P, P, P, P, P, SZ, P]),
     "zmoe_sort_error_flag": (P, [P]),
+    "zmoe_flatten_sort_count_noalloc": (I32, [P, I64, I32, P, P, P, P, P, P]),
     "zmoe_offsets_from_sorted": (I32, [P, I64, I32, P, P]),
     "zmoe_group": (I32, [P, I64, I64, I32, P, I64, I32, P, I32, P, I64, P]),
     "zmoe_scatter2scatter": (I32, [P, I64, P, I64, I64, I64, P, I64, P, P, P, I64, I64, I64, I32, I32, I32, I32,

@@ -94,6 +94,26 @@ int zmoe_flatten_sort_count(const int64_t* expert_idxs, int64_t R, int E,
 /* Device address of the out-of-range flag inside a sort workspace. */
 const int32_t* zmoe_sort_error_flag(const void* workspace);
 
+/* ---------------------------------------------------------------------------
+ * flatten_sort_count without a workspace argument: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * kernels and results as zmoe_flatten_sort_count; the tile table lives in a
+ * file-scope device array of ZMOE_SORT_NOALLOC_MAX_BYTES per GPU (held until the
+ * process ends), so the call allocates nothing. Sizes whose workspace
+ * (zmoe_sort_workspace_bytes(R, E)) exceeds that maximum return
+ * ZMOE_ERR_WORKSPACE: R up to ~16.6 M slots at E = 128, ~2.1 M at E = 1024.
+ * error_flag (nullable, caller-owned device int32) receives 1 when an id was
+ * outside [0, E), else 0. Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (different streams, threads) race; the array needs no
+ * clearing (each call writes what it reads).
+ * ------------------------------------------------------------------------- */
+#define ZMOE_SORT_NOALLOC_MAX_BYTES ((size_t)4 << 20)
+int zmoe_flatten_sort_count_noalloc(const int64_t* expert_idxs, int64_t R, int E,
+                                    int64_t* sorted_expert_idxs, int64_t* sorted_scattered_idxs,
+                                    int64_t* expert_offsets, int32_t* inverse, int32_t* error_flag,
+                                    void* stream);
+
 /* expert_offsets [E] (inclusive) from an already sorted expert list; used by
  * scatter2scatter callers that do not carry offsets (ops.py:192 signature). */
 int zmoe_offsets_from_sorted(const int64_t* sorted_expert_idxs, int64_t R, int E,
