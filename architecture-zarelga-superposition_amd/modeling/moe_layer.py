@@ -3,8 +3,10 @@
 Same submodules, parameters and state-dict keys as the reference:
 ``gate`` (MoEGate), ``shared_experts`` (ExpertMLP), ``routed_experts`` (GLUMLP).
 The optional unpad around the layer (the reference uses flash-attn's
-index_first_axis) is a torch gather; the re-pad of the output (pad_input) is folded
-into the routed experts' combine pass, which writes the padded layout directly.
+index_first_axis) is folded into the RMSNorm pass when the block's norm is passed
+(``forward(..., norm=...)``), else a torch gather; the re-pad of the output
+(pad_input) is folded into the routed experts' combine pass, which writes the padded
+layout directly.
 """
 
 import torch
@@ -12,6 +14,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from scattermoe.mlp import GLUMLP
+from zmoe import functional as _zf
 from zmoe import ops as _z
 
 from .expert_layer import ExpertMLP
@@ -156,23 +159,40 @@ class MoELayer(nn.Module):
               and ws[4].shape[0] % 8 == 0 and ws[0].shape[0] % 8 == 0)    # 16-byte rows of the dH | d_logits buffer
         return ws if ok else None
 
-    def forward(self, hidden_states, unpad_indices=None):
-        ws = self._fused_weights(hidden_states)
+    def forward(self, hidden_states, unpad_indices=None, norm=None):
+        """(out, topk_idx) as the reference's forward (moe_layer.py:38-59).
+
+        ``norm`` (a ZeroCenteredRMSNorm, optional): the layer's input is
+        ``norm(hidden_states)``, as the transformer block computes it before calling the
+        layer (transformer_block.py:41-42); the normalisation and the unpad gather then
+        run as one row pass (zmoe_rmsnorm_rows) instead of a norm pass and a gather."""
+        bsz, seq_len, h = hidden_states.shape
+        normed = None
+        if norm is not None:
+            # x = norm(hidden)[unpad_indices] in one pass; the layer sees already-gathered rows
+            normed = _zf.rmsnorm_rows(hidden_states.reshape(bsz * seq_len, h), norm.weight, norm.eps,
+                                      rows=unpad_indices)
+            if unpad_indices is None:
+                normed = normed.view(bsz, seq_len, h)
+        ws = self._fused_weights(hidden_states if normed is None else normed.view(1, -1, h))
         if ws is not None:
-            bsz, seq_len, h = hidden_states.shape
             flat = hidden_states.reshape(bsz * seq_len, h)
             stash = {}
             pad = () if unpad_indices is None else (unpad_indices, bsz * seq_len)
-            x = flat if unpad_indices is None else index_first_axis(flat, unpad_indices)
+            if normed is not None:
+                x = normed.reshape(-1, h)
+            else:
+                x = flat if unpad_indices is None else index_first_axis(flat, unpad_indices)
             out, topk_idx = _FusedMoELayer.apply(x, ws[0], self.gate.expert_biases, *ws[1:], self.gate.top_k,
                                                  self.routed_experts.num_experts, stash, *pad)
             self.routed_experts.last_expert_offsets = stash["expert_offsets"]
             if unpad_indices is None:
                 return out.view(bsz, seq_len, h), topk_idx.view(bsz, seq_len, -1)
             return out.view(bsz, seq_len, h), pad_input(topk_idx, unpad_indices, bsz, seq_len)
-        if unpad_indices is not None:
-            bsz, seq_len = hidden_states.shape[:2]
-            flat = hidden_states.reshape(bsz * seq_len, hidden_states.shape[-1])
+        if normed is not None:
+            x = normed if unpad_indices is None else normed.unsqueeze(0)
+        elif unpad_indices is not None:
+            flat = hidden_states.reshape(bsz * seq_len, h)
             x = index_first_axis(flat, unpad_indices).unsqueeze(0)
         else:
             x = hidden_states

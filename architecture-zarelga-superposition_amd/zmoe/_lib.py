@@ -66,6 +66,9 @@ SIGNATURES = {
     "zmoe_swiglu_backward": (I32, [P, P, I64, I64, I32, P, I64, P]),
     "zmoe_swiglu_backward_gates": (I32, [P, P, I64, I64, P, P, I32, P, P, P]),
     "zmoe_bias_update": (I32, [P, I32, F32, P, P]),
+    "zmoe_rmsnorm_rows": (I32, [P, I64, I64, P, I64, I64, P, I32, F32, I32, P, P, P]),
+    "zmoe_rmsnorm_rows_backward_workspace_bytes": (SZ, [I64, I64, I32]),
+    "zmoe_rmsnorm_rows_backward": (I32, [P, P, I64, I64, P, I64, I64, P, P, I32, I32, P, I64, P, P, SZ, P]),
     "zmoe_newton_schulz5_workspace_bytes": (SZ, [I64, I64, I64]),
     "zmoe_newton_schulz5": (I32, [P, I64, I64, I64, I32, F32, F32, F32, P, SZ, P]),
 }

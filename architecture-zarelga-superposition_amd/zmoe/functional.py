@@ -15,6 +15,8 @@ reference does.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 import torch.nn.functional as F
 
@@ -84,3 +86,30 @@ def swiglu_mlp(x: torch.Tensor, W_gate: torch.Tensor, W_up: torch.Tensor, W_down
     lead = x.shape[:-1]
     y = _SwiGLUMLP.apply(x.reshape(-1, x.shape[-1]), W_gate, W_up, W_down)
     return y.view(*lead, W_down.shape[0])
+
+
+class _RMSNormRows(torch.autograd.Function):
+    """x = ZeroCenteredRMSNorm(hidden)[rows] (zRMSNorm.py:10-17, then moe_layer.py:39-42)."""
+
+    @staticmethod
+    def forward(ctx, hidden2, weight, eps: float, rows):
+        y, rstd = ops.rmsnorm_rows(hidden2, weight, eps, rows)
+        ctx.save_for_backward(hidden2, weight, rstd, rows if rows is not None else torch.empty(0))
+        ctx.has_rows = rows is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        hidden2, weight, rstd, rows = ctx.saved_tensors
+        dx, dw = ops.rmsnorm_rows_backward(dy.contiguous(), hidden2, rows if ctx.has_rows else None, rstd, weight)
+        return dx, dw, None, None
+
+
+def rmsnorm_rows(hidden: torch.Tensor, weight: torch.Tensor, eps: float,
+                 rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """ZeroCenteredRMSNorm of ``hidden`` [..., d], gathered at flat rows ``rows`` (None: all
+    rows, keeping hidden's shape; else [len(rows), d]). One HIP pass each way."""
+    d = hidden.shape[-1]
+    flat = hidden.reshape(-1, d)
+    y = _RMSNormRows.apply(flat, weight, float(eps), rows)
+    return y.view(hidden.shape) if rows is None else y

@@ -520,6 +520,48 @@ def bias_update_(expert_biases: torch.Tensor, expert_offsets: torch.Tensor, upda
     return expert_biases
 
 
+def rmsnorm_rows(X: torch.Tensor, weight: torch.Tensor, eps: float, rows: Optional[torch.Tensor] = None):
+    """modeling/zRMSNorm.py:10-17 on rows ``rows`` of X [N, d] (all rows when None):
+    returns (Y [n, d] in X's dtype, rstd [n] f32)."""
+    dev = _require_cuda(X, weight, rows)
+    X = _rows(X)
+    N, d = X.shape
+    if weight.numel() != d:
+        raise ValueError("rmsnorm_rows: weight must have d entries")
+    w = weight.reshape(-1).contiguous()
+    r = None if rows is None else _idx64(rows)
+    n = N if r is None else r.numel()
+    Y = torch.empty((n, d), dtype=X.dtype, device=dev)
+    rstd = torch.empty(n, dtype=torch.float32, device=dev)
+    with profiling.region("rmsnorm_rows", dev):
+        L.call("zmoe_rmsnorm_rows", _ptr(X), X.stride(0), N, _ptr(r), n, d, _ptr(w), _dtype_code(w), float(eps),
+               _dtype_code(X), _ptr(Y), _ptr(rstd), _stream(dev))
+    return Y, rstd
+
+
+def rmsnorm_rows_backward(dY: torch.Tensor, X: torch.Tensor, rows: Optional[torch.Tensor], rstd: torch.Tensor,
+                          weight: torch.Tensor):
+    """Backward of ``rmsnorm_rows``: (dX [N, d] with zeros outside ``rows``, dweight [d])."""
+    dev = _require_cuda(dY, X, rows, rstd, weight)
+    X = _rows(X)
+    N, d = X.shape
+    dY = dY.to(X.dtype).contiguous()
+    r = None if rows is None else _idx64(rows)
+    n = N if r is None else r.numel()
+    if dY.shape != (n, d) or rstd.numel() != n:
+        raise ValueError("rmsnorm_rows_backward: dY must be [n, d] and rstd [n]")
+    w = weight.reshape(-1).contiguous()
+    dX = torch.empty_like(X) if r is None else torch.zeros((N, d), dtype=X.dtype, device=dev)
+    dw = torch.empty(d, dtype=w.dtype, device=dev)
+    nbytes = L.load().zmoe_rmsnorm_rows_backward_workspace_bytes(n, d, _dtype_code(X))
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    with profiling.region("rmsnorm_rows_backward", dev):
+        L.call("zmoe_rmsnorm_rows_backward", _ptr(dY), _ptr(X), X.stride(0), N, _ptr(r), n, d,
+               _ptr(rstd.contiguous()), _ptr(w), _dtype_code(w), _dtype_code(X), _ptr(dX), dX.stride(0), _ptr(dw),
+               _ptr(ws), ws.numel(), _stream(dev))
+    return dX, dw.view(weight.shape)
+
+
 NS_COEFFS = (3.4445, -4.7750, 2.0315)  # optimizer/muon.py:16
 
 

@@ -316,6 +316,34 @@ int zmoe_swiglu_backward_gates(const void* dA, const void* H, int64_t R, int64_t
 int zmoe_bias_update(const int64_t* expert_offsets, int E, float update_rate,
                      float* expert_biases, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * ZeroCenteredRMSNorm (modeling/zRMSNorm.py:10-17) fused with the unpad gather
+ * that follows it (modeling/transformer_block.py:41-42 normalises, then
+ * modeling/moe_layer.py:39-42 gathers the valid tokens with index_first_axis):
+ *   Y[i] = X[rows[i]] * rsqrt(mean_j X[rows[i], j]^2 + eps) * (1 + w)
+ * in fp32, stored in X's dtype. X [x_rows, x_stride]; rows [n] int64 (NULL:
+ * rows[i] = i; a row outside [0, x_rows) gives a zero output row); Y [n, d]
+ * contiguous; rstd [n] fp32 (nullable) receives each row's rsqrt, which the
+ * backward needs. weight [d] in w_dtype (F32 or BF16). d <= 16384 (bf16) /
+ * 8192 (f32), a multiple of 8 (bf16) or 4 (f32) elements.
+ * ------------------------------------------------------------------------- */
+int zmoe_rmsnorm_rows(const void* X, int64_t x_stride, int64_t x_rows, const int64_t* rows, int64_t n,
+                      int64_t d, const void* weight, int w_dtype, float eps, int dtype, void* Y,
+                      float* rstd, void* stream);
+
+/* Backward of zmoe_rmsnorm_rows (the autograd of zRMSNorm.py:10-17 and of the
+ * gather): dX[rows[i]] = r (1 + w) dY[i] - X[rows[i]] r^3 / d * sum_j dY[i,j] (1 + w_j) X[rows[i],j]
+ * with r = rstd[i]; the caller zero-fills dX [x_rows, dx_stride] (rows outside
+ * the gather keep their zeros; rows must be distinct, as unpad indices are).
+ * dweight[j] = sum_i dY[i,j] X[rows[i],j] r_i in w_dtype, from fp32 partials
+ * summed in a fixed order (deterministic). Workspace:
+ * zmoe_rmsnorm_rows_backward_workspace_bytes(n, d, dtype), 16-byte aligned. */
+size_t zmoe_rmsnorm_rows_backward_workspace_bytes(int64_t n, int64_t d, int dtype);
+int zmoe_rmsnorm_rows_backward(const void* dY, const void* X, int64_t x_stride, int64_t x_rows,
+                               const int64_t* rows, int64_t n, int64_t d, const float* rstd,
+                               const void* weight, int w_dtype, int dtype, void* dX, int64_t dx_stride,
+                               void* dweight, void* workspace, size_t workspace_bytes, void* stream);
+
 /* optimizer/muon.py:6-32 (zeropower_via_newtonschulz5) on a stack of E matrices,
  * the orthogonalisation inside the MuonMD step on 3-D expert weights
  * (muon.py:399-508, called at :449). X [E, m, n] bf16, contiguous, m <= n (the

@@ -28,6 +28,11 @@ Pinning (what checks each function, all in ``tests/test_oracle.py``):
                            torch autograd of an independent dense formulation and
                            float64 central finite differences on tiny shapes.
 * ``bias_update``          closed form on a hand-built histogram.
+* ``zc_rmsnorm_rows``      closed forms: a constant row c gives sign(c)(1 + w)/sqrt(1 +
+                           eps/c^2); scale invariance at eps = 0; w = 0 gives rows of
+                           unit RMS; the gather equals normalising every row then
+                           indexing; backward against torch autograd of the reference
+                           expression and central finite differences.
 * ``newton_schulz5``       exact mode: the SVD closed form U phi^steps(S/||G||) V^T
                            with phi(s) = a s + b s^3 + c s^5; transpose symmetry;
                            bf16 mode: rounding points checked against torch's bf16
@@ -75,6 +80,8 @@ __all__ = [
     "shared_expert_forward",
     "shared_expert_backward",
     "MoELayerOracle",
+    "zc_rmsnorm_rows",
+    "zc_rmsnorm_rows_backward",
     "bias_update",
     "moe_load_metrics",
     "NS_COEFFS",
@@ -613,6 +620,37 @@ class MoELayerOracle:
             dx_dense = r(dx_dense)
         grads.update(x=r(dx_routed + dx_dense), W1=dW1, W2=dW2, d_gates=d_gates, d_logits=dz)
         return grads
+
+
+# --------------------------------------------------------------------------- #
+# (f)-2: the RMSNorm producer and the unpad gather in front of the layer
+# --------------------------------------------------------------------------- #
+def zc_rmsnorm_rows(hidden, weight, eps=1e-6, rows=None):
+    """ZeroCenteredRMSNorm (modeling/zRMSNorm.py:10-17) then index_first_axis
+    (modeling/moe_layer.py:39-42): y[i] = h * rsqrt(mean(h^2) + eps) * (1 + w) with
+    h = hidden[rows[i]] (all rows when ``rows`` is None). Float arithmetic throughout
+    (the reference's fp32, here this module's float type); the caller rounds to the
+    input dtype. Returns (y [n, d], rstd [n])."""
+    H = np.asarray(hidden, dtype=_f())
+    H = H if rows is None else H[np.asarray(rows, dtype=np.int64)]
+    r = 1.0 / np.sqrt((H * H).mean(axis=-1, keepdims=True) + eps)
+    return H * r * (1.0 + np.asarray(weight, dtype=_f())), r[:, 0]
+
+
+def zc_rmsnorm_rows_backward(dy, hidden, weight, rstd, rows=None):
+    """Autograd of ``zc_rmsnorm_rows``: (dhidden [N, d], zero outside ``rows``; dweight [d]).
+
+    With g = dy (1 + w): dh = r g - h r^3 / d * sum_j g_j h_j; dw = sum_i dy_i h_i r_i."""
+    H_all = np.asarray(hidden, dtype=_f())
+    idx = np.arange(H_all.shape[0]) if rows is None else np.asarray(rows, dtype=np.int64)
+    H = H_all[idx]
+    dy = np.asarray(dy, dtype=_f())
+    r = np.asarray(rstd, dtype=_f())[:, None]
+    g = dy * (1.0 + np.asarray(weight, dtype=_f()))
+    dh = r * g - H * r ** 3 * (g * H).sum(axis=-1, keepdims=True) / H.shape[-1]
+    dH = np.zeros_like(H_all)
+    dH[idx] = dh
+    return dH, (dy * H * r).sum(axis=0)
 
 
 # --------------------------------------------------------------------------- #

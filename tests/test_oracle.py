@@ -595,3 +595,58 @@ def test_summand_rss_brute_force():
         # gate weight grad: sum over tokens of d_logits[t]^T x[t]
         terms = np.einsum("te,td->ted", g["d_logits"], P["x"])
         np.testing.assert_allclose(g["rss"]["gate_weight"], np.sqrt((terms ** 2).sum(0)), rtol=1e-12, atol=1e-15)
+
+
+# ----------------------------------------------------------------- RMSNorm producer
+def test_rmsnorm_closed_forms():
+    r = rng(40)
+    w = r.standard_normal(16) * 0.1
+    # constant rows: y = sign(c) (1 + w) / sqrt(1 + eps / c^2)
+    for c in (3.0, -0.25, 1e-3):
+        y, rs = O.zc_rmsnorm_rows(np.full((1, 16), c), w, eps=1e-6)
+        np.testing.assert_allclose(y[0], np.sign(c) * (1 + w) / np.sqrt(1 + 1e-6 / c ** 2), rtol=1e-13)
+        np.testing.assert_allclose(rs[0], 1 / np.sqrt(c * c + 1e-6), rtol=1e-13)
+    # scale invariance at eps = 0, and w = 0 gives unit-RMS rows
+    X = r.standard_normal((5, 16))
+    y1, _ = O.zc_rmsnorm_rows(X, w, eps=0.0)
+    y2, _ = O.zc_rmsnorm_rows(X * 37.5, w, eps=0.0)
+    np.testing.assert_allclose(y1, y2, rtol=1e-13)
+    y0, _ = O.zc_rmsnorm_rows(X, np.zeros(16), eps=0.0)
+    np.testing.assert_allclose(np.sqrt((y0 ** 2).mean(axis=1)), 1.0, rtol=1e-13)
+    # the gather: normalise every row, then index
+    rows = np.array([4, 0, 2])
+    yg, rg = O.zc_rmsnorm_rows(X, w, rows=rows)
+    ya, ra = O.zc_rmsnorm_rows(X, w)
+    np.testing.assert_array_equal(yg, ya[rows])
+    np.testing.assert_array_equal(rg, ra[rows])
+
+
+def test_rmsnorm_backward_vs_torch_autograd_and_fd():
+    r = rng(41)
+    N, d = 7, 12
+    X = r.standard_normal((N, d))
+    w = r.standard_normal(d) * 0.2
+    rows = np.array([6, 1, 3, 2])
+    dy = r.standard_normal((rows.size, d))
+    y, rstd = O.zc_rmsnorm_rows(X, w, eps=1e-6, rows=rows)
+    dX, dw = O.zc_rmsnorm_rows_backward(dy, X, w, rstd, rows=rows)
+    # torch autograd of the reference expression (zRMSNorm.py:10-17), float64
+    tx = torch.tensor(X, requires_grad=True)
+    tw = torch.tensor(w, requires_grad=True)
+    h = tx[torch.tensor(rows)]
+    ty = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + tw)
+    np.testing.assert_allclose(y, ty.detach().numpy(), rtol=1e-13, atol=1e-14)
+    (ty * torch.tensor(dy)).sum().backward()
+    np.testing.assert_allclose(dX, tx.grad.numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-12, atol=1e-13)
+    assert not dX[[0, 4, 5]].any()  # rows outside the gather get no gradient
+    # central finite differences of sum(y * dy)
+    eps = 1e-6
+    for (a, q), an in (((X, (1, 5)), dX[1, 5]), ((w, (3,)), dw[3])):
+        old = a[q]
+        a[q] = old + eps
+        lp = float((O.zc_rmsnorm_rows(X, w, rows=rows)[0] * dy).sum())
+        a[q] = old - eps
+        lm = float((O.zc_rmsnorm_rows(X, w, rows=rows)[0] * dy).sum())
+        a[q] = old
+        assert abs((lp - lm) / (2 * eps) - an) < 1e-7
