@@ -1,5 +1,5 @@
 // Grouped expert GEMMs for gfx950 (scattermoe/kernels/ops.py:122-255 and
-// :263-438, plus the fused SwiGLU forward/backward of scattermoe/mlp.py:96-102),
+// :263-438, plus the fused SwiGLU forward/backward of scattermoe/mlp.py:80-86),
 // the split-K dense weight grads of the shared expert and gate, and the grouped
 // GEMMs of the Newton-Schulz step (optimizer/muon.py:6-32).
 //

@@ -1,8 +1,8 @@
 // HBM-bound row kernels of the MoE path: dispatch gather (ops.py:449-529), the
-// weighted combine (parallel_experts.py:161-163 + moe_layer.py:53), its backward
-// (parallel_experts.py:191-208), the k-reduction of the input grad
-// (parallel_experts.py:236), rowwise_sum_product (ops.py:9-80) and stand-alone
-// SwiGLU (mlp.py:101-102).
+// weighted combine (parallel_experts.py:50-52 + moe_layer.py:53), its backward
+// (parallel_experts.py:80-97), the k-reduction of the input grad
+// (parallel_experts.py:125), rowwise_sum_product (ops.py:9-80) and stand-alone
+// SwiGLU (mlp.py:86).
 //
 // Layout: a row of d elements is d/VEC 16-byte chunks (VEC = 8 bf16 or 4 f32).
 // A group of TPR threads (64, 128 or 256; a whole number of waves) owns one row

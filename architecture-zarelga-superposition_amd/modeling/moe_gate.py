@@ -15,7 +15,7 @@ import torch
 import torch.nn as nn
 
 from zmoe import functional as _zf
-from zmoe import ops as _z
+from zmoe import library as _zl
 
 
 class RouteTopK(torch.autograd.Function):
@@ -23,10 +23,10 @@ class RouteTopK(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits, expert_biases, k: int):
-        idx, w, p = _z.route_topk(logits, expert_biases, k, round_probs_bf16=logits.dtype == torch.bfloat16)
+        idx, w, p = _zl.route_topk(logits, expert_biases, k, logits.dtype == torch.bfloat16)
         ctx.save_for_backward(p, idx)
         ctx.num_experts = logits.shape[-1]
-        ctx.logits_dtype = logits.dtype
+        ctx.like = logits.new_empty(0)                    # the logits' dtype and device
         ctx.mark_non_differentiable(idx)
         return idx, w
 
@@ -35,7 +35,7 @@ class RouteTopK(torch.autograd.Function):
         if d_weight is None:
             return None, None, None
         p, idx = ctx.saved_tensors
-        d_logits = _z.route_topk_backward(d_weight, p, idx, ctx.num_experts, ctx.logits_dtype)
+        d_logits = _zl.route_topk_backward(d_weight, p, idx, ctx.num_experts, ctx.like)
         return d_logits, None, None
 
 

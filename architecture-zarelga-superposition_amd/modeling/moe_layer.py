@@ -15,7 +15,7 @@ import torch.nn.functional as F
 
 from scattermoe.mlp import GLUMLP
 from zmoe import functional as _zf
-from zmoe import ops as _z
+from zmoe import library as _zl
 
 from .expert_layer import ExpertMLP
 from .moe_gate import MoEGate
@@ -52,66 +52,62 @@ class _FusedMoELayer(torch.autograd.Function):
     adds over [T, d]).
 
     (x [T, d], gate weight, expert_biases, W1, W2, shared gate/up/down weights, k, E,
-    stash, pad_rows, pad_total) -> (out, topk_idx [T, k]); out is [T, d], or with pad_rows
-    (int64 [T]) the padded [pad_total, d] whose row pad_rows[t] is token t's.
+    pad_rows, pad_total) -> (out, topk_idx [T, k], expert_offsets [E]); out is [T, d], or
+    with pad_rows (int64 [T]) the padded [pad_total, d] whose row pad_rows[t] is token t's.
+    Every launch is a ``zmoe::`` custom op, so torch.compile traces through the function
+    without a graph break.
     """
 
     @staticmethod
-    def forward(ctx, x, gate_w, expert_biases, W1, W2, Ws_gate, Ws_up, Ws_down, k: int, E: int, stash: dict,
-                pad_rows=None, pad_total=None):
+    def forward(ctx, x, gate_w, expert_biases, W1, W2, Ws_gate, Ws_up, Ws_down, k: int, E: int, pad_rows=None,
+                pad_total: int = 0):
         logits = F.linear(x, gate_w)                                                 # moe_gate.py:26
-        idx, w, p = _z.route_topk(logits, expert_biases, k, round_probs_bf16=logits.dtype == torch.bfloat16)
+        idx, w, p = _zl.route_topk(logits, expert_biases, k, logits.dtype == torch.bfloat16)
         fs = Ws_up.shape[0]
         W3 = torch.cat([Ws_up, Ws_gate, gate_w], dim=0)     # [2fs + E, d]; rows :2fs = [up | gate]
         Hs = F.linear(x, W3[:2 * fs])
-        As = _z.swiglu(Hs)
+        As = _zl.swiglu(Hs)
         S = F.linear(As, Ws_down)                                                    # expert_layer.py:23-24
-        se, ss, off, inv = _z.flatten_sort_count(idx, E)                             # mlp.py:80-82
-        stash["expert_offsets"] = off
+        se, ss, off, inv = _zl.flatten_sort_count(idx, E)                            # mlp.py:76-77
         w_sorted = w.reshape(-1).index_select(0, ss)
-        H, A_s = _z.glu_w1_forward(x, W1, se, ss, off, k, row_scale=w_sorted)        # A_s = w * A
-        Y_s = _z.scatter2scatter(A_s, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
-                                 expert_offsets=off)                                 # = w * Y
-        out = _z.combine(Y_s, None, k, addend=S, out_rows=pad_rows, out_total=pad_total)  # moe_layer.py:48-56
-        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s)
+        H, A_s = _zl.glu_w1_forward(x, W1, se, ss, off, k, w_sorted)                 # A_s = w * A
+        Y_s = _zl.grouped_mm(A_s, W2.permute(0, 2, 1), se, ss, 1, True, False, off,
+                             "scatter2scatter")                                      # = w * Y
+        out = _zl.combine(Y_s, None, k, S, pad_rows, pad_total)                      # moe_layer.py:48-56
+        ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s, pad_rows)
         ctx.k, ctx.E, ctx.fs = k, E, fs
-        ctx.pad_rows = pad_rows
-        ctx.mark_non_differentiable(idx)
-        return out, idx
+        ctx.mark_non_differentiable(idx, off)
+        return out, idx, off
 
     @staticmethod
-    def backward(ctx, dout, d_idx):
-        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s = ctx.saved_tensors
+    def backward(ctx, dout, d_idx, d_off):
+        x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s, pad_rows = ctx.saved_tensors
         k, E, fs = ctx.k, ctx.E, ctx.fs
         need = ctx.needs_input_grad
         dout = dout.to(x.dtype).contiguous()
-        pad_rows = ctx.pad_rows
         # the grad of the combine's inputs: dout for the shared expert's output (the addend),
         # gates * dout[t] for the routed rows, <dout[t], Y> for the gates
         dS = dout if pad_rows is None else dout.index_select(0, pad_rows)
         # routed experts: dA = dout[t] W2_e as a plain grouped GEMM on dS's rows read in
         # place, then one row pass for the SwiGLU backward of w * dA and the gates' grad (no
         # pass over Y; an epilogue that reads H inside the GEMM measured slower)
-        dA = _z.scatter2scatter(dS, W2, se, ss, k, x_grouped=False, y_grouped=True, expert_offsets=off,
-                                region="glu_w2_backward_dh")
-        dH, d_gates = _z.swiglu_backward_gates(dA, H, w_sorted, ss)
+        dA = _zl.grouped_mm(dS, W2, se, ss, k, False, True, off, "glu_w2_backward_dh")
+        dH, d_gates = _zl.swiglu_backward_gates(dA, H, w_sorted, ss)
         d_gates = d_gates.view(-1, k)
-        dW2 = _z.group_bwd_w_gather_dy(dS, ss, k, A_s, off, E) if need[4] else None        # sum dout[t]^T (w A)
-        dW1 = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)[0] if need[3] else None
-        dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False, expert_offsets=off)
-        # shared expert
+        dW2 = _zl.group_bwd_w_gather_dy(dS, ss, k, A_s, off, E) if need[4] else None     # sum dout[t]^T (w A)
+        dW1 = _zl.group_bwd_w(dH, x, off, E, ss, k) if need[3] else None
+        dXe = _zl.grouped_mm(dH, W1, se, ss, 1, True, False, off, "scatter2scatter")
+        # shared expert, and the gate projection through the routing's analytic backward:
+        # [d up | d gate | d_logits] side by side, one product for both input grads
         dAs = dS @ Ws_down
-        dWs_down = _z.dense_wgrad(dS, As) if need[7] else None
-        G = torch.empty((x.shape[0], 2 * fs + E), dtype=x.dtype, device=x.device)
-        _z.swiglu_backward(dAs, Hs, out=G[:, :2 * fs])                              # [d up | d gate]
-        # gate projection, through the routing's analytic backward
-        _z.route_topk_backward(d_gates, p, idx, E, x.dtype, out=G[:, 2 * fs:])     # d_logits
+        dWs_down = _zl.dense_wgrad(dS, As) if need[7] else None
+        G = _zl.swiglu_route_backward(dAs, Hs, d_gates, p, idx, E)
         dx_dense = G @ W3                                   # shared expert + gate input grads
-        dW3 = _z.dense_wgrad(G, x) if need[1] or need[5] or need[6] else None
-        dx = _z.sum_k(dXe, k, add0=dx_dense)
+        dW3 = _zl.dense_wgrad(G, x) if need[1] or need[5] or need[6] else None
+        dx = _zl.sum_k(dXe, k, dx_dense)
         part = (lambda a, b: None) if dW3 is None else (lambda a, b: dW3[a:b])
         return (dx, part(2 * fs, 2 * fs + E), None, dW1, dW2, part(fs, 2 * fs), part(0, fs), dWs_down,
-                None, None, None, None, None)
+                None, None, None, None)
 
 
 class MoELayer(nn.Module):
@@ -177,15 +173,14 @@ class MoELayer(nn.Module):
         ws = self._fused_weights(hidden_states if normed is None else normed.view(1, -1, h))
         if ws is not None:
             flat = hidden_states.reshape(bsz * seq_len, h)
-            stash = {}
-            pad = () if unpad_indices is None else (unpad_indices, bsz * seq_len)
+            pad = (None, 0) if unpad_indices is None else (unpad_indices, bsz * seq_len)
             if normed is not None:
                 x = normed.reshape(-1, h)
             else:
                 x = flat if unpad_indices is None else index_first_axis(flat, unpad_indices)
-            out, topk_idx = _FusedMoELayer.apply(x, ws[0], self.gate.expert_biases, *ws[1:], self.gate.top_k,
-                                                 self.routed_experts.num_experts, stash, *pad)
-            self.routed_experts.last_expert_offsets = stash["expert_offsets"]
+            out, topk_idx, offsets = _FusedMoELayer.apply(x, ws[0], self.gate.expert_biases, *ws[1:],
+                                                          self.gate.top_k, self.routed_experts.num_experts, *pad)
+            self.routed_experts.last_expert_offsets = offsets
             if unpad_indices is None:
                 return out.view(bsz, seq_len, h), topk_idx.view(bsz, seq_len, -1)
             return out.view(bsz, seq_len, h), pad_input(topk_idx, unpad_indices, bsz, seq_len)

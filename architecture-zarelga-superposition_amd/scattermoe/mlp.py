@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from zmoe import ops as _z
+from zmoe import library as _zl
 
 from .parallel_experts import ParallelExperts, flatten_sort_count
 
@@ -29,50 +29,46 @@ def _compute_dtype(x: torch.Tensor) -> torch.dtype:
 
 
 class GLUExpertsFunction(torch.autograd.Function):
-    """y = sum_j gates[:, j] * W2[e_j] silu(W1g[e_j] x) * (W1h[e_j] x) for every token."""
+    """y = sum_j gates[:, j] * W2[e_j] silu(W1g[e_j] x) * (W1h[e_j] x) for every token.
+
+    (x, gates, expert_idxs, W1, W2, k, num_experts, residual=None, pad_rows=None,
+    pad_total=0) -> (y, expert_offsets). ``residual`` [T, d] is added in the combine pass
+    (moe_layer.py:53 adds the shared expert's output); with ``pad_rows`` the output is the
+    padded [pad_total, d] (moe_layer.py:55-56). ``expert_offsets`` is the sort's (not
+    differentiable). Every launch is a ``zmoe::`` custom op, so torch.compile traces
+    through this function without a graph break.
+    """
 
     @staticmethod
-    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int, *extra):
-        # extra: (residual [T, d] or None, stash dict or None, pad_rows [T] or None, pad_total):
-        # residual is added in the combine pass; stash["expert_offsets"] receives the sort's
-        # offsets; with pad_rows the output is the padded [pad_total, d] (moe_layer.py:55-56)
-        residual = extra[0] if len(extra) > 0 else None
-        stash = extra[1] if len(extra) > 1 else None
-        pad_rows = extra[2] if len(extra) > 2 else None
-        pad_total = extra[3] if len(extra) > 3 else None
-        se, ss, off, inv = _z.flatten_sort_count(expert_idxs, num_experts)
-        if stash is not None:
-            stash["expert_offsets"] = off
-        H, A = _z.glu_w1_forward(x, W1, se, ss, off, k)                       # mlp.py:96-102
-        Y = _z.scatter2scatter(A, W2.permute(0, 2, 1), se, ss, 1, x_grouped=True, y_grouped=False,
-                               expert_offsets=off)                             # mlp.py:103-108
-        # + residual in the same pass (moe_layer.py:53 adds the shared expert's output)
-        out = _z.combine(Y, gates, k, addend=residual, out_rows=pad_rows, out_total=pad_total)  # :161-163
+    def forward(ctx, x, gates, expert_idxs, W1, W2, k: int, num_experts: int, residual=None, pad_rows=None,
+                pad_total: int = 0):
+        se, ss, off, inv = _zl.flatten_sort_count(expert_idxs, num_experts)
+        H, A = _zl.glu_w1_forward(x, W1, se, ss, off, k, None)                   # mlp.py:80-86
+        Y = _zl.grouped_mm(A, W2.permute(0, 2, 1), se, ss, 1, True, False, off,
+                           "scatter2scatter")                                    # mlp.py:87-93
+        out = _zl.combine(Y, gates, k, residual, pad_rows, pad_total)            # parallel_experts.py:50-52
         ctx.has_residual = residual is not None
-        ctx.n_extra = len(extra)
-        ctx.pad_rows = pad_rows
-        ctx.save_for_backward(x, gates, W1, W2, se, ss, off, inv, H, A, Y)
+        ctx.save_for_backward(x, gates, W1, W2, se, ss, off, inv, H, A, Y, pad_rows)
         ctx.k = k
         ctx.num_experts = num_experts
-        return out
+        ctx.mark_non_differentiable(off)
+        return out, off
 
     @staticmethod
-    def backward(ctx, dout):
-        x, gates, W1, W2, se, ss, off, inv, H, A, Y = ctx.saved_tensors
+    def backward(ctx, dout, d_off):
+        x, gates, W1, W2, se, ss, off, inv, H, A, Y, pad_rows = ctx.saved_tensors
         k, E = ctx.k, ctx.num_experts
         dout = dout.to(x.dtype)
-        d_gates, dYg = _z.combine_backward(Y, dout, gates, inv, grad_rows=ctx.pad_rows)  # :191-208
-        dH = _z.glu_w2_backward_dh(dYg, W2, H, se, off)                        # :223-231 + silu*mul backward
-        dW2, _ = _z.group_bwd_w(dYg, A, off, E)                                # :216-221 (W2)
-        dW1, _ = _z.group_bwd_w(dH, x, off, E, x_gather=ss, x_div=k)          # :213-221 (W1, x gathered)
-        dXe = _z.scatter2scatter(dH, W1, se, ss, 1, x_grouped=True, y_grouped=False,
-                                 expert_offsets=off)                           # :223-231 (W1)
-        dx = _z.sum_k(dXe, k)                                                  # :236
-        grads = (dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None)
-        extra = [None] * ctx.n_extra  # one grad per extra input (residual, stash, pad_rows, pad_total)
+        d_gates, dYg = _zl.combine_backward(Y, dout, gates, inv, pad_rows)  # parallel_experts.py:80-97
+        dH = _zl.glu_w2_backward_dh(dYg, W2, H, se, off)                        # :112-120 + silu*mul backward
+        dW2 = _zl.group_bwd_w(dYg, A, off, E, None, 1)                           # :98-110 (W2)
+        dW1 = _zl.group_bwd_w(dH, x, off, E, ss, k)                              # :98-110 (W1, x gathered)
+        dXe = _zl.grouped_mm(dH, W1, se, ss, 1, True, False, off, "scatter2scatter")  # :112-120 (W1)
+        dx = _zl.sum_k(dXe, k, None)                                             # :125
+        d_res = None
         if ctx.has_residual and ctx.needs_input_grad[7]:
-            extra[0] = dout if ctx.pad_rows is None else dout.index_select(0, ctx.pad_rows)
-        return grads + tuple(extra)
+            d_res = dout if pad_rows is None else dout.index_select(0, pad_rows)
+        return dx, d_gates.to(gates.dtype), None, dW1, dW2, None, None, d_res, None, None
 
 
 class MLP(nn.Module):
@@ -135,13 +131,10 @@ class GLUMLP(nn.Module):
         if self.fused:
             dtype = _compute_dtype(x)
             res = None if residual is None else residual.reshape(-1, residual.shape[-1]).to(dtype)
-            stash = {}
-            args = (res, stash) if pad is None else (res, stash, pad[0], int(pad[1]))
-            y = GLUExpertsFunction.apply(x.to(dtype), expert_p, expert_idxs,
-                                         self.experts.compute_weight(dtype),
-                                         self.output_experts.compute_weight(dtype), self.top_k, self.num_experts,
-                                         *args)
-            self.last_expert_offsets = stash["expert_offsets"]
+            rows, total = (None, 0) if pad is None else (pad[0], int(pad[1]))
+            y, self.last_expert_offsets = GLUExpertsFunction.apply(
+                x.to(dtype), expert_p, expert_idxs, self.experts.compute_weight(dtype),
+                self.output_experts.compute_weight(dtype), self.top_k, self.num_experts, res, rows, total)
             return y if pad is not None else y.view(*x_shape[:-1], y.size(-1))
         sorted_expert_idxs, sorted_scattered_idxs, expert_offsets = flatten_sort_count(
             expert_idxs, num_experts=self.num_experts)

@@ -9,6 +9,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
+from zmoe import library as _zl
 from zmoe import ops as _z
 
 from . import kernels
@@ -31,15 +32,13 @@ def flatten_sort_count(expert_idxs: torch.Tensor, num_experts: int):
     Returns (sorted_expert_idxs, sorted_scattered_idxs, expert_offsets); equal
     experts keep flat-slot order, offsets are inclusive ends.
     """
-    with torch.no_grad():
-        se, ss, off, _ = _z.flatten_sort_count(expert_idxs, num_experts)
+    se, ss, off, _ = _zl.flatten_sort_count(expert_idxs, num_experts)
     return se, ss, off
 
 
 def flatten_sort_count_with_inverse(expert_idxs: torch.Tensor, num_experts: int):
     """flatten_sort_count plus inverse[slot] = sorted position (int32)."""
-    with torch.no_grad():
-        return _z.flatten_sort_count(expert_idxs, num_experts)
+    return tuple(_zl.flatten_sort_count(expert_idxs, num_experts))
 
 
 class ParallelLinear(torch.autograd.Function):
@@ -56,7 +55,7 @@ class ParallelLinear(torch.autograd.Function):
             expert_offsets=expert_offsets)
         if gates is not None:
             output_expanded = output.view(gates.size(0), gates.size(1), output.size(-1))
-            output = _z.combine(output_expanded, gates, gates.size(1))
+            output = _zl.combine(output, gates, gates.size(1), None, None, 0)
         else:
             output_expanded = None
         ctx.save_for_backward(x, expert_weights, expert_biases, sorted_expert_idxs, sorted_scattered_idxs,
@@ -88,9 +87,13 @@ class ParallelLinear(torch.autograd.Function):
             grouped_grad_out = kernels.ops.group(grad_out, sorted_scattered_idxs, fan_out=gate_fan,
                                                  coeff=gates_flat, out=grouped_grad_out)
         # dW: the x gather happens inside the wgrad kernel (no grouped copy of x).
-        DWt, d_biases = _z.group_bwd_w(grouped_grad_out, x, expert_offsets, expert_weights.size(0),
-                                       has_bias=expert_biases is not None,
-                                       x_gather=None if grouped_in else sorted_scattered_idxs, x_div=k)
+        x_gather = None if grouped_in else sorted_scattered_idxs
+        if expert_biases is None:
+            DWt = _zl.group_bwd_w(grouped_grad_out, x, expert_offsets, expert_weights.size(0), x_gather, k)
+            d_biases = None
+        else:
+            DWt, d_biases = _zl.group_bwd_w_bias(grouped_grad_out, x, expert_offsets, expert_weights.size(0),
+                                                 x_gather, k)
         d_weights = DWt.permute(0, 2, 1)
         d_expanded_input = kernels.ops.scatter2scatter(
             X=grouped_grad_out, x_grouped=True, W=expert_weights.permute(0, 2, 1),
@@ -99,7 +102,7 @@ class ParallelLinear(torch.autograd.Function):
         if k == 1:
             d_input = d_expanded_input
         else:
-            d_input = _z.sum_k(d_expanded_input, k)
+            d_input = _zl.sum_k(d_expanded_input, k, None)
         return (d_input, d_weights, None, None, None, None, d_biases, d_gates, None, None)
 
 

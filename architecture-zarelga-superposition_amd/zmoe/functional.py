@@ -20,7 +20,7 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
-from . import ops
+from . import library as zl
 
 
 def _fused(*ts) -> bool:
@@ -40,7 +40,7 @@ class _Linear(torch.autograd.Function):
         x2, W = ctx.saved_tensors
         dy = dy.contiguous()
         dx = dy @ W if ctx.needs_input_grad[0] else None
-        dW = ops.dense_wgrad(dy, x2) if ctx.needs_input_grad[1] else None
+        dW = zl.dense_wgrad(dy, x2) if ctx.needs_input_grad[1] else None
         return dx, dW
 
 
@@ -61,7 +61,7 @@ class _SwiGLUMLP(torch.autograd.Function):
         f = W_up.shape[0]
         W_cat = torch.cat([W_up, W_gate], dim=0)     # [2f, d]: H = [up | gate], the GLU layout
         H = F.linear(x2, W_cat)
-        A = ops.swiglu(H)                             # silu(gate) * up, one rounding
+        A = zl.swiglu(H)                              # silu(gate) * up, one rounding
         y = F.linear(A, W_down)
         ctx.save_for_backward(x2, W_cat, W_down, H, A)
         ctx.f = f
@@ -73,10 +73,10 @@ class _SwiGLUMLP(torch.autograd.Function):
         f = ctx.f
         dy = dy.contiguous()
         dA = dy @ W_down                              # [M, f]
-        dW_down = ops.dense_wgrad(dy, A)              # [d, f]
-        dH = ops.swiglu_backward(dA, H)               # [M, 2f] = [d up | d gate]
+        dW_down = zl.dense_wgrad(dy, A)               # [d, f]
+        dH = zl.swiglu_backward(dA, H)                # [M, 2f] = [d up | d gate]
         dx = dH @ W_cat
-        dW_cat = ops.dense_wgrad(dH, x2)              # [2f, d]
+        dW_cat = zl.dense_wgrad(dH, x2)               # [2f, d]
         return dx, dW_cat[f:], dW_cat[:f], dW_down
 
 
@@ -93,7 +93,7 @@ class _RMSNormRows(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden2, weight, eps: float, rows):
-        y, rstd = ops.rmsnorm_rows(hidden2, weight, eps, rows)
+        y, rstd = zl.rmsnorm_rows(hidden2, weight, eps, rows)
         ctx.save_for_backward(hidden2, weight, rstd, rows if rows is not None else torch.empty(0))
         ctx.has_rows = rows is not None
         return y
@@ -101,7 +101,7 @@ class _RMSNormRows(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         hidden2, weight, rstd, rows = ctx.saved_tensors
-        dx, dw = ops.rmsnorm_rows_backward(dy.contiguous(), hidden2, rows if ctx.has_rows else None, rstd, weight)
+        dx, dw = zl.rmsnorm_rows_backward(dy.contiguous(), hidden2, rows if ctx.has_rows else None, rstd, weight)
         return dx, dw, None, None
 
 

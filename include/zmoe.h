@@ -204,7 +204,7 @@ int zmoe_rowwise_sum_product(const void* A, int a_dtype, const void* B, int b_dt
  * Fused GLU-expert pieces. Each replaces a sequence of reference calls.
  * ------------------------------------------------------------------------- */
 
-/* scattermoe/mlp.py:96-102 — W1 scatter2scatter (grouped_out=True) fused with
+/* scattermoe/mlp.py:80-86 — W1 scatter2scatter (grouped_out=True) fused with
  * chunk(2) and silu(gates) * h:
  *   H[i, :] = X[sorted_scattered_idxs[i] / k] @ W1[e]^T   ([R, 2f], sorted rows)
  *   A[i, j] = silu(H[i, f + j]) * H[i, j]                 ([R, f])
@@ -220,7 +220,7 @@ int zmoe_glu_w1_forward(const void* X, int64_t x_stride_m, const void* W1,
  *   A[i, j] = row_scale[i] * silu(H[i, f + j]) * H[i, j]   (one rounding)
  * row_scale [R] f32 in sorted order (gates[sorted_scattered_idxs[i]]). The W2
  * product of these rows is then already gate-weighted, so the combine sums the k
- * rows of a token with unit weights (parallel_experts.py:161-163 reassociated). */
+ * rows of a token with unit weights (parallel_experts.py:50-52 reassociated). */
 int zmoe_glu_w1_forward_scaled(const void* X, int64_t x_stride_m, const void* W1,
                                const int64_t* sorted_expert_idxs,
                                const int64_t* sorted_scattered_idxs,
@@ -229,7 +229,7 @@ int zmoe_glu_w1_forward_scaled(const void* X, int64_t x_stride_m, const void* W1
                                void* H, void* A, void* stream);
 
 /* scattermoe/parallel_experts.py:112-120 (W2 input grad, x_grouped and
- * y_grouped) fused with the backward of silu(gates) * h (mlp.py:102):
+ * y_grouped) fused with the backward of silu(gates) * h (mlp.py:86):
  *   dA[i, :] = dYg[i, :] @ W2[e]                 (W2 [E, d, f] contiguous)
  *   dH[i, j]     = dA[i, j] * silu(g)             (g = H[i, f + j], h = H[i, j])
  *   dH[i, f + j] = dA[i, j] * h * s * (1 + g (1 - s)),  s = sigmoid(g)        */
@@ -256,7 +256,7 @@ int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k, const void
                                   float* d_gates, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
-/* scattermoe/parallel_experts.py:161-163 (gates @ output_expanded) plus the
+/* scattermoe/parallel_experts.py:50-52 (gates @ output_expanded) plus the
  * residual sum of modeling/moe_layer.py:53:
  *   out[t, :] = addend[t, :] + sum_j gates[t, j] * Y[t * k + j, :]
  * Y [T*k, d] in slot order; addend may be NULL; gates may be NULL (all 1: rows
@@ -264,7 +264,7 @@ int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k, const void
 int zmoe_combine(const void* Y, const float* gates, const void* addend, int64_t T,
                  int k, int64_t d, int dtype, void* out, void* stream);
 
-/* scattermoe/parallel_experts.py:191-208 (rowwise_sum_product + group with
+/* scattermoe/parallel_experts.py:80-97 (rowwise_sum_product + group with
  * coeff=gates) in one pass over grad_out:
  *   d_gates[t, j] = sum_h Y[t*k+j, h] * grad_out[t, h]
  *   grouped_grad_out[inverse[t*k+j], :] = gates[t, j] * grad_out[t, :]
@@ -288,13 +288,13 @@ int zmoe_combine_backward_rows(const void* Y, const void* grad_out, const int64_
                                int64_t T, int k, int64_t d, int dtype, float* d_gates,
                                void* grouped_grad_out, void* stream);
 
-/* scattermoe/parallel_experts.py:236 (d_expanded_input.view(T,k,d).sum(-2))
+/* scattermoe/parallel_experts.py:125 (d_expanded_input.view(T,k,d).sum(-2))
  * plus up to two addends (gate and shared-expert input grads):
  *   out[t, :] = sum_j Xe[t*k + j, :] + add0[t, :] + add1[t, :]               */
 int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype,
                const void* add0, const void* add1, void* out, void* stream);
 
-/* scattermoe/mlp.py:101-102 stand-alone (shapes the fused kernels reject):
+/* scattermoe/mlp.py:86 stand-alone (shapes the fused kernels reject):
  * A = silu(H[:, f:]) * H[:, :f]; and its backward dH from (dA, H), rows of dH
  * ld_dh >= 2f elements apart (2f for a packed [R, 2f]). */
 int zmoe_swiglu(const void* H, int64_t R, int64_t f, int dtype, void* A, void* stream);
@@ -302,7 +302,7 @@ int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f,
                          int dtype, void* dH, int64_t ld_dh, void* stream);
 
 /* The SwiGLU backward of gate-scaled rows with the gates' grad (the combine backward
- * of parallel_experts.py:191-208 reassociated, as in zmoe_glu_w2_backward_dh_gates,
+ * of parallel_experts.py:80-97 reassociated, as in zmoe_glu_w2_backward_dh_gates,
  * after a plain dA GEMM on the output grad's rows), per sorted row r:
  *   dH[r] = swiglu_backward(row_scale[r] * dA[r], H[r])
  *   d_gates[slot_of_row[r]] = sum_j dA[r, j] * silu(H[r, f + j]) * H[r, j]

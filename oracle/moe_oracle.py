@@ -399,8 +399,8 @@ def glu_mlp_forward(x, expert_p, expert_idxs, W1, W2, store=None, gate_scale_on=
     x [T, d]; expert_p, expert_idxs [T, k]; W1 [E, 2f, d] and W2 [E, d, f] in
     ``nn.Parameter`` storage (the reference permutes them to [E, in, out]).
 
-    ``store`` rounds at the stored tensors (see ``storage_rounder``): H (:79-84), the
-    activation A (:85-87), the per-slot W2 outputs Y (:88-93) and the combined output.
+    ``store`` rounds at the stored tensors (see ``storage_rounder``): H (:80-85), the
+    activation A (:86), the per-slot W2 outputs Y (:87-93) and the combined output.
     ``gate_scale_on`` says where the routing weights multiply: ``"Y"`` on the W2 outputs
     as the reference does (parallel_experts.py:50-52), ``"A"`` on the activations before
     the W2 product (w (A W2) = (w A) W2, equal in exact arithmetic; the rounding points
@@ -412,19 +412,19 @@ def glu_mlp_forward(x, expert_p, expert_idxs, W1, W2, store=None, gate_scale_on=
     x = np.asarray(x, dtype=_f())
     T, k = np.asarray(expert_idxs).shape
     E = np.asarray(W1).shape[0]
-    se, ss, off = flatten_sort_count(expert_idxs, E)                          # :77-78
+    se, ss, off = flatten_sort_count(expert_idxs, E)                          # :76-77
     W1l = np.transpose(np.asarray(W1, dtype=_f()), (0, 2, 1))
     W2l = np.transpose(np.asarray(W2, dtype=_f()), (0, 2, 1))
     gates = np.asarray(expert_p, dtype=_f())
     w_sorted = gates.reshape(-1)[ss]
-    H = r(scatter2scatter(x, W1l, se, ss, k, y_grouped=True))                 # :79-84
+    H = r(scatter2scatter(x, W1l, se, ss, k, y_grouped=True))                 # :80-85
     if gate_scale_on == "Y":
-        A = r(swiglu(H))                                                      # :85-87
+        A = r(swiglu(H))                                                      # :86
     elif gate_scale_on == "A":
         A = r(w_sorted[:, None] * swiglu(H))
     else:
         raise ValueError("gate_scale_on must be 'Y' or 'A'")
-    Y = r(scatter2scatter(A, W2l, se, ss, 1, x_grouped=True, y_grouped=False))  # :88-93, slot order
+    Y = r(scatter2scatter(A, W2l, se, ss, 1, x_grouped=True, y_grouped=False))  # :87-93, slot order
     Y3 = Y.reshape(T, k, -1)
     y = np.einsum("tj,tjn->tn", gates, Y3) if gate_scale_on == "Y" else Y3.sum(axis=1)  # parallel_experts.py:50-52
     if residual is not None:

@@ -109,10 +109,10 @@ class TorchGLURef:
                 self.H.append(None)
                 self.A.append(None)
                 continue
-            H = r(x64[tok] @ self.W1[e].to(F64).T)                              # mlp.py:79-84
+            H = r(x64[tok] @ self.W1[e].to(F64).T)                              # mlp.py:80-85
             we = w64[tok, slot][:, None]
-            A = r(_swiglu(H)) if self.gate_scale_on == "Y" else r(we * _swiglu(H))   # mlp.py:85-87
-            Y = r(A @ self.W2[e].to(F64).T)                                     # mlp.py:88-93
+            A = r(_swiglu(H)) if self.gate_scale_on == "Y" else r(we * _swiglu(H))   # mlp.py:86
+            Y = r(A @ self.W2[e].to(F64).T)                                     # mlp.py:87-93
             acc.index_add_(0, tok, we * Y if self.gate_scale_on == "Y" else Y)  # parallel_experts.py:50-52
             self.H.append(H)
             self.A.append(A)

@@ -86,7 +86,7 @@ def test_c2_forward_full(hip_device):
     idx, w = route_and_check(x, Wg, bias, k)
     sort_invariants(idx, E)
     with torch.no_grad():
-        y = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
+        y, _ = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
     ref, args = glu_reference(x, W1, W2, idx, w)
     close_t(y, ref.forward(*args), "C2 output")
 
@@ -109,7 +109,7 @@ def test_c4_skewed_forward_backward(hip_device):
     wg = w.clone().requires_grad_(True)
     W1g = W1.clone().requires_grad_(True)
     W2g = W2.clone().requires_grad_(True)
-    y = GLUExpertsFunction.apply(xg, wg, idx, W1g, W2g, k, E)
+    y, _ = GLUExpertsFunction.apply(xg, wg, idx, W1g, W2g, k, E)
     dout = torch.randn(T, d, device=hip_device, generator=g).to(torch.bfloat16)
     y.backward(dout)
 
@@ -138,7 +138,7 @@ def test_c5_small_batch_forward(hip_device, T):
     idx, w = route_and_check(x, Wg, bias, k)
     sort_invariants(idx, E)
     with torch.no_grad():
-        y = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
+        y, _ = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
     ref, args = glu_reference(x, W1, W2, idx, w)
     close_t(y, ref.forward(*args), f"C5 T={T} output")
 

@@ -235,8 +235,8 @@ def test_c3_full_size_properties(hip_device):
     assert torch.equal(torch.sort(ss).values, torch.arange(T * k, device=hip_device))
     assert torch.equal(se, idx.view(-1)[ss])
     assert bool((se[1:] >= se[:-1]).all())
-    y1 = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
-    y2 = GLUExpertsFunction.apply(x, w * 2, idx, W1, W2, k, E)
+    y1, _ = GLUExpertsFunction.apply(x, w, idx, W1, W2, k, E)
+    y2, _ = GLUExpertsFunction.apply(x, w * 2, idx, W1, W2, k, E)
     assert torch.equal(y2.float(), (y1.float() * 2))
     # sampled tokens vs the oracle (each token depends only on its own row)
     rows = torch.randperm(T, generator=gen(2))[:48].to(hip_device)
