@@ -13,30 +13,57 @@ namespace zmoe {
 
 constexpr int kRouteMaxPerLane = 16;  // E <= 1024
 
-// Sort key of a routing candidate; a larger key takes an earlier slot. The high word is
-// a monotone image of the biased score (every NaN canonicalised above +inf, -0 folded
-// into +0), the low word the inverted expert id, so equal scores go to the lower expert.
-__device__ __forceinline__ uint64_t route_key(float s, int e) {
+// Sort key of a routing candidate's score; a larger key takes an earlier slot. A monotone
+// image of the biased score: every NaN canonicalised above +inf, -0 folded into +0. Equal
+// scores go to the lower expert. Key 0 marks a taken (or padding) candidate: a real
+// score's key is at least 0x007fffff (that of -inf).
+__device__ __forceinline__ uint32_t score_key(float s) {
   uint32_t b = __float_as_uint(s);
   if (s != s) b = 0x7fffffffu;
   else if (s == 0.f) b = 0u;
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((uint64_t)b << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
-}
-// key 0 is below every candidate's key (the high word of a real key is at least 0x007fffff)
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
-  return ((uint64_t)hi << 32) | lo;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
 // sigmoid evaluated in double, rounded once to float
 __device__ __forceinline__ float sigmoid_f64(float z) { return (float)(1.0 / (1.0 + exp(-(double)z))); }
 
-// One wave per token; lane l holds experts l + 64 q (q < PL). The score is the sigmoid
-// evaluated in double and rounded once to float (then to bf16 when the gate ran in
-// bf16, as autocast stores it); k rounds of a wave-wide max over route_key pick the
-// slots in contract order.
+// bf16(sigmoid_f64(z)) (the probability a bf16 gate stores) from fp32 arithmetic where that
+// is provably the same value: the fp32 estimate is within a few fp32 ulps of the true
+// sigmoid (expf, one add, one divide), and so is sigmoid_f64's fp32 rounding, so both round
+// to the same bf16 unless they lie within 16 fp32 ulps of a bf16 rounding midpoint (low 16
+// bits near 0x8000). Those lanes (about 1 score in 2000), saturated arguments (|z| >= 80,
+// where expf overflows) and NaN take the double evaluation.
+__device__ __forceinline__ float sigmoid_bf16(float z) {
+  if (fabsf(z) < 80.f) {  // false for NaN
+    const float s = 1.0f / (1.0f + expf(-z));
+    const uint32_t low = __float_as_uint(s) & 0xffffu;
+    const uint32_t dist = low > 0x8000u ? low - 0x8000u : 0x8000u - low;
+    if (dist > 16u) return to_f32(bf16_bits(s));
+  }
+  return to_f32(bf16_bits(sigmoid_f64(z)));
+}
+
+// Wave-wide max of a 32-bit key, the same value in every lane: DPP within rows of 16
+// (xor 1, xor 2, half mirror, mirror: no LDS round trip), then the four row maxima
+// through readlane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// Waves stride over tokens (each wave one token at a time, the next row's logits loaded
+// before the current one is ranked); lane l holds experts l + 64 q (q < PL). The score is
+// the sigmoid evaluated in double and rounded once to float (then to bf16 when the gate
+// ran in bf16, as autocast stores it). k rounds each take the wave max of the score keys
+// and the lowest expert holding it (ballots in expert order), so slots come in contract
+// order: score desc, expert asc, NaN first.
 template <int PL, typename LT>
 __global__ __launch_bounds__(256) void route_topk_kernel(const LT* __restrict__ logits, int64_t T, int E,
                                                          int k, const float* __restrict__ bias,
@@ -44,59 +71,173 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const LT* __restrict__ 
                                                          float* __restrict__ out_w,
                                                          float* __restrict__ out_p) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const LT* row = logits + t * (int64_t)E;
-
-  float p[PL];
-  uint64_t key[PL];
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  float bq[PL];
+  LT nxt[PL];
 #pragma unroll
   for (int q = 0; q < PL; ++q) {
     const int e = lane + 64 * q;
-    p[q] = 0.f;
-    key[q] = 0;  // padding never wins
-    if (e < E) {
-      const float z = to_f32(row[e]);
-      float pv = sigmoid_f64(z);
-      if (round_bf16) pv = to_f32(bf16_bits(pv));
-      p[q] = pv;
-      key[q] = route_key(pv + bias[e], e);
+    bq[q] = e < E ? bias[e] : 0.f;
+    nxt[q] = LT{};
+    if (t < T && e < E) nxt[q] = logits[t * (int64_t)E + e];
+  }
+  for (; t < T; t += nwaves) {
+    LT cur[PL];
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      const int e = lane + 64 * q;
+      cur[q] = nxt[q];
+      if (t + nwaves < T && e < E) nxt[q] = logits[(t + nwaves) * (int64_t)E + e];
+    }
+    float p[PL];
+    uint32_t key[PL];
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      const int e = lane + 64 * q;
+      p[q] = 0.f;
+      key[q] = 0;  // padding never wins
+      if (e < E) {
+        const float pv = round_bf16 ? sigmoid_bf16(to_f32(cur[q])) : sigmoid_f64(to_f32(cur[q]));
+        p[q] = pv;
+        key[q] = score_key(pv + bq[q]);
+      }
+    }
+    int my_e = 0;  // slot owned by this lane (lane j keeps slot j)
+    float my_p = 0.f;
+    for (int j = 0; j < k; ++j) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int q = 1; q < PL; ++q) m = max(m, key[q]);
+      m = wave_max_u32(m);
+      // the lowest expert whose key is the max: experts l + 64 q, checked in q order
+      int be = -1;
+#pragma unroll
+      for (int q = 0; q < PL; ++q) {
+        const uint64_t hit = __ballot(key[q] == m);
+        if (be < 0 && hit) be = 64 * q + __builtin_ctzll(hit);
+      }
+      const int owner = be & 63, oq = be >> 6;  // uniform across the wave
+      float pw = p[0];
+#pragma unroll
+      for (int q = 1; q < PL; ++q) pw = q == oq ? p[q] : pw;
+      pw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pw), owner));
+      if (lane == owner) {
+#pragma unroll
+        for (int q = 0; q < PL; ++q) key[q] = q == oq ? 0u : key[q];
+      }
+      if (lane == j) {
+        my_e = be;
+        my_p = pw;
+      }
+    }
+    const float sum = wave_sum(lane < k ? fabsf(my_p) : 0.f);
+    const float denom = sum < 1e-12f ? 1e-12f : sum;  // NaN propagates
+    if (lane < k) {
+      out_idx[t * k + lane] = my_e;
+      out_w[t * k + lane] = my_p / denom;
+      if (out_p) out_p[t * k + lane] = my_p;
     }
   }
+}
 
-  int my_e = 0;  // slot owned by this lane (lane j keeps slot j)
-  float my_p = 0.f;
-  for (int j = 0; j < k; ++j) {
-    uint64_t best = key[0];
-#pragma unroll
-    for (int q = 1; q < PL; ++q) best = key[q] > best ? key[q] : best;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint64_t other = shfl_xor_u64(best, o);
-      best = other > best ? other : best;
-    }
-    const int be = (int)(0xffffffffu - (uint32_t)best);  // uniform across the wave
-    const int owner = be & 63, oq = be >> 6;
-    float pw = p[0];
-#pragma unroll
-    for (int q = 1; q < PL; ++q) pw = q == oq ? p[q] : pw;
-    pw = __shfl(pw, owner, 64);
-    if (lane == owner) {
-#pragma unroll
-      for (int q = 0; q < PL; ++q) key[q] = q == oq ? 0 : key[q];
-    }
-    if (lane == j) {
-      my_e = be;
-      my_p = pw;
-    }
-  }
+// Row (16-lane) reductions by DPP; every lane of a row ends with the row's result.
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true));
+  return v;
+}
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0xB1, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x4E, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x141, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x140, 0xF, 0xF, false));
+  return v;
+}
+__device__ __forceinline__ float row_sum_f32(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));
+  return v;
+}
 
-  const float sum = wave_sum(lane < k ? fabsf(my_p) : 0.f);
-  const float denom = sum < 1e-12f ? 1e-12f : sum;  // NaN propagates
-  if (lane < k) {
-    out_idx[t * k + lane] = my_e;
-    out_w[t * k + lane] = my_p / denom;
-    if (out_p) out_p[t * k + lane] = my_p;
+// bf16 logits, E % 8 == 0, E <= 16 * VPL, k <= 16: four tokens per wave, one per 16-lane
+// row. Lane r of a row holds experts VPL r .. VPL r + VPL - 1 (16-byte loads of the
+// contiguous logits row). Each round takes the row max of the score keys and the lowest
+// expert holding it (a row min over expert ids), both by DPP within the row; the taken
+// candidate's key is cleared in its lane. The selected probabilities are read back from
+// LDS once at the end. Same contract and values as route_topk_kernel.
+template <int VPL>
+__global__ __launch_bounds__(256) void route_topk_rows_kernel(const uint16_t* __restrict__ logits, int64_t T,
+                                                              int E, int k, const float* __restrict__ bias,
+                                                              int round_bf16, int64_t* __restrict__ out_idx,
+                                                              float* __restrict__ out_w,
+                                                              float* __restrict__ out_p) {
+  __shared__ float ps[4][4][16 * VPL];  // [wave][row][expert]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = lane >> 4, r = lane & 15;
+  const int e0 = r * VPL;
+  const bool has = e0 < E;  // E % 8 == 0: each 8-expert chunk of a lane is wholly in [0, E) or out
+  float bq[VPL];
+#pragma unroll
+  for (int q = 0; q < VPL; ++q) bq[q] = e0 + q < E ? bias[e0 + q] : 0.f;
+  const int64_t groups = (T + 3) / 4;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t g = (int64_t)blockIdx.x * 4 + wave; g < groups; g += nwaves) {
+    const int64_t t = g * 4 + row;
+    const bool live = t < T && has;
+    uint4 raw[VPL / 8];
+#pragma unroll
+    for (int c = 0; c < VPL / 8; ++c)
+      raw[c] = live && e0 + 8 * c < E ? *reinterpret_cast<const uint4*>(logits + t * (int64_t)E + e0 + 8 * c)
+                                      : make_uint4(0, 0, 0, 0);
+    float p[VPL];
+    uint32_t key[VPL];
+#pragma unroll
+    for (int c = 0; c < VPL / 8; ++c) {
+      float z[8];
+      unpack_chunk(raw[c], z, uint16_t{});
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int q = 8 * c + u;
+        const float pv = round_bf16 ? sigmoid_bf16(z[u]) : sigmoid_f64(z[u]);
+        p[q] = pv;
+        key[q] = live && e0 + q < E ? score_key(pv + bq[q]) : 0u;
+      }
+    }
+    if (has) {
+#pragma unroll
+      for (int q = 0; q < VPL; q += 4)
+        *reinterpret_cast<float4*>(&ps[wave][row][e0 + q]) = make_float4(p[q], p[q + 1], p[q + 2], p[q + 3]);
+    }
+    uint32_t my_e = 0;
+    for (int j = 0; j < k; ++j) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int q = 1; q < VPL; ++q) m = max(m, key[q]);
+      m = row_max_u32(m);
+      uint32_t qsel = VPL;
+#pragma unroll
+      for (int q = VPL - 1; q >= 0; --q) qsel = key[q] == m ? (uint32_t)q : qsel;
+      const uint32_t ew = row_min_u32(qsel < VPL ? (uint32_t)e0 + qsel : 0xffffffffu);
+      const uint32_t qq = ew - (uint32_t)e0;  // < VPL only in the owner lane
+#pragma unroll
+      for (int q = 0; q < VPL; ++q) key[q] = qq == (uint32_t)q ? 0u : key[q];
+      if (r == j) my_e = ew;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float my_p = r < k ? ps[wave][row][my_e] : 0.f;
+    const float sum = row_sum_f32(r < k ? fabsf(my_p) : 0.f);
+    const float denom = sum < 1e-12f ? 1e-12f : sum;  // NaN propagates
+    if (t < T && r < k) {
+      out_idx[t * k + r] = my_e;
+      out_w[t * k + r] = my_p / denom;
+      if (out_p) out_p[t * k + r] = my_p;
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -161,7 +302,9 @@ extern "C" int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, 
   ZMOE_REQUIRE(k >= 1 && k <= E && k <= 64, ZMOE_ERR_SHAPE, "route_topk: need 1 <= k <= min(E, 64) (k=%d, E=%d)", k, E);
   if (T == 0) return ZMOE_OK;
   ZMOE_REQUIRE(logits && expert_biases && topk_idx && topk_weight, ZMOE_ERR_NULL, "route_topk: null pointer");
-  const dim3 grid((unsigned)cdiv(T, 4)), block(256);
+  // 4 waves per block, 8 blocks per CU at most: the waves loop over the remaining tokens
+  const int64_t blocks = cdiv(T, 4) < 2048 ? cdiv(T, 4) : 2048;
+  const dim3 grid((unsigned)blocks), block(256);
   const int per_lane = (E + 63) / 64;
   auto launch = [&](auto pl, auto lt) {
     using LT = decltype(lt);
@@ -176,6 +319,18 @@ extern "C" int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, 
     else if (per_lane <= 8) launch(std::integral_constant<int, 8>{}, lt);
     else launch(std::integral_constant<int, 16>{}, lt);
   };
+  if (logits_dtype == ZMOE_DTYPE_BF16 && E % 8 == 0 && E <= 256 && k <= 16 && aligned16(logits)) {
+    // four tokens per wave, one per 16-lane row (8 or 16 experts per lane)
+    const int64_t rows_blocks = cdiv(cdiv(T, 4), 4);
+    const dim3 g4((unsigned)(rows_blocks < 2048 ? rows_blocks : 2048));
+    if (E <= 128)
+      hipLaunchKernelGGL(route_topk_rows_kernel<8>, g4, block, 0, as_stream(stream), (const uint16_t*)logits, T, E, k,
+                         expert_biases, round_probs_bf16, topk_idx, topk_weight, topk_prob);
+    else
+      hipLaunchKernelGGL(route_topk_rows_kernel<16>, g4, block, 0, as_stream(stream), (const uint16_t*)logits, T, E,
+                         k, expert_biases, round_probs_bf16, topk_idx, topk_weight, topk_prob);
+    return check_launch("route_topk");
+  }
   if (logits_dtype == ZMOE_DTYPE_BF16) by_width(uint16_t{});
   else by_width(float{});
   return check_launch("route_topk");

@@ -2,10 +2,12 @@
 //
 // flatten_sort_count is a three-launch LDS counting sort over R = T*k slots:
 //   1. tile histograms: each 256-thread block counts kSortTile slots into LDS
-//      (E+1 buckets; bucket E collects out-of-range ids);
-//   2. one block turns the [tiles x buckets] table into per-tile bucket bases
-//      (column prefix over tiles, then an exclusive scan over buckets) and
-//      writes the inclusive expert_offsets;
+//      (E+1 buckets; bucket E collects out-of-range ids) and writes them into a
+//      bucket-major table, table[e * ntiles + tile];
+//   2. one block turns the table into per-tile bucket bases: one wave per bucket
+//      reads the bucket's contiguous row of tile counts (16-byte loads), the row
+//      totals are scanned over the buckets in LDS, then each wave prefix-scans its
+//      rows in place; it also writes the inclusive expert_offsets and the flag;
 //   3. each block re-reads its tile in order, 256 slots per round; a wave finds
 //      lanes holding the same expert with a ballot per id bit, ranks itself
 //      among them, and adds the counts of the earlier waves, so equal experts
@@ -18,126 +20,215 @@
 
 namespace zmoe {
 
-constexpr int kSortTile = 2048;
+constexpr int kSortTile = 1024;
 constexpr int kSortThreads = 256;
 constexpr int kSortMaxE = 1024;
 constexpr size_t kSortHeader = 256;  // flag + padding at the start of the workspace
+constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ int bucket_of(int64_t v, int E) { return (v >= 0 && v < E) ? (int)v : E; }
 
 __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(const int64_t* __restrict__ idx, int64_t R,
-                                                                 int E, int32_t* __restrict__ tile_hist) {
+                                                                 int E, int ntiles, int32_t* __restrict__ table) {
   __shared__ int32_t h[kSortMaxE + 1];
   for (int e = threadIdx.x; e <= E; e += kSortThreads) h[e] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  for (int i = threadIdx.x; i < kSortTile; i += kSortThreads) {
-    const int64_t s = base + i;
+#pragma unroll
+  for (int i = 0; i < kSortTile / kSortThreads; ++i) {
+    const int64_t s = base + i * kSortThreads + threadIdx.x;
     if (s < R) atomicAdd(&h[bucket_of(idx[s], E)], 1);
   }
   __syncthreads();
-  int32_t* out = tile_hist + (int64_t)blockIdx.x * (E + 1);
-  for (int e = threadIdx.x; e <= E; e += kSortThreads) out[e] = h[e];
+  for (int e = threadIdx.x; e <= E; e += kSortThreads) table[(int64_t)e * ntiles + blockIdx.x] = h[e];
 }
 
-// Single block of 1024 threads; buckets are strided over the threads. A bucket's column
-// is walked kScanBatch tiles at a time, all of a batch's loads issued before any is used
-// (one memory round trip per batch instead of per tile).
-constexpr int kScanBatch = 16;
-__global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ tile_hist, int ntiles, int E,
-                                                         int64_t* __restrict__ offsets,
-                                                         int32_t* __restrict__ flag) {
-  __shared__ int64_t tot[kSortMaxE + 1];
-  __shared__ int64_t start[kSortMaxE + 1];
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    int64_t total = 0;
-    for (int b0 = 0; b0 < ntiles; b0 += kScanBatch) {
-      int32_t c[kScanBatch];
+// Sum (mode 0) or exclusive prefix plus `start` written back in place (mode 1) of one
+// bucket's row of ntiles counts, by one wave. Lanes take 4 consecutive tiles per step
+// (one 16-byte load when the row is 16-byte aligned, ntiles % 4 == 0).
+__device__ __forceinline__ int64_t scan_row(int32_t* __restrict__ row, int ntiles, int lane, bool vec,
+                                            int64_t start, bool write) {
+  int64_t run = start;
+  for (int c0 = 0; c0 < ntiles; c0 += 256) {
+    const int i0 = c0 + lane * 4;
+    int32_t v[4] = {0, 0, 0, 0};
+    if (vec && i0 + 3 < ntiles) {
+      const int4 q = *reinterpret_cast<const int4*>(row + i0);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
 #pragma unroll
-      for (int j = 0; j < kScanBatch; ++j)
-        c[j] = b0 + j < ntiles ? tile_hist[(int64_t)(b0 + j) * (E + 1) + e] : 0;
-#pragma unroll
-      for (int j = 0; j < kScanBatch; ++j) total += c[j];
+      for (int u = 0; u < 4; ++u) v[u] = i0 + u < ntiles ? row[i0 + u] : 0;
     }
-    tot[e] = total;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {  // E+1 <= 1025 buckets: a serial scan is cheap next to the column sums
-    int64_t run = 0;
-    for (int q = 0; q <= E; ++q) {
-      start[q] = run;
-      run += tot[q];
+    const int32_t mine = v[0] + v[1] + v[2] + v[3];
+    // inclusive wave scan of the lane sums
+    int32_t inc = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t t = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += t;
     }
-    flag[0] = tot[E] > 0 ? 1 : 0;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    if (e < E) offsets[e] = start[e] + tot[e];
-    int64_t run = start[e];
-    for (int b0 = 0; b0 < ntiles; b0 += kScanBatch) {
-      int32_t c[kScanBatch];
+    if (write) {
+      int64_t pos = run + (inc - mine);
 #pragma unroll
-      for (int j = 0; j < kScanBatch; ++j)
-        c[j] = b0 + j < ntiles ? tile_hist[(int64_t)(b0 + j) * (E + 1) + e] : 0;
-#pragma unroll
-      for (int j = 0; j < kScanBatch; ++j) {
-        if (b0 + j < ntiles) tile_hist[(int64_t)(b0 + j) * (E + 1) + e] = (int32_t)run;
-        run += c[j];
+      for (int u = 0; u < 4; ++u) {
+        if (i0 + u < ntiles) row[i0 + u] = (int32_t)pos;
+        pos += v[u];
       }
     }
+    run += __shfl(inc, 63, 64);
   }
+  return run;
+}
+
+// Rows of at most 256 tiles (R <= 262144 slots), kScanRows buckets per wave: every row a
+// wave owns is loaded at once and kept in registers between the totals and the write-back.
+constexpr int kScanRows = 17;  // E + 1 <= 272 buckets (C3: 129, C4: 257)
+
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(int32_t* __restrict__ table, int ntiles, int E,
+                                                                 int64_t* __restrict__ offsets,
+                                                                 int32_t* __restrict__ flag) {
+  __shared__ int64_t tot[kSortMaxE + 1];
+  __shared__ int64_t start[kSortMaxE + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = kScanThreads / 64;
+  const bool vec = (ntiles & 3) == 0;
+  const bool fast = vec && ntiles <= 256 && E + 1 <= nwaves * kScanRows;
+  int4 row[kScanRows];
+  int32_t inc[kScanRows];
+  if (fast) {  // one batch of loads per wave, rows kept for the write-back
+#pragma unroll
+    for (int r = 0; r < kScanRows; ++r) {
+      const int e = wave + r * nwaves;
+      row[r] = make_int4(0, 0, 0, 0);
+      if (e <= E && lane * 4 < ntiles) row[r] = *reinterpret_cast<const int4*>(table + (int64_t)e * ntiles + lane * 4);
+    }
+#pragma unroll
+    for (int r = 0; r < kScanRows; ++r) inc[r] = wave_incl_scan(row[r].x + row[r].y + row[r].z + row[r].w, lane);
+#pragma unroll
+    for (int r = 0; r < kScanRows; ++r) {
+      const int e = wave + r * nwaves;
+      if (e <= E && lane == 63) tot[e] = inc[r];
+    }
+  } else {
+    for (int e = wave; e <= E; e += nwaves) {
+      const int64_t t = scan_row(table + (int64_t)e * ntiles, ntiles, lane, vec, 0, false);
+      if (lane == 0) tot[e] = t;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of the E+1 bucket totals, 64 buckets per step
+    int64_t run = 0;
+    for (int e0 = 0; e0 <= E; e0 += 64) {
+      const int e = e0 + lane;
+      const int64_t mine = e <= E ? tot[e] : 0;
+      int64_t inc = mine;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int64_t u = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += u;
+      }
+      if (e <= E) {
+        start[e] = run + inc - mine;
+        if (e < E) offsets[e] = run + inc;
+        if (e == E) flag[0] = mine > 0 ? 1 : 0;
+      }
+      run += __shfl(inc, 63, 64);
+    }
+  }
+  __syncthreads();
+  if (fast) {
+#pragma unroll
+    for (int r = 0; r < kScanRows; ++r) {
+      const int e = wave + r * nwaves;
+      if (e <= E && lane * 4 < ntiles) {
+        const int32_t b = (int32_t)start[e] + inc[r] - (row[r].x + row[r].y + row[r].z + row[r].w);
+        *reinterpret_cast<int4*>(table + (int64_t)e * ntiles + lane * 4) =
+            make_int4(b, b + row[r].x, b + row[r].x + row[r].y, b + row[r].x + row[r].y + row[r].z);
+      }
+    }
+    return;
+  }
+  for (int e = wave; e <= E; e += nwaves)
+    scan_row(table + (int64_t)e * ntiles, ntiles, lane, vec, start[e], true);
+}
+
+// Each wave owns kSortTile / 4 consecutive slots of the block's tile. Pass 1: the wave
+// counts its slots per bucket (peer groups by ballots over the id bits, the group leader
+// adds the group size). After one barrier every wave's base for bucket e is the tile's
+// base plus the counts of the waves before it. Pass 2 re-ranks the slots 64 at a time in
+// slot order, with no further block barrier: stable within the wave, and the waves'
+// ranges follow slot order.
+constexpr int kWaveSlots = kSortTile / (kSortThreads / 64);
+
+__device__ __forceinline__ uint64_t peer_mask(int key, int nbits) {
+  uint64_t peers = ~0ull;
+  for (int b = 0; b < nbits + 1; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
 }
 
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
-    const int64_t* __restrict__ idx, int64_t R, int E, const int32_t* __restrict__ tile_base,
+    const int64_t* __restrict__ idx, int64_t R, int E, int ntiles, const int32_t* __restrict__ table,
     int64_t* __restrict__ sorted_expert, int64_t* __restrict__ sorted_slot, int32_t* __restrict__ inverse) {
-  __shared__ int32_t base[kSortMaxE + 1];
-  __shared__ int32_t wcount[kSortThreads / 64][kSortMaxE + 1];
+  __shared__ int32_t wcount[kSortThreads / 64][kSortMaxE + 1];  // pass 1: per-wave bucket counts
+  __shared__ int32_t wpos[kSortThreads / 64][kSortMaxE + 1];    // pass 2: per-wave running positions
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int32_t* tb = tile_base + (int64_t)blockIdx.x * (E + 1);
-  for (int e = threadIdx.x; e <= E; e += kSortThreads) {
-    base[e] = tb[e];
+  for (int e = threadIdx.x; e <= E; e += kSortThreads)
 #pragma unroll
     for (int w = 0; w < kSortThreads / 64; ++w) wcount[w][e] = 0;
-  }
   __syncthreads();
   int nbits = 1;
   while ((1 << nbits) <= E) ++nbits;  // ids 0..E need nbits bits
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int64_t tile0 = (int64_t)blockIdx.x * kSortTile;
-  for (int r = 0; r < kSortTile; r += kSortThreads) {
-    const int64_t s = tile0 + r + threadIdx.x;
-    const bool live = s < R;
-    int64_t v = 0;
-    int key = E + 1;  // lanes past R use an id no live lane has
-    if (live) {
-      v = idx[s];
-      key = bucket_of(v, E);
-    }
-    uint64_t peers = ~0ull;
-    for (int b = 0; b < nbits + 1; ++b) {
-      const bool bit = (key >> b) & 1;
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
-    }
+  const int64_t s0 = (int64_t)blockIdx.x * kSortTile + (int64_t)wave * kWaveSlots;
+  int64_t v[kWaveSlots / 64];
+  int key[kWaveSlots / 64];
+#pragma unroll
+  for (int r = 0; r < kWaveSlots / 64; ++r) {
+    const int64_t s = s0 + r * 64 + lane;
+    v[r] = s < R ? idx[s] : 0;
+    key[r] = s < R ? bucket_of(v[r], E) : E + 1;  // lanes past R use an id no live lane has
+  }
+#pragma unroll
+  for (int r = 0; r < kWaveSlots / 64; ++r) {
+    const uint64_t peers = peer_mask(key[r], nbits);
+    if (key[r] <= E && __popcll(peers & lt_mask) == 0) wcount[wave][key[r]] += __popcll(peers);
+  }
+  __syncthreads();
+  // this wave's running position per bucket: tile base + counts of the earlier waves
+  for (int e = lane; e <= E; e += 64) {
+    int32_t base = table[(int64_t)e * ntiles + blockIdx.x];
+    for (int w = 0; w < wave; ++w) base += wcount[w][e];
+    wpos[wave][e] = base;  // only this wave touches its row from here on
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int r = 0; r < kWaveSlots / 64; ++r) {
+    const int64_t s = s0 + r * 64 + lane;
+    const uint64_t peers = peer_mask(key[r], nbits);
     const int rank = __popcll(peers & lt_mask);
-    const int cnt = __popcll(peers);
-    const bool leader = rank == 0;
-    if (live && leader) wcount[wave][key] = cnt;
-    __syncthreads();
+    const bool live = key[r] <= E;
+    int pos = 0;
+    if (live) pos = wpos[wave][key[r]] + rank;
+    __builtin_amdgcn_wave_barrier();
+    if (live && rank == 0) wpos[wave][key[r]] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
     if (live) {
-      int pos = base[key] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcount[w][key];
-      sorted_expert[pos] = v;
+      sorted_expert[pos] = v[r];
       sorted_slot[pos] = s;
       if (inverse) inverse[s] = pos;
     }
-    __syncthreads();
-    if (live && leader) {
-      atomicAdd(&base[key], cnt);
-      wcount[wave][key] = 0;
-    }
-    __syncthreads();
   }
 }
 
@@ -211,14 +302,14 @@ int sort_pointer_checks(const int64_t* expert_idxs, int64_t R, int64_t* sorted_e
 // every byte they read is written earlier in the same call, so nothing needs clearing.
 int sort_launch(const int64_t* expert_idxs, int64_t R, int E, int64_t* sorted_expert_idxs,
                 int64_t* sorted_scattered_idxs, int64_t* expert_offsets, int32_t* inverse, int32_t* flag,
-                int32_t* tile_hist, hipStream_t s, const char* name) {
+                int32_t* table, hipStream_t s, const char* name) {
   const int ntiles = (int)cdiv(R, kSortTile);
   if (ntiles > 0)
-    hipLaunchKernelGGL(sort_hist_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, tile_hist);
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, s, tile_hist, ntiles, E, expert_offsets, flag);
+    hipLaunchKernelGGL(sort_hist_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles, table);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, table, ntiles, E, expert_offsets, flag);
   if (ntiles > 0)
-    hipLaunchKernelGGL(sort_scatter_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, tile_hist,
-                       sorted_expert_idxs, sorted_scattered_idxs, inverse);
+    hipLaunchKernelGGL(sort_scatter_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles,
+                       table, sorted_expert_idxs, sorted_scattered_idxs, inverse);
   return check_launch(name);
 }
 

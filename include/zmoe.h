@@ -102,7 +102,7 @@ const int32_t* zmoe_sort_error_flag(const void* workspace);
  * file-scope device array of ZMOE_SORT_NOALLOC_MAX_BYTES per GPU (held until the
  * process ends), so the call allocates nothing. Sizes whose workspace
  * (zmoe_sort_workspace_bytes(R, E)) exceeds that maximum return
- * ZMOE_ERR_WORKSPACE: R up to ~16.6 M slots at E = 128, ~2.1 M at E = 1024.
+ * ZMOE_ERR_WORKSPACE: R up to ~8.3 M slots at E = 128, ~1.05 M at E = 1024.
  * error_flag (nullable, caller-owned device int32) receives 1 when an id was
  * outside [0, E), else 0. Every call on one GPU shares that GPU's array, so calls
  * that overlap on one GPU (different streams, threads) race; the array needs no

@@ -47,7 +47,7 @@ def test_pure_host_entry_points():
     assert lib.zmoe_status_string(0) == b"ok"
     assert lib.zmoe_status_string(4) == b"misaligned pointer or stride"
     # workspace sizing is host arithmetic: header + one int32 per (tile, bucket)
-    assert lib.zmoe_sort_workspace_bytes(262144, 128) == 256 + (262144 // 2048) * 129 * 4
+    assert lib.zmoe_sort_workspace_bytes(262144, 128) == 256 + (262144 // 1024) * 129 * 4
 
 
 def test_argument_errors_are_reported_without_a_gpu():

@@ -25,7 +25,10 @@ def _route_case(T, E, k, seed, dtype, bias_std, ties=False, nan=False):
 
 
 @pytest.mark.parametrize("T,E,k", [(2048, 8, 2), (1000, 64, 8), (777, 128, 8), (300, 256, 8), (64, 1024, 16),
-                                   (33, 5, 5), (16, 70, 1)])
+                                   (33, 5, 5), (16, 70, 1),
+                                   # bf16 four-tokens-per-wave kernel: partial 16-expert lanes, one
+                                   # occupied lane, k = 16, token counts not divisible by 4
+                                   (513, 200, 8), (99, 136, 16), (50, 8, 8), (1001, 120, 3), (64, 256, 16)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_route_topk_bit_exact(hip_device, T, E, k, dtype):
     logits, bias = _route_case(T, E, k, seed=T + E, dtype=dtype, bias_std=0.1, ties=True, nan=T > 3)
@@ -38,6 +41,22 @@ def test_route_topk_bit_exact(hip_device, T, E, k, dtype):
     np.testing.assert_array_equal(p.cpu().numpy(), rp)  # sigmoid evaluated identically (f64, one rounding)
     ok = ~np.isnan(rw).any(axis=1)
     assert_close(w.cpu().numpy()[ok], rw[ok], rtol=1e-6, atol=1e-7, what="topk_weight")
+
+
+@pytest.mark.parametrize("bias_std", [0.0, 0.3])
+def test_route_topk_every_bf16_logit(hip_device, bias_std):
+    """Every one of the 65536 bf16 values as a logit (NaNs, infinities, subnormals and both
+    zeros included), all selected (k = E = 64): each probability equals the oracle's
+    bf16(fp32(sigmoid in float64)) bit for bit, whichever evaluation the kernel used."""
+    from zmoe import ops
+
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    logits = bits.view(torch.bfloat16).reshape(1024, 64)
+    bias = torch.randn(64, generator=gen(9)) * bias_std
+    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), 64, round_probs_bf16=True)
+    ridx, rw, rp = O.route_topk(logits.float().numpy(), bias.numpy(), 64, round_probs_bf16=True)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)
 
 
 def test_route_equal_scores_and_forced_bias(hip_device):

@@ -76,7 +76,7 @@ def test_noalloc_sort_rejects_sizes_above_its_scratch():
     lib = L.load()
     p = ctypes.c_void_p(256)
     E = 1024
-    R = 2048 * 1100  # 1100 tiles x 1025 buckets x 4 bytes > 4 MiB
+    R = 2048 * 1100  # 2200 tiles of 1024 slots x 1025 buckets x 4 bytes > 4 MiB
     assert lib.zmoe_sort_workspace_bytes(R, E) > 4 << 20
     rc = lib.zmoe_flatten_sort_count_noalloc(p, R, E, p, p, p, None, None, None)
     assert rc == 5 and b"maximum" in lib.zmoe_last_error()
