@@ -236,39 +236,6 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
   return base + x - v;
 }
 
-// tstart[e] = first m-tile of expert e (tiles of BM rows, back to back); tstart[E] = total.
-template <int BM, int NT = kGemmThreads>
-__device__ int build_tile_starts(const int64_t* __restrict__ off, int E, int* tstart, int* tmp) {
-  const int ept = (E + NT - 1) / NT;  // <= 4
-  const int e0 = threadIdx.x * ept;
-  int nt[4] = {0, 0, 0, 0};
-  int local = 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int e = e0 + q;
-    if (q < ept && e < E) {
-      const int64_t a = e ? off[e - 1] : 0;
-      int64_t c = off[e] - a;
-      c = c < 0 ? 0 : c;
-      nt[q] = (int)((c + BM - 1) / BM);
-      local += nt[q];
-    }
-  }
-  int total;
-  int run = block_exclusive_scan<NT>(local, tmp, &total);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int e = e0 + q;
-    if (q < ept && e < E) {
-      tstart[e] = run;
-      run += nt[q];
-    }
-  }
-  if (threadIdx.x == 0) tstart[E] = total;
-  __syncthreads();
-  return total;
-}
-
 // Logical tile of this workgroup under the XCD-aware mapping, or -1.
 __device__ __forceinline__ int xcd_logical_tile(int total) {
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
@@ -354,25 +321,50 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
     t.rows = min(BM, p.ns_sym_m - mt * BM);
     return true;
   }
-  int* tstart = reinterpret_cast<int*>(smem);
-  int* tmp = tstart + kGemmMaxE + 4;
-  const int mtiles = build_tile_starts<BM, NT>(p.offsets, p.E, tstart, tmp);
-  const int logical = xcd_logical_tile(mtiles * p.n_tiles);
-  if (logical < 0) return false;
-  const int mt = logical / p.n_tiles;
-  t.nt = logical % p.n_tiles;
-  int lo = 0, hi = p.E - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tstart[mid] <= mt) lo = mid;
-    else hi = mid - 1;
+  // One pass over the expert ends: each thread counts the m-tiles of its experts, a
+  // block scan places them, and the thread whose expert holds this workgroup's m-tile
+  // posts (expert, first row, rows) to LDS. The offsets are read once, so the decode
+  // costs one global round trip.
+  int64_t* found = reinterpret_cast<int64_t*>(smem);  // [0] expert, [1] first row, [2] rows
+  int* tmp = reinterpret_cast<int*>(smem + 32);
+  const int ept = (p.E + NT - 1) / NT;  // <= 4
+  const int e0 = threadIdx.x * ept;
+  int64_t ebeg[4] = {0, 0, 0, 0}, eend[4] = {0, 0, 0, 0};
+  int ntl[4] = {0, 0, 0, 0};
+  int local = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = e0 + q;
+    if (q < ept && e < p.E) {
+      ebeg[q] = e ? p.offsets[e - 1] : 0;
+      eend[q] = p.offsets[e];
+      const int64_t c = eend[q] > ebeg[q] ? eend[q] - ebeg[q] : 0;
+      ntl[q] = (int)((c + BM - 1) / BM);
+      local += ntl[q];
+    }
   }
-  t.e = lo;
+  int mtiles;
+  int run = block_exclusive_scan<NT>(local, tmp, &mtiles);
+  const int logical = xcd_logical_tile(mtiles * p.n_tiles);
+  if (logical < 0) return false;  // uniform per workgroup
+  const int mt = logical / p.n_tiles;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (mt >= run && mt < run + ntl[q]) {  // (ntl[q] is 0 past the last expert)
+      const int64_t r0 = ebeg[q] + (int64_t)(mt - run) * BM;
+      found[0] = e0 + q;
+      found[1] = r0;
+      found[2] = min((int64_t)BM, eend[q] - r0);
+    }
+    run += ntl[q];
+  }
+  __syncthreads();
+  t.e = (int)found[0];
+  t.row0 = found[1];
+  t.rows = (int)found[2];
+  t.nt = logical % p.n_tiles;
   t.mt = 0;
-  const int64_t e_begin = lo ? p.offsets[lo - 1] : 0;
-  t.row0 = e_begin + (int64_t)(mt - tstart[lo]) * BM;
-  t.rows = (int)min((int64_t)BM, p.offsets[lo] - t.row0);
-  __syncthreads();  // tstart is dead; LDS becomes operand stages
+  __syncthreads();  // the decode area is dead; LDS becomes operand stages
   return true;
 }
 
