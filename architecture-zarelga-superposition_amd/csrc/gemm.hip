@@ -34,8 +34,9 @@
 //     sharing an expert's weights and rows run on one XCD and share its L2.
 // The f32 kernels use the same tiling with VGPR-staged loads, 32-deep stages and
 // v_mfma_f32_32x32x2f32 (four per 16-byte fragment).
-#include <cstdlib>
+#include <mutex>
 #include <type_traits>
+#include <unordered_set>
 
 #include "zmoe_internal.h"
 
@@ -1712,15 +1713,18 @@ constexpr int bf16_lds_bytes() {
   return main_loop > decode ? main_loop : decode;
 }
 
+// One attribute call per kernel (keyed by the kernel's address: instantiations share a
+// function type), under a lock, since callers may launch from several host threads.
 template <typename K>
 int prepare(K kernel, int lds_bytes) {
-  static bool done = false;  // one attribute call per instantiation
-  if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
-    if (e != hipSuccess) return set_error(ZMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    done = true;
-  }
+  static std::mutex mu;
+  static std::unordered_set<const void*> done;
+  const void* key = reinterpret_cast<const void*>(kernel);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count(key)) return ZMOE_OK;
+  hipError_t e = hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+  if (e != hipSuccess) return set_error(ZMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  done.insert(key);
   return ZMOE_OK;
 }
 
@@ -1777,31 +1781,14 @@ int launch_wgrad_big(const WgradParams& p, hipStream_t s) {
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
-// ZMOE_GEMM_TILE=128|256 pins the choice (a tuning knob; unset = automatic).
-inline bool use_big_tiles(int64_t R, int E, int64_t N) {
-  static const int forced = [] {
-    const char* v = getenv("ZMOE_GEMM_TILE");
-    return v ? atoi(v) : 0;
-  }();
-  if (forced == 128) return false;
-  if (forced == 256) return N >= 256;
-  return R >= (int64_t)E * 256 && N >= 256;
-}
+inline bool use_big_tiles(int64_t R, int E, int64_t N) { return R >= (int64_t)E * 256 && N >= 256; }
 
 // Weight grads under a skewed routing: experts holding at most this many rows get a
 // launch of 128 x 128 tiles of their own (two workgroups per CU, so one's output writes
 // overlap the other's loads), the rest the 256 x 256 tiles; 0 = one launch. The row
 // counts stay on the device: each launch covers every expert's tiles and a workgroup
 // whose expert belongs to the other launch exits at once (~0.2-0.5 ns per workgroup).
-// ZMOE_WGRAD_SMALL_ROWS=n pins the bound (a tuning knob; unset = automatic).
-inline int wgrad_small_rows(int64_t R, int E) {
-  static const int forced = [] {
-    const char* v = getenv("ZMOE_WGRAD_SMALL_ROWS");
-    return v ? atoi(v) : -1;
-  }();
-  if (forced >= 0) return forced;
-  return R < (int64_t)E * 1024 ? 64 : 0;
-}
+inline int wgrad_small_rows(int64_t R, int E) { return R < (int64_t)E * 1024 ? 64 : 0; }
 
 // ==================================================================== small-M streaming path
 // Forward rows GEMMs when the experts hold few rows (the small-batch regime, e.g. a

@@ -13,7 +13,9 @@ the timed region.
 
 Prints ONE JSON line. ``roofline`` covers the dominant grouped-GEMM launch,
 timed live with HIP events on the stream it runs on; ``cpu_baseline`` times the
-numpy oracle (float32) on a bounded sample of the same workload.
+numpy oracle (float32) on a bounded sample of the same workload, and, under
+``c1_fwd_torch_eager``, the reference forward as eager torch at BASELINE.json's
+CPU config C1.
 """
 
 from __future__ import annotations
@@ -47,7 +49,11 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # HBM-side bytes per launch at C3 (L2 -> memory fabric reads and writes), from two
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over this script, each scaled by what
 # the same counter reads for a plain 1 GiB copy (reads x 2.000, writes x 1.000); the
-# commands and raw counts are in profiles/grouped_gemm_c3_hbm_bytes.md.
+# commands and raw counts are in TRAFFIC_C3_PROFILE. They hold for the GEMM source
+# they were measured on (TRAFFIC_C3_GEMM_SHA256, the sha256 of csrc/gemm.hip): when
+# that file differs, the line reports traffic null and says why.
+TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
+TRAFFIC_C3_GEMM_SHA256 = None
 TRAFFIC_C3 = {
     "glu_w1_forward#0": 6014018560,
     "scatter2scatter#0": 2750119936,
@@ -186,6 +192,44 @@ def cpu_baseline(T, d, E, k, f, fs, backward=True, budget_s=20.0, sample_T=1024)
                    f"(d={d}, E={E}, k={k}, f={f}, shared={fs}); mean of {len(timed)} steps after 1 warmup, "
                    f"{sec:.2f} s/step"),
     }
+
+
+def cpu_baseline_c1(budget_s=8.0):
+    """Time the reference forward as eager torch (float32) at C1
+    (T=2048, d=256, E=8, top-2, SwiGLU f=512, no shared expert), on the host cores."""
+    import torch
+
+    from oracle.torch_eager import c1_inputs, moe_forward
+
+    x, Wg, bias, W1, W2 = c1_inputs()
+    moe_forward(x, Wg, bias, W1, W2, 2)  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 50 and (time.perf_counter() - t_start < budget_s or len(times) < 3):
+        t0 = time.perf_counter()
+        moe_forward(x, Wg, bias, W1, W2, 2)
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[len(times) // 2]
+    return {
+        "value": x.shape[0] / sec,
+        "unit": "tokens/s",
+        "cores": int(torch.get_num_threads()),
+        "kind": "port",
+        "sample": (f"C1 forward (fp32, T=2048 d=256 E=8 k=2 SwiGLU f=512, no shared expert) as eager torch "
+                   f"(oracle/torch_eager.py); median of {len(times)} runs after 1 warmup, {1e3 * sec:.1f} ms/run"),
+    }
+
+
+def traffic_c3(name):
+    """(bytes, source note) of the dominant launch's measured HBM traffic at C3."""
+    import hashlib
+
+    path = os.path.join(PKG_ROOT, "csrc", "gemm.hip")
+    with open(path, "rb") as fh:
+        sha = hashlib.sha256(fh.read()).hexdigest()
+    if TRAFFIC_C3_GEMM_SHA256 is None or sha != TRAFFIC_C3_GEMM_SHA256:
+        return None, f"not measured for this csrc/gemm.hip (sha256 {sha[:12]}); {TRAFFIC_C3_PROFILE} is older"
+    return TRAFFIC_C3.get(name), f"{TRAFFIC_C3_PROFILE} (csrc/gemm.hip sha256 {sha[:12]})"
 
 
 COPY_PROBE_BYTES = 1 << 30  # device-to-device copy used to calibrate FETCH_SIZE / WRITE_SIZE
@@ -459,6 +503,9 @@ def main(argv=None):
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(T, d, E, k, f, fs, backward=backward, sample_T=min(1024, T))
+        cpu["c1_fwd_torch_eager"] = cpu_baseline_c1()
+    traffic, traffic_source = (traffic_c3(dom_name) if args.workload == "c3"
+                               else (None, "measured for the c3 workload only"))
 
     line = {
         "metric": METRIC,
@@ -489,7 +536,8 @@ def main(argv=None):
             "unit": "TFLOP/s",
             "frac": dom["tflops"] / PEAK_BF16_TFLOPS,
             "avg_ms": dom["avg_ms"],
-            "traffic": TRAFFIC_C3.get(dom_name) if args.workload == "c3" else None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
         },
         "cpu_baseline": cpu,
     }

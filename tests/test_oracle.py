@@ -650,3 +650,32 @@ def test_rmsnorm_backward_vs_torch_autograd_and_fd():
         lm = float((O.zc_rmsnorm_rows(X, w, rows=rows)[0] * dy).sum())
         a[q] = old
         assert abs((lp - lm) / (2 * eps) - an) < 1e-7
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_torch_eager_forward_equals_numpy_oracle(shared):
+    """oracle/torch_eager.py (the C1 CPU baseline: the reference forward as eager torch)
+    computes the numpy oracle's forward: the same routing, and on float64 inputs the
+    same outputs up to the oracle's float32 routing probabilities (it rounds the
+    logits and p to float32, as the layer stores them: relative 1e-6); on float32
+    inputs, float32 accuracy norm-wise. Top-k slot order is unspecified in the
+    reference (topk(sorted=False)), so slots are compared as per-token sets."""
+    from oracle.torch_eager import c1_inputs, moe_forward
+
+    x, Wg, bias, W1, W2 = c1_inputs(T=96, d=64, E=6, f=40, seed=3)
+    bias = torch.randn(6, generator=torch.Generator().manual_seed(4)) * 0.1
+    sh = tuple(torch.randn(s, generator=torch.Generator().manual_seed(5)) * 0.125
+               for s in ((24, 64), (24, 64), (64, 24))) if shared else None
+    orc = O.MoELayerOracle(_f64(Wg), bias.numpy().astype(np.float32), _f64(W1), _f64(W2), 3,
+                           shared=tuple(_f64(s) for s in sh) if shared else None)
+    rout, ridx, rw = orc.forward(_f64(x))
+    d = lambda t: t.to(torch.float64)  # noqa: E731
+    out, idx, w = moe_forward(d(x), d(Wg), d(bias), d(W1), d(W2), 3, shared=tuple(map(d, sh)) if shared else None)
+    np.testing.assert_array_equal(np.sort(idx.numpy(), axis=1), np.sort(ridx, axis=1))
+    order = np.argsort(idx.numpy(), axis=1)
+    rorder = np.argsort(ridx, axis=1)
+    np.testing.assert_allclose(np.take_along_axis(w.numpy(), order, 1), np.take_along_axis(rw, rorder, 1),
+                               rtol=1e-6, atol=0)
+    np.testing.assert_allclose(out.numpy(), rout, rtol=1e-6, atol=1e-7)
+    out32, _, _ = moe_forward(x, Wg, bias, W1, W2, 3, shared=sh)
+    assert np.linalg.norm(out32.double().numpy() - rout) <= 1e-5 * np.linalg.norm(rout)
