@@ -294,7 +294,22 @@ struct WgradParams {
   int m_tiles, n_tiles;
   uint32_t dy_bytes, x_bytes;  // addressable bytes from p.dy / p.x
   int rows_lo = 0, rows_hi = 0x7fffffff;  // bf16 kernels: only experts with rows_lo <= rows <= rows_hi
+  // >= 0: a dense split-K launch over this many rows, "expert" e being split e of E (the
+  // ranges of split_end below; offsets unused); < 0: the row ranges come from offsets
+  int64_t split_rows = -1;
 };
+
+// Row ranges of the split-K partials as inclusive ends: S near-equal ranges of M rows,
+// cut at multiples of 64 rows (whole K-loop stages).
+__host__ __device__ __forceinline__ int64_t split_end(int64_t M, int S, int s) {
+  const int64_t end = (s + 1 == S) ? M : ((M * (s + 1) / S + 63) / 64) * 64;
+  return end < M ? end : M;
+}
+
+// Inclusive end of expert (or split) e's rows in a weight-grad launch.
+__device__ __forceinline__ int64_t wgrad_rows_end(const WgradParams& p, int e) {
+  return p.split_rows >= 0 ? split_end(p.split_rows, p.E, e) : p.offsets[e];
+}
 
 struct RowsTile {
   int e, nt, rows, mt;  // mt: m-tile index within the expert (symmetric launches)
@@ -1541,8 +1556,8 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   const int e = logical / per_e;
   const int rem = logical % per_e;
   const int mt = rem / p.n_tiles, nt = rem % p.n_tiles;
-  const int64_t r_begin = e ? p.offsets[e - 1] : 0;
-  const int64_t r_end = p.offsets[e];
+  const int64_t r_begin = e ? wgrad_rows_end(p, e - 1) : 0;
+  const int64_t r_end = wgrad_rows_end(p, e);
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   if (nrows < p.rows_lo || nrows > p.rows_hi) return;  // the other launch of a split covers this expert
   const int m0 = mt * BM, n0 = nt * BN;
@@ -1664,13 +1679,11 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
 }
 
 // ------------------------------------------------------------------ dense split-K weight grads
-// Row ranges of the split-K partials as inclusive ends (the wgrad kernels' expert offsets):
-// S near-equal ranges, cut at multiples of 64 rows (whole K-loop stages).
+// The row range of an unsplit dense weight grad as a one-entry offsets array (for the
+// grouped entry point it runs through).
 __global__ void split_offsets_kernel(int64_t* __restrict__ off, int64_t M, int S) {
   const int s = threadIdx.x;
-  if (s >= S) return;
-  int64_t end = (s + 1 == S) ? M : ((M * (s + 1) / S + 63) / 64) * 64;
-  off[s] = end < M ? end : M;
+  if (s < S) off[s] = split_end(M, S, s);
 }
 
 // out[i] = sum over s of part[s][i] (fp32), rounded once to the output type.
@@ -2370,8 +2383,9 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   return check_launch("bias_grad_kernel");
 }
 
-// Workspace: the split offsets (one int64 per split, kDenseMaxSplits of them: 512 bytes, which
-// keeps the partials 256-byte aligned) + S fp32 partials of [N, K].
+// Workspace: a 512-byte header (the one-entry row range of an unsplit launch; the split
+// launches compute their ranges in the kernel; the header keeps the partials 256-byte
+// aligned) + S fp32 partials of [N, K].
 constexpr int kDenseMaxSplits = 64;
 constexpr size_t kDenseHeaderBytes = kDenseMaxSplits * sizeof(int64_t);
 
@@ -2398,12 +2412,15 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
                    (M == 0 || (ok_rows(dtype, DY, dy_stride_m) && ok_rows(dtype, X, x_stride_m))),
                ZMOE_ERR_ALIGN, "dense_wgrad: N, K and strides must be multiples of %d elements", v);
   hipStream_t s = as_stream(stream);
-  int64_t* off = reinterpret_cast<int64_t*>(workspace);
-  hipLaunchKernelGGL(split_offsets_kernel, dim3(1), dim3(64), 0, s, off, M, S);
-  int rc = check_launch("split_offsets_kernel");
-  if (rc) return rc;
-  if (S == 1) return zmoe_group_bwd_w(DY, dy_stride_m, X, x_stride_m, nullptr, 1, off, M, N, K, 1, dtype, DW,
-                                      nullptr, stream);
+  int rc = ZMOE_OK;
+  if (S == 1) {
+    int64_t* off = reinterpret_cast<int64_t*>(workspace);
+    hipLaunchKernelGGL(split_offsets_kernel, dim3(1), dim3(64), 0, s, off, M, S);
+    rc = check_launch("split_offsets_kernel");
+    if (rc) return rc;
+    return zmoe_group_bwd_w(DY, dy_stride_m, X, x_stride_m, nullptr, 1, off, M, N, K, 1, dtype, DW, nullptr,
+                            stream);
+  }
   WgradParams p{};
   p.dy = DY;
   p.lddy = dy_stride_m;
@@ -2413,7 +2430,8 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
   p.x_div = 1;
   p.x_div_shift = 0;
   p.dw = reinterpret_cast<char*>(workspace) + kDenseHeaderBytes;
-  p.offsets = off;
+  p.offsets = nullptr;
+  p.split_rows = M;  // the split ranges are computed in the kernel
   p.Ndy = (int)N;
   p.Kx = (int)K;
   p.E = S;

@@ -29,13 +29,14 @@ __device__ __forceinline__ float sigmoid_f64(float z) { return (float)(1.0 / (1.
 
 // bf16(sigmoid_f64(z)) (the probability a bf16 gate stores) from fp32 arithmetic where that
 // is provably the same value: the fp32 estimate is within a few fp32 ulps of the true
-// sigmoid (expf, one add, one divide), and so is sigmoid_f64's fp32 rounding, so both round
-// to the same bf16 unless they lie within 16 fp32 ulps of a bf16 rounding midpoint (low 16
-// bits near 0x8000). Those lanes (about 1 score in 2000), saturated arguments (|z| >= 80,
-// where expf overflows) and NaN take the double evaluation.
+// sigmoid (expf within 1 ulp, one add, v_rcp_f32 within 1 ulp), and so is sigmoid_f64's
+// fp32 rounding, so both round to the same bf16 unless they lie within 16 fp32 ulps of a
+// bf16 rounding midpoint (low 16 bits near 0x8000). Those lanes (about 1 score in 2000),
+// saturated arguments (|z| >= 80, where expf overflows) and NaN take the double
+// evaluation. (1 + expf(-z) lies in [1, 6e34] here, so the reciprocal is a normal float.)
 __device__ __forceinline__ float sigmoid_bf16(float z) {
   if (fabsf(z) < 80.f) {  // false for NaN
-    const float s = 1.0f / (1.0f + expf(-z));
+    const float s = __builtin_amdgcn_rcpf(1.0f + expf(-z));
     const uint32_t low = __float_as_uint(s) & 0xffffu;
     const uint32_t dist = low > 0x8000u ? low - 0x8000u : 0x8000u - low;
     if (dist > 16u) return to_f32(bf16_bits(s));
@@ -264,6 +265,25 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(const float* _
   const float dp = S_raw > 1e-12f ? (dwj - inner * sgn) / S : dwj / S;
   const float dz = dp * pj * (1.f - pj);
   GT* row = dlogits + t * ld;
+  if (k <= 16) {
+    // the k (expert, grad) pairs read once into scalar registers (k is uniform), then
+    // every lane picks its expert's grad: no cross-lane traffic per 64-expert block
+    int ek[16];
+    float vk[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      ek[j] = j < k ? __builtin_amdgcn_readlane(ej, j) : -1;
+      vk[j] = j < k ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dz), j)) : 0.f;
+    }
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v = ek[j] == e ? vk[j] : v;
+      if (e < E) row[e] = from_f32<GT>(v);
+    }
+    return;
+  }
   for (int e0 = 0; e0 < E; e0 += 64) {
     const int e = e0 + lane;
     float v = 0.f;

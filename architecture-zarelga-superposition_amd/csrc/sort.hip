@@ -1,9 +1,13 @@
 // Expert counting and the stable expert sort (scattermoe/parallel_experts.py:6-28).
 //
-// flatten_sort_count is a three-launch LDS counting sort over R = T*k slots:
+// flatten_sort_count is an LDS counting sort over R = T*k slots:
 //   1. tile histograms: each 256-thread block counts kSortTile slots into LDS
 //      (E+1 buckets; bucket E collects out-of-range ids) and writes them into a
 //      bucket-major table, table[e * ntiles + tile];
+//   2+3. for at most 256 tiles and 65536 counts (every C1-C5 shape), one
+//      scatter launch in which each block sums the table's bucket rows itself (all
+//      tiles, and the tiles before its own), scans the totals and ranks its tile as
+//      in 3 below; otherwise:
 //   2. one block turns the table into per-tile bucket bases: one wave per bucket
 //      reads the bucket's contiguous row of tile counts (16-byte loads), the row
 //      totals are scanned over the buckets in LDS, then each wave prefix-scans its
@@ -232,6 +236,154 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
   }
 }
 
+// Two-launch form of the sort for at most kFusedMaxTiles tiles and kFusedMaxTable counts
+// (every C1-C5 shape): the scatter blocks derive the bucket bases themselves, so the one-block scan
+// launch between histogram and scatter goes away. Block b reads the whole tile table
+// (L2-resident after the histogram launch; one wave per bucket row, 16-byte loads), sums
+// each bucket over all tiles and over the tiles before b, scans the bucket totals, and
+// ranks its tile as sort_scatter_kernel does, with eight waves of 128 slots.
+constexpr int kFusedThreads = 512;
+constexpr int kFusedWaves = kFusedThreads / 64;
+constexpr int kFusedWaveSlots = kSortTile / kFusedWaves;
+constexpr int64_t kFusedMaxTable = 1 << 16;
+constexpr int kFusedMaxTiles = 256;  // R <= 262144 slots: one 16-byte piece of a bucket row per lane
+
+// Wave-wide sum of a 32-bit integer: DPP within rows of 16, then the four row sums.
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);  // row_half_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true);  // row_mirror
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
+}
+
+__global__ __launch_bounds__(kFusedThreads) void sort_scatter_scan_kernel(
+    const int64_t* __restrict__ idx, int64_t R, int E, int ntiles, const int32_t* __restrict__ table,
+    int64_t* __restrict__ offsets, int32_t* __restrict__ flag, int64_t* __restrict__ sorted_expert,
+    int64_t* __restrict__ sorted_slot, int32_t* __restrict__ inverse) {
+  // pass 1: per-wave bucket counts, turned in place into each wave's running positions
+  __shared__ int32_t wcount[kFusedWaves][kSortMaxE + 1];
+  __shared__ int32_t tot[kSortMaxE + 1];                  // bucket totals over every tile
+  __shared__ int32_t base[kSortMaxE + 1];                 // counts before this tile, then its bucket bases
+  __shared__ int32_t part[kFusedWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.x;
+  for (int e = threadIdx.x; e <= E; e += kFusedThreads)
+#pragma unroll
+    for (int w = 0; w < kFusedWaves; ++w) wcount[w][e] = 0;
+  int nbits = 1;
+  while ((1 << nbits) <= E) ++nbits;  // ids 0..E need nbits bits
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t s0 = (int64_t)b * kSortTile + (int64_t)wave * kFusedWaveSlots;
+  int64_t v[kFusedWaveSlots / 64];
+  int key[kFusedWaveSlots / 64];
+#pragma unroll
+  for (int r = 0; r < kFusedWaveSlots / 64; ++r) {
+    const int64_t s = s0 + r * 64 + lane;
+    v[r] = s < R ? idx[s] : 0;
+    key[r] = s < R ? bucket_of(v[r], E) : E + 1;  // lanes past R use an id no live lane has
+  }
+  // bucket rows of the table: the sum over all tiles and over the tiles before this one.
+  // ntiles <= 256, so lane l holds tiles 4l .. 4l+3 of a row; a wave issues the loads of
+  // kRowBatch rows before reducing any, so their latencies overlap.
+  constexpr int kRowBatch = 17;  // E + 1 <= 136 rows in one batch of the eight waves
+  const bool vec = (ntiles & 3) == 0;
+  const int i0 = lane * 4;
+  for (int e0 = wave; e0 <= E; e0 += kRowBatch * kFusedWaves) {
+    int4 q[kRowBatch];
+#pragma unroll
+    for (int j = 0; j < kRowBatch; ++j) {
+      const int e = e0 + j * kFusedWaves;
+      q[j] = make_int4(0, 0, 0, 0);
+      if (e <= E && i0 < ntiles) {
+        const int32_t* row = table + (int64_t)e * ntiles + i0;
+        if (vec) {
+          q[j] = *reinterpret_cast<const int4*>(row);
+        } else {
+          q[j].x = row[0];
+          q[j].y = i0 + 1 < ntiles ? row[1] : 0;
+          q[j].z = i0 + 2 < ntiles ? row[2] : 0;
+          q[j].w = i0 + 3 < ntiles ? row[3] : 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRowBatch; ++j) {
+      const int e = e0 + j * kFusedWaves;
+      const int32_t all = q[j].x + q[j].y + q[j].z + q[j].w;
+      const int32_t before = (i0 < b ? q[j].x : 0) + (i0 + 1 < b ? q[j].y : 0) + (i0 + 2 < b ? q[j].z : 0) +
+                             (i0 + 3 < b ? q[j].w : 0);
+      const int32_t sa = wave_sum_i32(all), sb = wave_sum_i32(before);
+      if (lane == 0 && e <= E) {
+        tot[e] = sa;
+        base[e] = sb;
+      }
+    }
+  }
+  __syncthreads();  // wcount zeroed; tot and base complete
+#pragma unroll
+  for (int r = 0; r < kFusedWaveSlots / 64; ++r) {
+    const uint64_t peers = peer_mask(key[r], nbits);
+    if (key[r] <= E && __popcll(peers & lt_mask) == 0) wcount[wave][key[r]] += __popcll(peers);
+  }
+  // exclusive scan of the bucket totals: thread t owns buckets t * per .. t * per + per - 1
+  const int per = (E + 1 + kFusedThreads - 1) / kFusedThreads;  // <= 3
+  const int eb = (int)threadIdx.x * per;
+  int32_t mine = 0;
+  for (int u = 0; u < per; ++u)
+    if (eb + u <= E) mine += tot[eb + u];
+  int32_t inc = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) part[wave] = inc;
+  __syncthreads();  // pass-1 counts and the wave totals of the scan are in LDS
+  int32_t run = inc - mine;
+  for (int w = 0; w < wave; ++w) run += part[w];
+  for (int u = 0; u < per; ++u) {
+    const int e = eb + u;
+    if (e <= E) {
+      const int32_t t = tot[e];
+      // wave w's first position in bucket e: bucket start + counts of the earlier tiles +
+      // counts of the earlier waves of this tile
+      int32_t pos = run + base[e];
+#pragma unroll
+      for (int w = 0; w < kFusedWaves; ++w) {
+        const int32_t c = wcount[w][e];
+        wcount[w][e] = pos;
+        pos += c;
+      }
+      if (b == 0) {
+        if (e < E) offsets[e] = (int64_t)run + t;
+        else flag[0] = t > 0 ? 1 : 0;
+      }
+      run += t;
+    }
+  }
+  __syncthreads();  // every wave's running positions are in LDS
+  int32_t* wpos_row = wcount[wave];  // only this wave touches its row from here on
+#pragma unroll
+  for (int r = 0; r < kFusedWaveSlots / 64; ++r) {
+    const int64_t s = s0 + r * 64 + lane;
+    const uint64_t peers = peer_mask(key[r], nbits);
+    const int rank = __popcll(peers & lt_mask);
+    const bool live = key[r] <= E;
+    int pos = 0;
+    if (live) pos = wpos_row[key[r]] + rank;
+    __builtin_amdgcn_wave_barrier();
+    if (live && rank == 0) wpos_row[key[r]] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    if (live) {
+      sorted_expert[pos] = v[r];
+      sorted_slot[pos] = s;
+      if (inverse) inverse[s] = pos;
+    }
+  }
+}
+
 __global__ void zero_i64_kernel(int64_t* __restrict__ p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
@@ -298,14 +450,21 @@ int sort_pointer_checks(const int64_t* expert_idxs, int64_t R, int64_t* sorted_e
   return ZMOE_OK;
 }
 
-// The three launches over a workspace laid out as [flag | header padding | tile table];
-// every byte they read is written earlier in the same call, so nothing needs clearing.
+// The launches over a workspace laid out as [flag | header padding | tile table]: the
+// tile histograms, then the scatter that derives the bucket bases itself, or (for empty
+// inputs and larger tables) the one-block scan and the scatter.
+// Every byte they read is written earlier in the same call, so nothing needs clearing.
 int sort_launch(const int64_t* expert_idxs, int64_t R, int E, int64_t* sorted_expert_idxs,
                 int64_t* sorted_scattered_idxs, int64_t* expert_offsets, int32_t* inverse, int32_t* flag,
                 int32_t* table, hipStream_t s, const char* name) {
   const int ntiles = (int)cdiv(R, kSortTile);
   if (ntiles > 0)
     hipLaunchKernelGGL(sort_hist_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles, table);
+  if (ntiles > 0 && ntiles <= kFusedMaxTiles && (int64_t)(E + 1) * ntiles <= kFusedMaxTable) {
+    hipLaunchKernelGGL(sort_scatter_scan_kernel, dim3(ntiles), dim3(kFusedThreads), 0, s, expert_idxs, R, E,
+                       ntiles, table, expert_offsets, flag, sorted_expert_idxs, sorted_scattered_idxs, inverse);
+    return check_launch(name);
+  }
   hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, table, ntiles, E, expert_offsets, flag);
   if (ntiles > 0)
     hipLaunchKernelGGL(sort_scatter_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles,
