@@ -53,14 +53,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # they were measured on (TRAFFIC_C3_GEMM_SHA256, the sha256 of csrc/gemm.hip): when
 # that file differs, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
-TRAFFIC_C3_GEMM_SHA256 = None
+TRAFFIC_C3_GEMM_SHA256 = "742742fd211fc71bc445222673bf3505f57350b40985511ed96f50d7007bec6b"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6014018560,
-    "scatter2scatter#0": 2750119936,
-    "glu_w2_backward_dh#0": 2388471808,
-    "scatter2scatter#1": 5074219008,
-    "group_bwd_w#0": 2234429440,
-    "group_bwd_w#1": 3897198592,
+    "glu_w1_forward#0": 6080032682,
+    "scatter2scatter#0": 2737578581,
+    "glu_w2_backward_dh#0": 2409403264,
+    "scatter2scatter#1": 4963683882,
+    "group_bwd_w#0": 2261360810,
+    "group_bwd_w#1": 3878102016,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
