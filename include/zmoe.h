@@ -83,8 +83,10 @@ size_t zmoe_sort_workspace_bytes(int64_t R, int E);
  *   sorted_expert_idxs [R], sorted_scattered_idxs [R] (flat slot ids, equal
  *   experts in slot order), expert_offsets [E] (inclusive cumsum of counts),
  *   all int64; inverse [R] int32 (inverse[slot] = sorted position, may be NULL).
- * Indices outside [0, E) set the int32 flag at workspace offset 0 to 1 and are
- * dropped (not written); read it with zmoe_sort_error_flag.                   */
+ * Indices outside [0, E) are placed after every valid slot with their original
+ * value (the outputs stay a permutation; expert_offsets counts only valid ones)
+ * and set the int32 flag at workspace offset 0 to 1; read it with
+ * zmoe_sort_error_flag.                                                       */
 int zmoe_flatten_sort_count(const int64_t* expert_idxs, int64_t R, int E,
                             int64_t* sorted_expert_idxs,
                             int64_t* sorted_scattered_idxs,
