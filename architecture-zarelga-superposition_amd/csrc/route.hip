@@ -19,8 +19,8 @@ constexpr int kRouteMaxPerLane = 16;  // E <= 1024
 // score's key is at least 0x007fffff (that of -inf).
 __device__ __forceinline__ uint32_t score_key(float s) {
   uint32_t b = __float_as_uint(s);
-  if (s != s) b = 0x7fffffffu;
-  else if (s == 0.f) b = 0u;
+  b = s != s ? 0x7fffffffu : b;  // selects, not branches
+  b = s == 0.f ? 0u : b;
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
@@ -43,6 +43,19 @@ __device__ __forceinline__ float sigmoid_bf16(float z) {
   }
   return to_f32(bf16_bits(sigmoid_f64(z)));
 }
+
+// bf16(fp32(sigmoid_f64(z))) for every bf16 logit z, indexed by z's bits: the value
+// sigmoid_bf16 returns, read instead of evaluated when the logits themselves are bf16.
+// The build writes the entries (float64 sigmoid, one rounding to float, then to bf16 by
+// round to nearest even; NaN logits give 0x7fc0). 128 KB, read through the caches.
+__device__ const uint16_t kSigmoidBf16[65536] = {
+#include "zmoe_sigmoid_bf16.inc"
+};
+
+// The stored probability of a logit when the gate rounds to bf16: looked up for bf16
+// logits, evaluated for fp32 ones.
+__device__ __forceinline__ float sigmoid_bf16_of(uint16_t zb) { return to_f32(kSigmoidBf16[zb]); }
+__device__ __forceinline__ float sigmoid_bf16_of(float z) { return sigmoid_bf16(z); }
 
 // Wave-wide max of a 32-bit key, the same value in every lane: DPP within rows of 16
 // (xor 1, xor 2, half mirror, mirror: no LDS round trip), then the four row maxima
@@ -99,7 +112,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const LT* __restrict__ 
       p[q] = 0.f;
       key[q] = 0;  // padding never wins
       if (e < E) {
-        const float pv = round_bf16 ? sigmoid_bf16(to_f32(cur[q])) : sigmoid_f64(to_f32(cur[q]));
+        const float pv = round_bf16 ? sigmoid_bf16_of(cur[q]) : sigmoid_f64(to_f32(cur[q]));
         p[q] = pv;
         key[q] = score_key(pv + bq[q]);
       }
@@ -142,73 +155,106 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const LT* __restrict__ 
   }
 }
 
-// Row (16-lane) reductions by DPP; every lane of a row ends with the row's result.
+// Reductions over rows of LPR = 16 or 8 lanes by DPP (xor 1, xor 2, mirror within 8 lanes,
+// mirror within 16); every lane of a row ends with the row's result.
+template <int LPR>
 __device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, true));
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, true));
   v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, true));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true));
+  if (LPR == 16) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true));
   return v;
 }
+template <int LPR>
 __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0xB1, 0xF, 0xF, false));
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x4E, 0xF, 0xF, false));
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x141, 0xF, 0xF, false));
-  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x140, 0xF, 0xF, false));
+  if (LPR == 16) v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x140, 0xF, 0xF, false));
   return v;
 }
+template <int LPR>
 __device__ __forceinline__ float row_sum_f32(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));
+  if (LPR == 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));
   return v;
 }
 
-// bf16 logits, E % 8 == 0, E <= 16 * VPL, k <= 16: four tokens per wave, one per 16-lane
-// row. Lane r of a row holds experts VPL r .. VPL r + VPL - 1 (16-byte loads of the
-// contiguous logits row). Each round takes the row max of the score keys and the lowest
-// expert holding it (a row min over expert ids), both by DPP within the row; the taken
-// candidate's key is cleared in its lane. The selected probabilities are read back from
-// LDS once at the end. Same contract and values as route_topk_kernel.
-template <int VPL>
+// bf16 logits, E % 8 == 0, E <= LPR * VPL, k <= LPR: 64 / LPR tokens per wave, one per
+// row of LPR lanes. Lane r of a row holds experts VPL r .. VPL r + VPL - 1 (16-byte loads
+// of the contiguous logits row); with RB the bf16 probabilities come from kSigmoidBf16.
+// Each round takes the row max m of the score keys (DPP within the row), the
+// per-candidate hits key == m as wave masks, each lane's lowest hit expert, and the row
+// min of those (the lowest expert holding m); the owner lane clears its lowest hit, the
+// masks reused for that (a lane's first hit is a scalar mask product). The selected
+// probabilities are read back from LDS once at the end. A wave works through its groups
+// of rows with the next group's logits loaded while the current one is ranked. Same
+// contract and values as route_topk_kernel.
+template <int VPL, int LPR, bool RB>
 __global__ __launch_bounds__(256) void route_topk_rows_kernel(const uint16_t* __restrict__ logits, int64_t T,
                                                               int E, int k, const float* __restrict__ bias,
-                                                              int round_bf16, int64_t* __restrict__ out_idx,
+                                                              int64_t* __restrict__ out_idx,
                                                               float* __restrict__ out_w,
                                                               float* __restrict__ out_p) {
-  __shared__ float ps[4][4][16 * VPL];  // [wave][row][expert]
+  constexpr int TPW = 64 / LPR;  // tokens per wave
+  __shared__ float ps[4][TPW][LPR * VPL];  // [wave][row][expert]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = lane >> 4, r = lane & 15;
+  const int row = lane / LPR, r = lane % LPR;
   const int e0 = r * VPL;
   const bool has = e0 < E;  // E % 8 == 0: each 8-expert chunk of a lane is wholly in [0, E) or out
   float bq[VPL];
 #pragma unroll
   for (int q = 0; q < VPL; ++q) bq[q] = e0 + q < E ? bias[e0 + q] : 0.f;
-  const int64_t groups = (T + 3) / 4;
+  const int64_t groups = (T + TPW - 1) / TPW;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
-  for (int64_t g = (int64_t)blockIdx.x * 4 + wave; g < groups; g += nwaves) {
-    const int64_t t = g * 4 + row;
-    const bool live = t < T && has;
-    uint4 raw[VPL / 8];
-#pragma unroll
-    for (int c = 0; c < VPL / 8; ++c)
-      raw[c] = live && e0 + 8 * c < E ? *reinterpret_cast<const uint4*>(logits + t * (int64_t)E + e0 + 8 * c)
-                                      : make_uint4(0, 0, 0, 0);
-    float p[VPL];
-    uint32_t key[VPL];
+  // this lane's logits of group g, by buffer loads over the group's rows: lanes past T or E
+  // read zeros with no branch, so the wait for the table reads issued before a prefetch
+  // can leave the prefetch in flight
+  auto load = [&](int64_t gv, uint4* raw) {
+    // g is the same in every lane; say so, so that the descriptor stays in scalar registers
+    const int64_t g = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(gv >> 32)) << 32) |
+                                (uint32_t)__builtin_amdgcn_readfirstlane((int)gv));
+    const bool in = g < groups;
+    const int64_t rows_left = in ? T - TPW * g : 0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(logits + (in ? TPW * g * (int64_t)E : 0)), (short)0,
+        (int)((rows_left < TPW ? rows_left : TPW) * E * 2), 0x00020000);
 #pragma unroll
     for (int c = 0; c < VPL / 8; ++c) {
-      float z[8];
-      unpack_chunk(raw[c], z, uint16_t{});
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int q = 8 * c + u;
-        const float pv = round_bf16 ? sigmoid_bf16(z[u]) : sigmoid_f64(z[u]);
-        p[q] = pv;
-        key[q] = live && e0 + q < E ? score_key(pv + bq[q]) : 0u;
-      }
+      const uint32_t off = e0 + 8 * c < E ? (uint32_t)(row * E + e0 + 8 * c) * 2u : 0x80000000u;
+      raw[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
+  };
+  uint4 nxt[VPL / 8];
+  load((int64_t)blockIdx.x * 4 + wave, nxt);
+  for (int64_t g = (int64_t)blockIdx.x * 4 + wave; g < groups; g += nwaves) {
+    const int64_t t = g * TPW + row;
+    const bool live = t < T && has;
+    uint32_t zb[VPL];  // logit bits
+#pragma unroll
+    for (int c = 0; c < VPL / 8; ++c) {
+      const uint32_t w[4] = {nxt[c].x, nxt[c].y, nxt[c].z, nxt[c].w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) zb[8 * c + u] = (u & 1) ? w[u >> 1] >> 16 : w[u >> 1] & 0xffffu;
+    }
+    float p[VPL];
+    if constexpr (RB) {
+      uint32_t pb[VPL];  // all table reads in flight before the next group's logits are requested
+#pragma unroll
+      for (int q = 0; q < VPL; ++q) pb[q] = kSigmoidBf16[zb[q]];
+      load(g + nwaves, nxt);
+#pragma unroll
+      for (int q = 0; q < VPL; ++q) p[q] = __uint_as_float(pb[q] << 16);
+    } else {
+      load(g + nwaves, nxt);
+#pragma unroll
+      for (int q = 0; q < VPL; ++q) p[q] = sigmoid_f64(__uint_as_float(zb[q] << 16));
+    }
+    uint32_t key[VPL];
+#pragma unroll
+    for (int q = 0; q < VPL; ++q) key[q] = live && e0 + q < E ? score_key(p[q] + bq[q]) : 0u;
     if (has) {
 #pragma unroll
       for (int q = 0; q < VPL; q += 4)
@@ -219,19 +265,28 @@ __global__ __launch_bounds__(256) void route_topk_rows_kernel(const uint16_t* __
       uint32_t m = key[0];
 #pragma unroll
       for (int q = 1; q < VPL; ++q) m = max(m, key[q]);
-      m = row_max_u32(m);
-      uint32_t qsel = VPL;
+      m = row_max_u32<LPR>(m);
+      uint64_t hit[VPL];
 #pragma unroll
-      for (int q = VPL - 1; q >= 0; --q) qsel = key[q] == m ? (uint32_t)q : qsel;
-      const uint32_t ew = row_min_u32(qsel < VPL ? (uint32_t)e0 + qsel : 0xffffffffu);
-      const uint32_t qq = ew - (uint32_t)e0;  // < VPL only in the owner lane
+      for (int q = 0; q < VPL; ++q) hit[q] = __builtin_amdgcn_ballot_w64(key[q] == m);
+      // this lane's lowest expert holding m (none: all ones), then the row's lowest
+      uint32_t cand = 0xffffffffu;
 #pragma unroll
-      for (int q = 0; q < VPL; ++q) key[q] = qq == (uint32_t)q ? 0u : key[q];
-      if (r == j) my_e = ew;
+      for (int q = VPL - 1; q >= 0; --q) cand = __builtin_amdgcn_inverse_ballot_w64(hit[q]) ? (uint32_t)(e0 + q) : cand;
+      const uint32_t ew = row_min_u32<LPR>(cand);
+      const uint64_t owner = __builtin_amdgcn_ballot_w64(cand == ew);  // one lane per row
+      uint64_t seen = 0;
+#pragma unroll
+      for (int q = 0; q < VPL; ++q) {
+        const uint64_t first = hit[q] & owner & ~seen;
+        seen |= hit[q];
+        key[q] = __builtin_amdgcn_inverse_ballot_w64(first) ? 0u : key[q];
+      }
+      my_e = r == j ? ew : my_e;
     }
     __builtin_amdgcn_wave_barrier();
     const float my_p = r < k ? ps[wave][row][my_e] : 0.f;
-    const float sum = row_sum_f32(r < k ? fabsf(my_p) : 0.f);
+    const float sum = row_sum_f32<LPR>(r < k ? fabsf(my_p) : 0.f);
     const float denom = sum < 1e-12f ? 1e-12f : sum;  // NaN propagates
     if (t < T && r < k) {
       out_idx[t * k + r] = my_e;
@@ -340,15 +395,24 @@ extern "C" int zmoe_route_topk(const void* logits, int logits_dtype, int64_t T, 
     else launch(std::integral_constant<int, 16>{}, lt);
   };
   if (logits_dtype == ZMOE_DTYPE_BF16 && E % 8 == 0 && E <= 256 && k <= 16 && aligned16(logits)) {
-    // four tokens per wave, one per 16-lane row (8 or 16 experts per lane)
-    const int64_t rows_blocks = cdiv(cdiv(T, 4), 4);
-    const dim3 g4((unsigned)(rows_blocks < 2048 ? rows_blocks : 2048));
-    if (E <= 128)
-      hipLaunchKernelGGL(route_topk_rows_kernel<8>, g4, block, 0, as_stream(stream), (const uint16_t*)logits, T, E, k,
-                         expert_biases, round_probs_bf16, topk_idx, topk_weight, topk_prob);
-    else
-      hipLaunchKernelGGL(route_topk_rows_kernel<16>, g4, block, 0, as_stream(stream), (const uint16_t*)logits, T, E,
-                         k, expert_biases, round_probs_bf16, topk_idx, topk_weight, topk_prob);
+    // several tokens per wave, one per row of lanes; a wave ranks ~2 groups of rows
+    auto rows = [&](auto vpl, auto lpr, auto rb) {
+      constexpr int TPW = 64 / decltype(lpr)::value;
+      const int64_t blocks = cdiv(cdiv(T, TPW), 8);
+      hipLaunchKernelGGL((route_topk_rows_kernel<decltype(vpl)::value, decltype(lpr)::value, decltype(rb)::value>),
+                         dim3((unsigned)(blocks < 1024 ? blocks : 1024)), block, 0, as_stream(stream),
+                         (const uint16_t*)logits, T, E, k, expert_biases, topk_idx, topk_weight, topk_prob);
+    };
+    using I8 = std::integral_constant<int, 8>;
+    using I16 = std::integral_constant<int, 16>;
+    auto by_rb = [&](auto vpl, auto lpr) {
+      if (round_probs_bf16) rows(vpl, lpr, std::true_type{});
+      else rows(vpl, lpr, std::false_type{});
+    };
+    if (E <= 64 && k <= 8) by_rb(I8{}, I8{});         // 8 tokens per wave
+    else if (E <= 128 && k <= 8) by_rb(I16{}, I8{});
+    else if (E <= 128) by_rb(I8{}, I16{});            // 4 tokens per wave
+    else by_rb(I16{}, I16{});
     return check_launch("route_topk");
   }
   if (logits_dtype == ZMOE_DTYPE_BF16) by_width(uint16_t{});

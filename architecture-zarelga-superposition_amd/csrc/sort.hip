@@ -4,10 +4,10 @@
 //   1. tile histograms: each 256-thread block counts kSortTile slots into LDS
 //      (E+1 buckets; bucket E collects out-of-range ids) and writes them into a
 //      bucket-major table, table[e * ntiles + tile];
-//   2+3. for at most 256 tiles and 65536 counts (every C1-C5 shape), one
-//      scatter launch in which each block sums the table's bucket rows itself (all
-//      tiles, and the tiles before its own), scans the totals and ranks its tile as
-//      in 3 below; otherwise:
+//   2+3. for at most 256 tiles and 65536 counts (every C1-C5 shape), the counts are
+//      written as 16-bit values and one scatter launch follows, in which each block
+//      sums the table's bucket rows itself (all tiles, and the tiles before its own),
+//      scans the totals and ranks its tile as in 3 below; otherwise:
 //   2. one block turns the table into per-tile bucket bases: one wave per bucket
 //      reads the bucket's contiguous row of tile counts (16-byte loads), the row
 //      totals are scanned over the buckets in LDS, then each wave prefix-scans its
@@ -32,8 +32,9 @@ constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ int bucket_of(int64_t v, int E) { return (v >= 0 && v < E) ? (int)v : E; }
 
+template <typename CT>
 __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(const int64_t* __restrict__ idx, int64_t R,
-                                                                 int E, int ntiles, int32_t* __restrict__ table) {
+                                                                 int E, int ntiles, CT* __restrict__ table) {
   __shared__ int32_t h[kSortMaxE + 1];
   for (int e = threadIdx.x; e <= E; e += kSortThreads) h[e] = 0;
   __syncthreads();
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(const int64_t* 
     if (s < R) atomicAdd(&h[bucket_of(idx[s], E)], 1);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += kSortThreads) table[(int64_t)e * ntiles + blockIdx.x] = h[e];
+  for (int e = threadIdx.x; e <= E; e += kSortThreads) table[(int64_t)e * ntiles + blockIdx.x] = (CT)h[e];
 }
 
 // Sum (mode 0) or exclusive prefix plus `start` written back in place (mode 1) of one
@@ -204,10 +205,11 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     v[r] = s < R ? idx[s] : 0;
     key[r] = s < R ? bucket_of(v[r], E) : E + 1;  // lanes past R use an id no live lane has
   }
+  uint64_t peers[kWaveSlots / 64];  // lanes of this wave holding the same bucket, kept for pass 2
 #pragma unroll
   for (int r = 0; r < kWaveSlots / 64; ++r) {
-    const uint64_t peers = peer_mask(key[r], nbits);
-    if (key[r] <= E && __popcll(peers & lt_mask) == 0) wcount[wave][key[r]] += __popcll(peers);
+    peers[r] = peer_mask(key[r], nbits);
+    if (key[r] <= E && __popcll(peers[r] & lt_mask) == 0) wcount[wave][key[r]] += __popcll(peers[r]);
   }
   __syncthreads();
   // this wave's running position per bucket: tile base + counts of the earlier waves
@@ -220,13 +222,12 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 #pragma unroll
   for (int r = 0; r < kWaveSlots / 64; ++r) {
     const int64_t s = s0 + r * 64 + lane;
-    const uint64_t peers = peer_mask(key[r], nbits);
-    const int rank = __popcll(peers & lt_mask);
+    const int rank = __popcll(peers[r] & lt_mask);
     const bool live = key[r] <= E;
     int pos = 0;
     if (live) pos = wpos[wave][key[r]] + rank;
     __builtin_amdgcn_wave_barrier();
-    if (live && rank == 0) wpos[wave][key[r]] += __popcll(peers);
+    if (live && rank == 0) wpos[wave][key[r]] += __popcll(peers[r]);
     __builtin_amdgcn_wave_barrier();
     if (live) {
       sorted_expert[pos] = v[r];
@@ -238,28 +239,40 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 
 // Two-launch form of the sort for at most kFusedMaxTiles tiles and kFusedMaxTable counts
 // (every C1-C5 shape): the scatter blocks derive the bucket bases themselves, so the one-block scan
-// launch between histogram and scatter goes away. Block b reads the whole tile table
-// (L2-resident after the histogram launch; one wave per bucket row, 16-byte loads), sums
-// each bucket over all tiles and over the tiles before b, scans the bucket totals, and
-// ranks its tile as sort_scatter_kernel does, with eight waves of 128 slots.
+// launch between histogram and scatter goes away. Block b reads the whole tile table of
+// 16-bit counts (L2-resident after the histogram launch; 16 lanes per bucket row,
+// 16-byte loads), sums each bucket over all tiles and over the tiles before b, scans the
+// bucket totals, and ranks its tile as sort_scatter_kernel does, with eight waves of
+// 128 slots.
 constexpr int kFusedThreads = 512;
 constexpr int kFusedWaves = kFusedThreads / 64;
 constexpr int kFusedWaveSlots = kSortTile / kFusedWaves;
 constexpr int64_t kFusedMaxTable = 1 << 16;
 constexpr int kFusedMaxTiles = 256;  // R <= 262144 slots: one 16-byte piece of a bucket row per lane
 
-// Wave-wide sum of a 32-bit integer: DPP within rows of 16, then the four row sums.
-__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+// Inclusive prefix sum over the wave by DPP: shifts within rows of 16 lanes, then each
+// row's last lane broadcast into the rows after it.
+__device__ __forceinline__ int32_t wave_incl_scan_dpp(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// Sum over a row of 16 lanes by DPP; every lane of the row ends with it.
+__device__ __forceinline__ int32_t row16_sum_i32(int32_t v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
   v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
   v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);  // row_half_mirror
   v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true);  // row_mirror
-  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-         __builtin_amdgcn_readlane(v, 48);
+  return v;
 }
 
 __global__ __launch_bounds__(kFusedThreads) void sort_scatter_scan_kernel(
-    const int64_t* __restrict__ idx, int64_t R, int E, int ntiles, const int32_t* __restrict__ table,
+    const int64_t* __restrict__ idx, int64_t R, int E, int ntiles, const uint16_t* __restrict__ table,
     int64_t* __restrict__ offsets, int32_t* __restrict__ flag, int64_t* __restrict__ sorted_expert,
     int64_t* __restrict__ sorted_slot, int32_t* __restrict__ inverse) {
   // pass 1: per-wave bucket counts, turned in place into each wave's running positions
@@ -284,48 +297,77 @@ __global__ __launch_bounds__(kFusedThreads) void sort_scatter_scan_kernel(
     v[r] = s < R ? idx[s] : 0;
     key[r] = s < R ? bucket_of(v[r], E) : E + 1;  // lanes past R use an id no live lane has
   }
-  // bucket rows of the table: the sum over all tiles and over the tiles before this one.
-  // ntiles <= 256, so lane l holds tiles 4l .. 4l+3 of a row; a wave issues the loads of
-  // kRowBatch rows before reducing any, so their latencies overlap.
-  constexpr int kRowBatch = 17;  // E + 1 <= 136 rows in one batch of the eight waves
-  const bool vec = (ntiles & 3) == 0;
-  const int i0 = lane * 4;
-  for (int e0 = wave; e0 <= E; e0 += kRowBatch * kFusedWaves) {
-    int4 q[kRowBatch];
+  // bucket rows of the tile table (16-bit counts, bucket-major): each bucket's sum over all
+  // tiles and over the tiles before this one. A 16-lane group reads one row at a time, lane
+  // l tiles 16 l .. 16 l + 15 (ntiles <= 256; two 16-byte loads when rows are 16-byte
+  // aligned); a wave issues the loads of all its rows (kRowPasses per batch) before
+  // reducing any, by packed 16-bit adds and then DPP within the group. Rows go to the 32
+  // groups rotated by the block index, so that the blocks sharing an L2 read different
+  // rows at any one time.
+  {
+    constexpr int kRowPasses = 5;  // E + 1 <= 160 buckets in one batch (C3: 129)
+    const int grp = wave * 4 + (lane >> 4), gl = lane & 15;
+    const int t0 = gl * 16;
+    const bool vec = (ntiles & 7) == 0;
+    // the tiles before this one: all of lanes < gb, the first pb of lane gb (same for every row)
+    const int gb = b >> 4, pb = b & 15;
+    uint32_t pmask[8];  // 16-bit halves of lane gb's words that hold earlier tiles
 #pragma unroll
-    for (int j = 0; j < kRowBatch; ++j) {
-      const int e = e0 + j * kFusedWaves;
-      q[j] = make_int4(0, 0, 0, 0);
-      if (e <= E && i0 < ntiles) {
-        const int32_t* row = table + (int64_t)e * ntiles + i0;
-        if (vec) {
-          q[j] = *reinterpret_cast<const int4*>(row);
-        } else {
-          q[j].x = row[0];
-          q[j].y = i0 + 1 < ntiles ? row[1] : 0;
-          q[j].z = i0 + 2 < ntiles ? row[2] : 0;
-          q[j].w = i0 + 3 < ntiles ? row[3] : 0;
+    for (int j = 0; j < 8; ++j) pmask[j] = 2 * j + 1 < pb ? 0xffffffffu : (2 * j < pb ? 0x0000ffffu : 0u);
+    for (int r0 = 0; r0 <= E; r0 += 32 * kRowPasses) {
+      uint32_t w[kRowPasses][8];
+      int ev[kRowPasses];
+#pragma unroll
+      for (int u = 0; u < kRowPasses; ++u) {
+        const int e = r0 + u * 32 + ((grp + b) & 31);
+        ev[u] = e;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[u][j] = 0;
+        if (e <= E && t0 < ntiles) {
+          const uint16_t* row = table + (int64_t)e * ntiles + t0;
+          if (vec) {
+            const uint4 lo = *reinterpret_cast<const uint4*>(row);
+            w[u][0] = lo.x; w[u][1] = lo.y; w[u][2] = lo.z; w[u][3] = lo.w;
+            if (t0 + 8 < ntiles) {
+              const uint4 hi = *reinterpret_cast<const uint4*>(row + 8);
+              w[u][4] = hi.x; w[u][5] = hi.y; w[u][6] = hi.z; w[u][7] = hi.w;
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t a0 = t0 + 2 * j < ntiles ? row[2 * j] : 0u;
+              const uint32_t a1 = t0 + 2 * j + 1 < ntiles ? row[2 * j + 1] : 0u;
+              w[u][j] = a0 | (a1 << 16);
+            }
+          }
         }
       }
-    }
 #pragma unroll
-    for (int j = 0; j < kRowBatch; ++j) {
-      const int e = e0 + j * kFusedWaves;
-      const int32_t all = q[j].x + q[j].y + q[j].z + q[j].w;
-      const int32_t before = (i0 < b ? q[j].x : 0) + (i0 + 1 < b ? q[j].y : 0) + (i0 + 2 < b ? q[j].z : 0) +
-                             (i0 + 3 < b ? q[j].w : 0);
-      const int32_t sa = wave_sum_i32(all), sb = wave_sum_i32(before);
-      if (lane == 0 && e <= E) {
-        tot[e] = sa;
-        base[e] = sb;
+      for (int u = 0; u < kRowPasses; ++u) {
+        // packed sums: each half adds at most 8 counts of <= 1024, so no carry crosses halves
+        uint32_t sa = 0, sp = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sa += w[u][j];
+          sp += w[u][j] & pmask[j];
+        }
+        const int32_t all = (int32_t)((sa & 0xffffu) + (sa >> 16));
+        const int32_t part = (int32_t)((sp & 0xffffu) + (sp >> 16));
+        int32_t bef = gl < gb ? all : (gl == gb ? part : 0);
+        const int32_t ta = row16_sum_i32(all), tb = row16_sum_i32(bef);
+        if (gl == 0 && ev[u] <= E) {
+          tot[ev[u]] = ta;
+          base[ev[u]] = tb;
+        }
       }
     }
   }
   __syncthreads();  // wcount zeroed; tot and base complete
+  uint64_t peers[kFusedWaveSlots / 64];  // lanes of this wave holding the same bucket, kept for pass 2
 #pragma unroll
   for (int r = 0; r < kFusedWaveSlots / 64; ++r) {
-    const uint64_t peers = peer_mask(key[r], nbits);
-    if (key[r] <= E && __popcll(peers & lt_mask) == 0) wcount[wave][key[r]] += __popcll(peers);
+    peers[r] = peer_mask(key[r], nbits);
+    if (key[r] <= E && __popcll(peers[r] & lt_mask) == 0) wcount[wave][key[r]] += __popcll(peers[r]);
   }
   // exclusive scan of the bucket totals: thread t owns buckets t * per .. t * per + per - 1
   const int per = (E + 1 + kFusedThreads - 1) / kFusedThreads;  // <= 3
@@ -333,12 +375,7 @@ __global__ __launch_bounds__(kFusedThreads) void sort_scatter_scan_kernel(
   int32_t mine = 0;
   for (int u = 0; u < per; ++u)
     if (eb + u <= E) mine += tot[eb + u];
-  int32_t inc = mine;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int32_t t = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += t;
-  }
+  const int32_t inc = wave_incl_scan_dpp(mine);
   if (lane == 63) part[wave] = inc;
   __syncthreads();  // pass-1 counts and the wave totals of the scan are in LDS
   int32_t run = inc - mine;
@@ -368,13 +405,12 @@ __global__ __launch_bounds__(kFusedThreads) void sort_scatter_scan_kernel(
 #pragma unroll
   for (int r = 0; r < kFusedWaveSlots / 64; ++r) {
     const int64_t s = s0 + r * 64 + lane;
-    const uint64_t peers = peer_mask(key[r], nbits);
-    const int rank = __popcll(peers & lt_mask);
+    const int rank = __popcll(peers[r] & lt_mask);
     const bool live = key[r] <= E;
     int pos = 0;
     if (live) pos = wpos_row[key[r]] + rank;
     __builtin_amdgcn_wave_barrier();
-    if (live && rank == 0) wpos_row[key[r]] += __popcll(peers);
+    if (live && rank == 0) wpos_row[key[r]] += __popcll(peers[r]);
     __builtin_amdgcn_wave_barrier();
     if (live) {
       sorted_expert[pos] = v[r];
@@ -458,13 +494,18 @@ int sort_launch(const int64_t* expert_idxs, int64_t R, int E, int64_t* sorted_ex
                 int64_t* sorted_scattered_idxs, int64_t* expert_offsets, int32_t* inverse, int32_t* flag,
                 int32_t* table, hipStream_t s, const char* name) {
   const int ntiles = (int)cdiv(R, kSortTile);
-  if (ntiles > 0)
-    hipLaunchKernelGGL(sort_hist_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles, table);
   if (ntiles > 0 && ntiles <= kFusedMaxTiles && (int64_t)(E + 1) * ntiles <= kFusedMaxTable) {
+    // tile counts (<= kSortTile) as 16-bit values
+    uint16_t* table16 = reinterpret_cast<uint16_t*>(table);
+    hipLaunchKernelGGL(sort_hist_kernel<uint16_t>, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles,
+                       table16);
     hipLaunchKernelGGL(sort_scatter_scan_kernel, dim3(ntiles), dim3(kFusedThreads), 0, s, expert_idxs, R, E,
-                       ntiles, table, expert_offsets, flag, sorted_expert_idxs, sorted_scattered_idxs, inverse);
+                       ntiles, table16, expert_offsets, flag, sorted_expert_idxs, sorted_scattered_idxs, inverse);
     return check_launch(name);
   }
+  if (ntiles > 0)
+    hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles,
+                       table);
   hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, table, ntiles, E, expert_offsets, flag);
   if (ntiles > 0)
     hipLaunchKernelGGL(sort_scatter_kernel, dim3(ntiles), dim3(kSortThreads), 0, s, expert_idxs, R, E, ntiles,

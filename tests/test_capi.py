@@ -106,3 +106,29 @@ def test_newton_schulz_workspace_is_sized_for_one_pass():
     c4 = lib.zmoe_newton_schulz5_workspace_bytes(256, 4096, 7168)
     assert c4 == lib.zmoe_newton_schulz5_workspace_bytes(36, 4096, 7168)
     assert lib.zmoe_newton_schulz5_workspace_bytes(1, 65536, 65536) == 0  # one matrix above 2 GiB
+
+
+def test_sigmoid_table_matches_oracle(tmp_path):
+    """The build's routing-probability table (kSigmoidBf16, one entry per bf16 logit) equals
+    the oracle's bf16(fp32(sigmoid in float64)) for all 65536 bit patterns, NaNs included."""
+    import sys
+
+    import numpy as np
+
+    import oracle as O
+
+    sys.path.insert(0, os.path.join(ROOT, "architecture-zarelga-superposition_amd"))
+    import build_lib
+
+    path = tmp_path / "table.inc"
+    build_lib.write_sigmoid_table(str(path))
+    body = path.read_text().split("\n", 1)[1]
+    bits = np.array([int(v, 16) for v in body.replace(",", " ").split()], dtype=np.uint32)
+    assert bits.size == 65536
+    with np.errstate(all="ignore"):
+        z = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+        ref = O.bf16_round(O.sigmoid_f32(z))
+    got = (bits << 16).view(np.float32)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
