@@ -450,39 +450,58 @@ def main(argv=None):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+
+    def launch_times(nsteps):
+        """Per-launch kernel times from HIP events recorded on the launch stream."""
+        kernels = {}
+        for name in GEMM_OPS:
+            durs = profiling.durations_ms(name)
+            if not durs:
+                continue
+            per_step = len(durs) // nsteps
+            for j in range(per_step):
+                ds = durs[j::per_step]
+                fl = gemm_flops(name, j, T, d, k, f)
+                avg = sum(ds) / len(ds)
+                kernels[f"{name}#{j}"] = dict(avg_ms=avg, tflops=fl / (avg * 1e-3) / 1e12, flops=fl)
+        for name in ROW_OPS:
+            durs = profiling.durations_ms(name)
+            if not durs:
+                continue
+            avg = sum(durs) / len(durs)
+            by = row_bytes(name, T, d, E, k, f)
+            kernels[name] = dict(avg_ms=avg, gbs=by / (avg * 1e-3) / 1e9, bytes=by)
+        return kernels
+
+    # the per-launch breakdown (every GEMM and row launch bracketed by events) comes from an
+    # untimed pass; the timed steps carry events around the roofline kernel's op only, so the
+    # step time is not inflated by ~20 event pairs per step (~1% at C3)
+    nbreak = max(3, args.steps // 2)
     profiling.reset()
     profiling.enable(*GEMM_OPS, *ROW_OPS)
+    for _ in range(nbreak):
+        step()
+    torch.cuda.synchronize()
+    kernels = launch_times(nbreak)
+    profiling.disable()
+    gemm = {n: v for n, v in kernels.items() if "tflops" in v}
+    dom_name = max(gemm, key=lambda n: gemm[n]["avg_ms"])
+
+    profiling.reset()
+    profiling.enable(dom_name.split("#")[0])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    timed = launch_times(args.steps)
     profiling.disable()
     ms_per_step = 1000.0 * elapsed / args.steps
     tokens_per_s = T / (ms_per_step / 1000.0)
+    kernels[dom_name] = timed[dom_name]  # the roofline kernel as timed inside the timed region
 
-    # per-launch kernel times from HIP events recorded on the launch stream
-    kernels = {}
-    for name in GEMM_OPS:
-        durs = profiling.durations_ms(name)
-        if not durs:
-            continue
-        per_step = len(durs) // args.steps
-        for j in range(per_step):
-            ds = durs[j::per_step]
-            fl = gemm_flops(name, j, T, d, k, f)
-            avg = sum(ds) / len(ds)
-            kernels[f"{name}#{j}"] = dict(avg_ms=avg, tflops=fl / (avg * 1e-3) / 1e12, flops=fl)
-    for name in ROW_OPS:
-        durs = profiling.durations_ms(name)
-        if not durs:
-            continue
-        avg = sum(durs) / len(durs)
-        by = row_bytes(name, T, d, E, k, f)
-        kernels[name] = dict(avg_ms=avg, gbs=by / (avg * 1e-3) / 1e9, bytes=by)
     gemm = {n: v for n, v in kernels.items() if "tflops" in v}
-    dom_name = max(gemm, key=lambda n: gemm[n]["avg_ms"])
     dom = gemm[dom_name]
     gemm_ms = sum(v["avg_ms"] for v in gemm.values())
     gemm_flops_total = sum(v["flops"] for v in gemm.values())
