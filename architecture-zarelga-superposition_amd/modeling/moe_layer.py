@@ -77,10 +77,13 @@ class _FusedMoELayer(torch.autograd.Function):
         ctx.save_for_backward(x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s, pad_rows)
         ctx.k, ctx.E, ctx.fs = k, E, fs
         ctx.mark_non_differentiable(idx, off)
+        ctx.set_materialize_grads(False)  # no zero-filled grads for idx and off (two fill launches)
         return out, idx, off
 
     @staticmethod
     def backward(ctx, dout, d_idx, d_off):
+        if dout is None:  # out took no part in the loss
+            return (None,) * 12
         x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s, pad_rows = ctx.saved_tensors
         k, E, fs = ctx.k, ctx.E, ctx.fs
         need = ctx.needs_input_grad

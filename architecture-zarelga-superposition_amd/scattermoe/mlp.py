@@ -52,10 +52,13 @@ class GLUExpertsFunction(torch.autograd.Function):
         ctx.k = k
         ctx.num_experts = num_experts
         ctx.mark_non_differentiable(off)
+        ctx.set_materialize_grads(False)  # no zero-filled grad for off
         return out, off
 
     @staticmethod
     def backward(ctx, dout, d_off):
+        if dout is None:  # out took no part in the loss
+            return (None,) * 10
         x, gates, W1, W2, se, ss, off, inv, H, A, Y, pad_rows = ctx.saved_tensors
         k, E = ctx.k, ctx.num_experts
         dout = dout.to(x.dtype)
