@@ -28,7 +28,10 @@ def _route_case(T, E, k, seed, dtype, bias_std, ties=False, nan=False):
                                    (33, 5, 5), (16, 70, 1),
                                    # bf16 four-tokens-per-wave kernel: partial 16-expert lanes, one
                                    # occupied lane, k = 16, token counts not divisible by 4
-                                   (513, 200, 8), (99, 136, 16), (50, 8, 8), (1001, 120, 3), (64, 256, 16)])
+                                   (513, 200, 8), (99, 136, 16), (50, 8, 8), (1001, 120, 3), (64, 256, 16),
+                                   # eight tokens per wave (8-lane rows) for E <= 128 and k <= 8, 16-lane
+                                   # rows of 8 experts for k in 9..16 at E <= 128
+                                   (301, 128, 12), (77, 64, 16), (263, 16, 5)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_route_topk_bit_exact(hip_device, T, E, k, dtype):
     logits, bias = _route_case(T, E, k, seed=T + E, dtype=dtype, bias_std=0.1, ties=True, nan=T > 3)
@@ -39,6 +42,21 @@ def test_route_topk_bit_exact(hip_device, T, E, k, dtype):
     ridx, rw, rp = O.route_topk(logits.float().numpy(), bias.numpy(), k, round_probs_bf16=rb)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
     np.testing.assert_array_equal(p.cpu().numpy(), rp)  # sigmoid evaluated identically (f64, one rounding)
+    ok = ~np.isnan(rw).any(axis=1)
+    assert_close(w.cpu().numpy()[ok], rw[ok], rtol=1e-6, atol=1e-7, what="topk_weight")
+
+
+@pytest.mark.parametrize("T,E,k", [(777, 128, 8), (301, 128, 12), (130, 64, 8), (99, 200, 8)])
+def test_route_topk_bf16_logits_fp32_probs(hip_device, T, E, k):
+    """bf16 logits with probabilities kept in fp32 (round_probs_bf16=False): the several-tokens-per-wave
+    kernels evaluate the sigmoid in double instead of reading the bf16 table."""
+    logits, bias = _route_case(T, E, k, seed=3 * T + E, dtype=torch.bfloat16, bias_std=0.1, ties=True, nan=True)
+    from zmoe import ops
+
+    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), k, round_probs_bf16=False)
+    ridx, rw, rp = O.route_topk(logits.float().numpy(), bias.numpy(), k, round_probs_bf16=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)
     ok = ~np.isnan(rw).any(axis=1)
     assert_close(w.cpu().numpy()[ok], rw[ok], rtol=1e-6, atol=1e-7, what="topk_weight")
 
