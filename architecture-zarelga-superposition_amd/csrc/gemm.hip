@@ -374,12 +374,18 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
     const int tiles_e = ntl[q] * p.n_tiles;
     if (logical >= run && logical < run + tiles_e) {  // (ntl[q] is 0 past the last expert)
       const int loc = logical - run;
-      const int mt = p.n_major ? loc % ntl[q] : loc / p.n_tiles;
+      // serpentine: the inner index runs backwards on odd outer steps, so consecutive
+      // tiles across a turn share an operand block too (0.3-0.8% per launch)
+      const int outer = p.n_major ? loc / ntl[q] : loc / p.n_tiles;
+      const int inner = p.n_major ? loc % ntl[q] : loc % p.n_tiles;
+      const int ninner = p.n_major ? ntl[q] : p.n_tiles;
+      const int in2 = (outer & 1) ? ninner - 1 - inner : inner;
+      const int mt = p.n_major ? in2 : outer;
       const int64_t r0 = ebeg[q] + (int64_t)mt * BM;
       found[0] = e0 + q;
       found[1] = r0;
       found[2] = min((int64_t)BM, eend[q] - r0);
-      found[3] = p.n_major ? loc / ntl[q] : loc % p.n_tiles;
+      found[3] = p.n_major ? outer : in2;
     }
     run += tiles_e;
   }
@@ -1571,8 +1577,13 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   if (logical < 0) return;
   const int e = logical / per_e;
   const int rem = logical % per_e;
-  const int mt = p.n_major ? rem % p.m_tiles : rem / p.n_tiles;
-  const int nt = p.n_major ? rem / p.m_tiles : rem % p.n_tiles;
+  // tiles of the expert in serpentine order (the inner index runs backwards on odd outer steps)
+  const int w_outer = p.n_major ? rem / p.m_tiles : rem / p.n_tiles;
+  const int w_inner0 = p.n_major ? rem % p.m_tiles : rem % p.n_tiles;
+  const int w_ninner = p.n_major ? p.m_tiles : p.n_tiles;
+  const int w_inner = (w_outer & 1) ? w_ninner - 1 - w_inner0 : w_inner0;
+  const int mt = p.n_major ? w_inner : w_outer;
+  const int nt = p.n_major ? w_outer : w_inner;
   const int64_t r_begin = e ? wgrad_rows_end(p, e - 1) : 0;
   const int64_t r_end = wgrad_rows_end(p, e);
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
