@@ -53,14 +53,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # they were measured on (TRAFFIC_C3_GEMM_SHA256, the sha256 of csrc/gemm.hip): when
 # that file differs, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
-TRAFFIC_C3_GEMM_SHA256 = "aaf5da2af51ebff818ca84916cd5b86352097c4d69c0d368c11b0711d06fef1e"
+TRAFFIC_C3_GEMM_SHA256 = "53f53982be17121b6aa1917962978915650cec7655d01046ee679654bf1910ce"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6101736234,
-    "scatter2scatter#0": 2940665621,
-    "glu_w2_backward_dh#0": 2306495232,
-    "scatter2scatter#1": 5928163925,
-    "group_bwd_w#0": 2264993685,
-    "group_bwd_w#1": 3840553834,
+    "glu_w1_forward#0": 6098145322,
+    "scatter2scatter#0": 2913306304,
+    "glu_w2_backward_dh#0": 2340300714,
+    "scatter2scatter#1": 5856118656,
+    "group_bwd_w#0": 2240682816,
+    "group_bwd_w#1": 3844628586,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
