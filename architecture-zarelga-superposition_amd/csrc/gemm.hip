@@ -1807,6 +1807,11 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   if (rc) return rc;
   p.m_tiles = (int)cdiv(p.Ndy, BM);
   p.n_tiles = (int)cdiv(p.Kx, BN);
+  // n-tiles outer (tiles sharing a gathered X block together) pays only while an XCD's 32
+  // resident tiles span most of X's column blocks: dW1 at C3 (6 x 8 tiles per expert) 2%
+  // faster, at C4 (16 x 28) 8% slower than m-tiles outer, which then keeps the gathered
+  // rows' column blocks together in time
+  if (p.m_tiles * p.n_tiles > 64) p.n_major = 0;
   int64_t total = (int64_t)p.E * p.m_tiles * p.n_tiles;
   total = cdiv(total, kXcds) * kXcds;
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
@@ -2387,8 +2392,8 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   p.x_rows = x_gather_idxs;
   p.x_div = x_gather_div;
   p.x_div_shift = (x_gather_div > 0 && (x_gather_div & (x_gather_div - 1)) == 0) ? __builtin_ctz(x_gather_div) : -1;
-  // the tiles sharing a gathered X block run together (dW1 at C3: 2% faster than m-tiles
-  // outer; with DY gathered instead, m-tiles outer is 3% faster)
+  // the tiles sharing a gathered X block run together when an expert's tiles are few (see
+  // launch_wgrad_kernel); with DY gathered instead, m-tiles outer
   p.n_major = x_gather_idxs != nullptr ? 1 : 0;
   p.dw = DWt;
   p.offsets = expert_offsets;
