@@ -53,14 +53,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # they were measured on (TRAFFIC_C3_GEMM_SHA256, the sha256 of csrc/gemm.hip): when
 # that file differs, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
-TRAFFIC_C3_GEMM_SHA256 = "53f53982be17121b6aa1917962978915650cec7655d01046ee679654bf1910ce"
+TRAFFIC_C3_GEMM_SHA256 = "f771459624765c1e26052fc22074c882a7318af3f25271d05c50312d056d9905"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6098145322,
-    "scatter2scatter#0": 2913306304,
-    "glu_w2_backward_dh#0": 2340300714,
-    "scatter2scatter#1": 5856118656,
-    "group_bwd_w#0": 2240682816,
-    "group_bwd_w#1": 3844628586,
+    "glu_w1_forward#0": 5933937706,
+    "scatter2scatter#0": 2886102314,
+    "glu_w2_backward_dh#0": 2314637760,
+    "scatter2scatter#1": 5737438848,
+    "group_bwd_w#0": 2251489920,
+    "group_bwd_w#1": 3818416149,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
