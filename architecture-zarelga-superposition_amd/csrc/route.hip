@@ -1,10 +1,13 @@
 // Aux-loss-free sigmoid routing (modeling/moe_gate.py:27-34), its backward, and
 // the aux-loss-free bias update (main.py:161-175).
 //
-// One 64-lane wave owns one token row. Lane l holds experts l, l+64, ... so a
-// row of E <= 1024 scores sits in registers; k rounds of a wave-wide max
-// (xor-shuffle butterfly over packed (score, expert) keys) pick the slots in the
-// contract order (score desc, expert asc, NaN first).
+// Slots come in the contract order (score desc, expert asc, NaN first), picked in
+// k rounds of a max over the token's score keys. For bf16 logits with E % 8 == 0,
+// E <= 256 and k <= 16 a wave routes 4 or 8 tokens at once, one per row of 16 or 8
+// lanes, each lane holding 8 or 16 consecutive experts, with bf16 probabilities
+// read from a table the build writes (route_topk_rows_kernel). Otherwise one
+// 64-lane wave owns one token row: lane l holds experts l, l+64, ... (E <= 1024)
+// and each round is a wave-wide max (route_topk_kernel).
 #include <type_traits>
 
 #include "zmoe_internal.h"
