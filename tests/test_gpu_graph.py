@@ -68,3 +68,44 @@ def test_forward_graph_replays_match_eager(hip_device, T, d, E, k, f):
         graph.replay()
         torch.cuda.synchronize(hip_device)
         assert torch.equal(out, want), "replay on a new input differs from eager"
+
+
+# the training step (forward + backward into static .grad tensors): 128 x 128 and 256 x 256
+# tiles, the small-expert weight-grad split and the shared expert's split-K weight grads
+@pytest.mark.parametrize("T,d,E,k,f", [(512, 256, 16, 4, 128), (2048, 512, 8, 2, 256)])
+def test_train_step_graph_replays_match_eager(hip_device, T, d, E, k, f):
+    layer, x0 = _layer(T, d, E, k, f, hip_device, seed=T + 1)
+    x = x0.clone().requires_grad_(True)
+    dout = torch.randn(x.shape, generator=torch.Generator(device=hip_device).manual_seed(3),
+                       device=hip_device).to(x.dtype)
+    params = [p for p in layer.parameters() if p.requires_grad]
+    leaves = [x] + params
+
+    def eager_grads():
+        out, _ = layer(x)
+        return [out.detach().clone()] + [g.clone() for g in torch.autograd.grad(out, leaves, dout)]
+
+    side = torch.cuda.Stream(hip_device)
+    side.wait_stream(torch.cuda.current_stream(hip_device))
+    with torch.cuda.stream(side):  # warm up off the capture stream
+        for _ in range(2):
+            eager_grads()
+    torch.cuda.current_stream(hip_device).wait_stream(side)
+    ref = eager_grads()
+    for t in leaves:
+        t.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, _ = layer(x)
+        out.backward(dout)
+    names = ["out", "dx"] + [n for n, p in layer.named_parameters() if p.requires_grad]
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize(hip_device)
+        got = [out] + [t.grad for t in leaves]
+        for name, g, want in zip(names, got, ref):
+            assert g is not None and torch.equal(g, want), f"replay {r}: {name} differs from eager"
+        again = eager_grads()
+        torch.cuda.synchronize(hip_device)
+        for name, g, want in zip(names, again, ref):
+            assert torch.equal(g, want), f"eager run after replay {r}: {name} differs"
