@@ -49,10 +49,11 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # HBM-side bytes per launch at C3 (L2 -> memory fabric reads and writes), from two
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over this script, each scaled by what
 # the same counter reads for a plain 1 GiB copy (reads x 2.000, writes x 1.000); the
-# commands and raw counts are in TRAFFIC_C3_PROFILE. They hold for the GEMM source
-# they were measured on (TRAFFIC_C3_GEMM_SHA256, the sha256 of csrc/gemm.hip): when
-# that file differs, the line reports traffic null and says why.
+# commands and raw counts are in TRAFFIC_C3_PROFILE. They hold for the GEMM sources
+# they were measured on (TRAFFIC_C3_GEMM_SHA256, the sha256 of TRAFFIC_C3_SOURCES read
+# one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
+TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
 TRAFFIC_C3_GEMM_SHA256 = "f771459624765c1e26052fc22074c882a7318af3f25271d05c50312d056d9905"
 TRAFFIC_C3 = {
     "glu_w1_forward#0": 5933937706,
@@ -224,12 +225,15 @@ def traffic_c3(name):
     """(bytes, source note) of the dominant launch's measured HBM traffic at C3."""
     import hashlib
 
-    path = os.path.join(PKG_ROOT, "csrc", "gemm.hip")
-    with open(path, "rb") as fh:
-        sha = hashlib.sha256(fh.read()).hexdigest()
+    h = hashlib.sha256()
+    for src in TRAFFIC_C3_SOURCES:
+        with open(os.path.join(PKG_ROOT, "csrc", src), "rb") as fh:
+            h.update(fh.read())
+    sha = h.hexdigest()
+    what = " + ".join("csrc/" + s for s in TRAFFIC_C3_SOURCES)
     if TRAFFIC_C3_GEMM_SHA256 is None or sha != TRAFFIC_C3_GEMM_SHA256:
-        return None, f"not measured for this csrc/gemm.hip (sha256 {sha[:12]}); {TRAFFIC_C3_PROFILE} is older"
-    return TRAFFIC_C3.get(name), f"{TRAFFIC_C3_PROFILE} (csrc/gemm.hip sha256 {sha[:12]})"
+        return None, f"not measured for this {what} (sha256 {sha[:12]}); {TRAFFIC_C3_PROFILE} is older"
+    return TRAFFIC_C3.get(name), f"{TRAFFIC_C3_PROFILE} ({what} sha256 {sha[:12]})"
 
 
 COPY_PROBE_BYTES = 1 << 30  # device-to-device copy used to calibrate FETCH_SIZE / WRITE_SIZE
