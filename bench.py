@@ -54,14 +54,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "f771459624765c1e26052fc22074c882a7318af3f25271d05c50312d056d9905"
+TRAFFIC_C3_GEMM_SHA256 = "b6ec5e941d32c260773030bf86d88c223c17dadb3f9707cbc584262dd1f59859"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 5933937706,
-    "scatter2scatter#0": 2886102314,
-    "glu_w2_backward_dh#0": 2314637760,
-    "scatter2scatter#1": 5737438848,
-    "group_bwd_w#0": 2251489920,
-    "group_bwd_w#1": 3818416149,
+    "glu_w1_forward#0": 5990696032,
+    "scatter2scatter#0": 2909888021,
+    "glu_w2_backward_dh#0": 2339320341,
+    "scatter2scatter#1": 5735295296,
+    "group_bwd_w#0": 2256839509,
+    "group_bwd_w#1": 3857995498,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
