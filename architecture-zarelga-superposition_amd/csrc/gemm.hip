@@ -252,11 +252,18 @@ __device__ __forceinline__ int xcd_logical_tile(int total) {
 // skewed: 2.4x the mean at C4's Zipf(1.1) popularity, dW1 + dW2 13.0 -> 10.1 ms with
 // slabs. A slab still keeps 32 concurrent tiles of one expert on one XCD (same time as
 // the contiguous ranges at C3; slabs of 8 time the same at C4, of 1 are 3-11% slower at
-// C3). The launch rounds its grid up to whole slabs on every XCD.
+// C3). A launch of at most 8 slabs (the dense split-K grads) takes one slab of
+// ceil(total / 8) tiles per XCD, i.e. the contiguous ranges, so no XCD sits idle. The
+// launch rounds its grid up to whole slabs on every XCD.
 constexpr int kSlab = 32;
+__host__ __device__ __forceinline__ int wgrad_slab(int64_t total) {
+  const int64_t per_xcd = (total + kXcds - 1) / kXcds;
+  return per_xcd < kSlab ? (int)(per_xcd > 0 ? per_xcd : 1) : kSlab;
+}
 __device__ __forceinline__ int wgrad_logical_tile(int total) {
+  const int slab = wgrad_slab(total);
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
-  const int logical = ((slot / kSlab) * kXcds + xcd) * kSlab + slot % kSlab;
+  const int logical = ((slot / slab) * kXcds + xcd) * slab + slot % slab;
   return logical < total ? logical : -1;
 }
 
@@ -1828,7 +1835,8 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   // rows' column blocks together in time
   if (p.m_tiles * p.n_tiles > 64) p.n_major = 0;
   int64_t total = (int64_t)p.E * p.m_tiles * p.n_tiles;
-  total = cdiv(total, kXcds * kSlab) * kXcds * kSlab;  // whole slabs on every XCD (wgrad_logical_tile)
+  const int slab = wgrad_slab(total);
+  total = cdiv(total, (int64_t)kXcds * slab) * kXcds * slab;  // whole slabs on every XCD (wgrad_logical_tile)
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads), lds, s, p);
   return check_launch("grouped wgrad kernel");
