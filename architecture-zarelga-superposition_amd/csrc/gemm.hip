@@ -245,23 +245,23 @@ __device__ __forceinline__ int xcd_logical_tile(int total) {
   return (slot < chunk && logical < total) ? logical : -1;
 }
 
-// Logical tile of a weight-grad launch: slabs of kSlab consecutive tiles (the workgroups
-// one XCD holds at once) dealt to the XCDs in turn. A weight-grad tile's cost grows with
-// its expert's rows, so xcd_logical_tile's contiguous per-XCD ranges (equal tile counts)
-// leave the XCD that holds a popular expert with most of the work when routing is
-// skewed: 2.4x the mean at C4's Zipf(1.1) popularity, dW1 + dW2 13.0 -> 10.1 ms with
-// slabs. A slab still keeps 32 concurrent tiles of one expert on one XCD (same time as
-// the contiguous ranges at C3; slabs of 8 time the same at C4, of 1 are 3-11% slower at
-// C3). A launch of at most 8 slabs (the dense split-K grads) takes one slab of
-// ceil(total / 8) tiles per XCD, i.e. the contiguous ranges, so no XCD sits idle. The
-// launch rounds its grid up to whole slabs on every XCD.
+// Logical tile under slabs of kSlab consecutive tiles (the workgroups one XCD holds at
+// once) dealt to the XCDs in turn. The weight-grad launches always map this way: a
+// weight-grad tile's cost grows with its expert's rows, so xcd_logical_tile's contiguous
+// per-XCD ranges (equal tile counts) leave the XCD that holds a popular expert with most
+// of the work when routing is skewed: 2.4x the mean at C4's Zipf(1.1) popularity, dW1 +
+// dW2 13.0 -> 10.1 ms with slabs. A slab still keeps 32 concurrent tiles of one expert on
+// one XCD (same time as the contiguous ranges at C3; slabs of 8 time the same at C4, of 1
+// are 3-11% slower at C3). A launch of at most 8 slabs (the dense split-K grads) takes one
+// slab of ceil(total / 8) tiles per XCD, i.e. the contiguous ranges, so no XCD sits idle.
+// The launches round their grids up to whole slabs on every XCD.
 constexpr int kSlab = 32;
-__host__ __device__ __forceinline__ int wgrad_slab(int64_t total) {
+__host__ __device__ __forceinline__ int slab_size(int64_t total) {
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   return per_xcd < kSlab ? (int)(per_xcd > 0 ? per_xcd : 1) : kSlab;
 }
-__device__ __forceinline__ int wgrad_logical_tile(int total) {
-  const int slab = wgrad_slab(total);
+__device__ __forceinline__ int slab_logical_tile(int total) {
+  const int slab = slab_size(total);
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
   const int logical = ((slot / slab) * kXcds + xcd) * slab + slot % slab;
   return logical < total ? logical : -1;
@@ -385,11 +385,24 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
       local += ntl[q];
     }
   }
+  // experts whose rows fit one m-tile, per wave (ballots: no LDS round trips)
+  int single = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) single += __builtin_popcountll(__builtin_amdgcn_ballot_w64(ntl[q] == 1));
+  int* single_w = tmp + 16;  // per-wave counts; the scan's barrier orders them before the reads
+  if ((threadIdx.x & 63) == 0) single_w[threadIdx.x >> 6] = single;
   // expert e owns ntl_e * n_tiles consecutive logical tiles, its m-tiles outer (tiles
   // sharing A rows run together) or its n-tiles outer (tiles sharing B columns do)
   int ttiles;
   int run = block_exclusive_scan<NT>(local * p.n_tiles, tmp, &ttiles);
-  const int logical = xcd_logical_tile(ttiles);
+  int singles = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) singles += single_w[w];
+  // Skewed routing, with over a quarter of the experts in a single m-tile: their tiles
+  // stream a whole weight block for a few rows (HBM-bound) beside the compute-bound tiles
+  // of the popular experts, and slabs give every XCD its share of both (C4: W1 forward 6%,
+  // W1 input grad 4% faster). Otherwise each XCD keeps whole experts (1% faster at C3).
+  const int logical = 4 * singles > p.E ? slab_logical_tile(ttiles) : xcd_logical_tile(ttiles);
   if (logical < 0) return false;  // uniform per workgroup
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -688,7 +701,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_wgrad_kernel(WgradParams
   constexpr int MI = WM / 32, NI = WN / 32;
 
   const int per_e = p.m_tiles * p.n_tiles;
-  const int logical = wgrad_logical_tile(p.E * per_e);
+  const int logical = slab_logical_tile(p.E * per_e);
   if (logical < 0) return;
   const int e = logical / per_e;
   const int rem = logical % per_e;
@@ -1595,7 +1608,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   constexpr int kStage = (BM + BN) * KS * 2;
 
   const int per_e = p.m_tiles * p.n_tiles;
-  const int logical = wgrad_logical_tile(p.E * per_e);
+  const int logical = slab_logical_tile(p.E * per_e);
   if (logical < 0) return;
   const int e = logical / per_e;
   const int rem = logical % per_e;
@@ -1798,7 +1811,7 @@ int launch_rows_kernel(K kern, int lds, int BM, const RowsParams& p, int64_t R, 
   if (rc) return rc;
   const int64_t mt_bound = cdiv(R, BM) + (R < p.E ? R : p.E);
   int64_t total = mt_bound * p.n_tiles;
-  total = cdiv(total, kXcds) * kXcds;
+  total = cdiv(total, (int64_t)kXcds * kSlab) * kXcds * kSlab;  // covers either mapping (decode_rows_tile)
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "grouped gemm: too many tiles");
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads), lds, s, p);
   return check_launch("grouped rows kernel");
@@ -1835,8 +1848,8 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   // rows' column blocks together in time
   if (p.m_tiles * p.n_tiles > 64) p.n_major = 0;
   int64_t total = (int64_t)p.E * p.m_tiles * p.n_tiles;
-  const int slab = wgrad_slab(total);
-  total = cdiv(total, (int64_t)kXcds * slab) * kXcds * slab;  // whole slabs on every XCD (wgrad_logical_tile)
+  const int slab = slab_size(total);
+  total = cdiv(total, (int64_t)kXcds * slab) * kXcds * slab;  // whole slabs on every XCD (slab_logical_tile)
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads), lds, s, p);
   return check_launch("grouped wgrad kernel");
