@@ -54,14 +54,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "621da2df909303201219f3fd03aaf81ad613a8e79dbbc7f5e18213ddd804f81e"
+TRAFFIC_C3_GEMM_SHA256 = "b03a0d2dde13ecd9a8d9164a0d40aa0c869725cf1d9a4163dcc7ff6cb96f8bdd"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 5965571445,
-    "scatter2scatter#0": 2891706346,
-    "glu_w2_backward_dh#0": 2295507584,
-    "scatter2scatter#1": 5768758741,
-    "group_bwd_w#0": 2165667242,
-    "group_bwd_w#1": 3666513557,
+    "glu_w1_forward#0": 5784742325,
+    "scatter2scatter#0": 2887367466,
+    "glu_w2_backward_dh#0": 2309779264,
+    "scatter2scatter#1": 5768308245,
+    "group_bwd_w#0": 2171362474,
+    "group_bwd_w#1": 3656050624,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
