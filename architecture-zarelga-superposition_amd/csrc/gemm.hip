@@ -31,7 +31,10 @@
 //     Newton-Schulz terms.
 //   * Workgroup -> tile: XCD-aware. Workgroup b runs on XCD b % 8; each XCD takes
 //     a contiguous range of the (expert, m-tile, n-tile) sequence so that tiles
-//     sharing an expert's weights and rows run on one XCD and share its L2.
+//     sharing an expert's weights and rows run on one XCD and share its L2, or,
+//     for weight grads and for rows launches under skewed routing, slabs of 32
+//     consecutive tiles dealt to the XCDs in turn so that uneven per-tile costs
+//     even out (xcd_logical_tile, slab_logical_tile).
 // The f32 kernels use the same tiling with VGPR-staged loads, 32-deep stages and
 // v_mfma_f32_32x32x2f32 (four per 16-byte fragment).
 #include <mutex>
