@@ -54,7 +54,7 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "b03a0d2dde13ecd9a8d9164a0d40aa0c869725cf1d9a4163dcc7ff6cb96f8bdd"
+TRAFFIC_C3_GEMM_SHA256 = "3a69d040bc6228b5a5d278f493c0e41b28435eb2a7d0028b336d57abfe0deaaf"
 TRAFFIC_C3 = {
     "glu_w1_forward#0": 5784742325,
     "scatter2scatter#0": 2887367466,
