@@ -105,10 +105,11 @@ def test_group_bwd_w_gather_dy(hip_device, T, K, N, E, k, skew):
 
 
 def test_group_bwd_w_gather_dy_small_expert_split(hip_device):
-    """The DY gather on both sides of the small-expert split (0, 1, 64, 65 rows)."""
+    """The DY gather on both sides of the few-rows split and its k-step bounds (0, 1, 5, 16,
+    17, 63, 64, 65 rows)."""
     from zmoe import ops
 
-    counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0])
+    counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0, 16, 17, 5])
     E, k, N, K = len(counts), 2, 256, 320
     off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
     R = int(counts.sum())
@@ -146,11 +147,12 @@ def test_glu_w1_forward_scaled(hip_device, T, d, f, E, k, skew):
 @pytest.mark.parametrize("gather", [False, True])
 def test_group_bwd_w_small_expert_split(hip_device, gather):
     """bf16 weight grads with 256 x 256 tiles and fewer than 1024 rows per expert on average:
-    experts of at most 64 rows go to a separate launch of 128 x 128 tiles. Row counts on
-    both sides of that bound (0, 1, 64, 65) beside large experts."""
+    experts of at most 64 rows go to the write-bound few-rows kernel (one to four 16-deep
+    k-steps). Row counts at each k-step bound and on both sides of the split (0, 1, 5, 16,
+    17, 63, 64, 65) beside large experts; K = 320 leaves a partial 256-column tile."""
     from zmoe import ops
 
-    counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0])
+    counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0, 16, 17, 5])
     E, k, N, K = len(counts), 2, 256, 320
     off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
     R = int(counts.sum())
