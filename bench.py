@@ -54,14 +54,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "3a69d040bc6228b5a5d278f493c0e41b28435eb2a7d0028b336d57abfe0deaaf"
+TRAFFIC_C3_GEMM_SHA256 = "bc268b8528c4dff2f507056b7316fac940d0c89406498e31b0bd10a046878858"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 5784742325,
-    "scatter2scatter#0": 2887367466,
-    "glu_w2_backward_dh#0": 2309779264,
-    "scatter2scatter#1": 5768308245,
-    "group_bwd_w#0": 2171362474,
-    "group_bwd_w#1": 3656050624,
+    "glu_w1_forward#0": 5961600629,
+    "scatter2scatter#0": 2897061482,
+    "glu_w2_backward_dh#0": 2297685909,
+    "scatter2scatter#1": 5772380672,
+    "group_bwd_w#0": 2164063488,
+    "group_bwd_w#1": 3656080128,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
