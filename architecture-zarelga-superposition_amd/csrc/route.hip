@@ -27,8 +27,36 @@ __device__ __forceinline__ uint32_t score_key(float s) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// sigmoid evaluated in double, rounded once to float
-__device__ __forceinline__ float sigmoid_f64(float z) { return (float)(1.0 / (1.0 + exp(-(double)z))); }
+// Logits at or below this value give probability 0: there torch's sigmoid, which forms
+// 1 / (1 + exp(-z)) in fp32, overflows exp(-z) to inf (fp32 exp overflows from
+// 88.72283935546875 up; the true probabilities, below 2.9e-39, would be subnormal).
+constexpr float kSigmoidZeroBelow = -88.72283935546875f;
+
+// Below this |z| the probability comes from p = 0.5 + z/4 - z^3/48 + ...: 0.5 + z/4 is
+// exact in double, and the cubic term cannot move it across an fp32 rounding midpoint
+// unless it lies exactly on one (its distance from a midpoint is a multiple of z's last
+// bit / 4, more than |z|^3/48 here).
+constexpr float kSigmoidSeriesBelow = 0x1p-12f;
+
+// sigmoid correctly rounded to float: for |z| < kSigmoidSeriesBelow, 0.5 + z/4 rounded to
+// nearest with an exact tie going to the side the cubic term puts the true value on (down
+// for z > 0, up for z < 0; many small bf16 logits land on such ties, where a double
+// evaluation's rounding would hang on the last bit of its exp); otherwise
+// 1 / (1 + exp(-z)) in double, rounded once; 0 at or below kSigmoidZeroBelow.
+__device__ __forceinline__ float sigmoid_f64(float z) {
+  if (z <= kSigmoidZeroBelow) return 0.f;
+  if (fabsf(z) < kSigmoidSeriesBelow) {
+    const double s = 0.5 + 0.25 * (double)z;
+    const float f = (float)s;
+    const double fd = (double)f;
+    if (fd != s) {  // f > 0: its other neighbour around s is one bit pattern up or down
+      const float o = __uint_as_float(__float_as_uint(f) + (fd < s ? 1u : 0xffffffffu));
+      if (fabs(s - fd) == fabs((double)o - s)) return z > 0.f ? fminf(f, o) : fmaxf(f, o);
+    }
+    return f;
+  }
+  return (float)(1.0 / (1.0 + exp(-(double)z)));
+}
 
 // bf16(sigmoid_f64(z)) (the probability a bf16 gate stores) from fp32 arithmetic where that
 // is provably the same value: the fp32 estimate is within a few fp32 ulps of the true
@@ -50,7 +78,8 @@ __device__ __forceinline__ float sigmoid_bf16(float z) {
 // bf16(fp32(sigmoid_f64(z))) for every bf16 logit z, indexed by z's bits: the value
 // sigmoid_bf16 returns, read instead of evaluated when the logits themselves are bf16.
 // The build writes the entries (float64 sigmoid, one rounding to float, then to bf16 by
-// round to nearest even; NaN logits give 0x7fc0). 128 KB, read through the caches.
+// round to nearest even; 0 at or below kSigmoidZeroBelow; NaN logits give 0x7fc0). 128 KB,
+// read through the caches.
 __device__ const uint16_t kSigmoidBf16[65536] = {
 #include "zmoe_sigmoid_bf16.inc"
 };

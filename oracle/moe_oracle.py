@@ -24,9 +24,18 @@ Pinning (what checks each function, all in ``tests/test_oracle.py``):
 * ``scatter2scatter``      per-row dense loop (textbook matmul per row).
 * ``group_bwd_w``          per-row outer-product accumulation; empty expert = 0.
 * ``rowwise_sum_product``  einsum.
-* ``parallel_linear_*`` / ``glu_mlp_*`` / ``gate_*`` / ``moe_layer_*`` backward:
-                           torch autograd of an independent dense formulation and
-                           float64 central finite differences on tiny shapes.
+* ``parallel_linear_forward`` / ``parallel_linear_backward``: torch float64
+                           autograd of a slot-by-slot formulation in every caller
+                           mode (gathered or grouped input, slot or grouped
+                           output, gates, bias), and float64 central differences
+                           of every input element on tiny shapes; the bf16
+                           storage mode against torch's own bf16 autograd of the
+                           reference's composition (bit-equal but for rare
+                           accumulation-order flips, far closer than exact mode).
+* ``route_topk_backward``  torch autograd through sigmoid, gather and L1 normalise.
+* ``glu_mlp_*`` / ``MoELayerOracle``: torch autograd of an independent per-token
+                           dense formulation of the layer; float64 central
+                           differences of the GLU experts on tiny shapes.
 * ``bias_update``          closed form on a hand-built histogram.
 * ``zc_rmsnorm_rows``      closed forms: a constant row c gives sign(c)(1 + w)/sqrt(1 +
                            eps/c^2); scale invariance at eps = 0; w = 0 gives rows of
@@ -59,6 +68,8 @@ def _f():
 __all__ = [
     "set_precision",
     "bf16_round",
+    "SIGMOID_ZERO_BELOW",
+    "SIGMOID_SERIES_BELOW",
     "sigmoid_f32",
     "route_topk",
     "route_topk_backward",
@@ -105,16 +116,46 @@ def bf16_round(x):
     return np.where(np.isnan(x), x, out).astype(np.float32)
 
 
-def sigmoid_f32(logits):
-    """sigmoid evaluated in float64 and rounded once to float32.
+SIGMOID_ZERO_BELOW = -88.72283935546875
+SIGMOID_SERIES_BELOW = 2.0 ** -12
 
-    Restates ``torch.sigmoid(gate_output)`` (modeling/moe_gate.py:27). The HIP
-    kernel evaluates the same float64 expression, so p agrees bit-for-bit.
+
+def sigmoid_f32(logits):
+    """sigmoid of float32 logits, correctly rounded to float32; 0 for logits at or below
+    ``SIGMOID_ZERO_BELOW``.
+
+    Restates ``torch.sigmoid(gate_output)`` (modeling/moe_gate.py:27). torch forms
+    1 / (1 + exp(-z)) in float32, whose exp(-z) overflows to inf from z <= -88.7228...
+    on, so its probability there is 0 (not the subnormal float64 value); this function
+    follows it. Elsewhere torch's float32 evaluation can differ from the correctly
+    rounded value by an ulp; the contract is the correctly rounded one:
+
+    * |z| < 2^-12: p = 0.5 + z/4 - z^3/48 + ...; 0.5 + z/4 is exact in float64 and the
+      cubic term cannot move it across an fp32 rounding midpoint unless it lies exactly on
+      one (its distance from a midpoint is a multiple of z's last bit / 4, which exceeds
+      |z|^3/48 here), so p is 0.5 + z/4 rounded to nearest, an exact tie going to the
+      side the cubic term puts the true value on (down for z > 0, up for z < 0). Many
+      small bf16 logits land on such ties, where a float64 evaluation's rounding depends
+      on the last bit of its exp.
+    * otherwise 1 / (1 + exp(-z)) in float64, rounded once.
+
+    The HIP kernel evaluates the same two forms, so p agrees bit-for-bit.
     """
-    z = np.asarray(logits, dtype=np.float64)
-    with np.errstate(over="ignore"):
+    z = np.asarray(logits, dtype=np.float32).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
         p = 1.0 / (1.0 + np.exp(-z))
-    return p.astype(np.float32)
+    p = np.where(z <= SIGMOID_ZERO_BELOW, 0.0, p).astype(np.float32)
+    small = np.abs(z) < SIGMOID_SERIES_BELOW
+    if small.any():
+        zs = z[small]
+        s = 0.5 + 0.25 * zs                                   # exact
+        f = s.astype(np.float32)
+        fd = f.astype(np.float64)
+        other = np.where(fd < s, np.nextafter(f, np.float32(1)), np.nextafter(f, np.float32(0)))
+        tie = (fd != s) & (np.abs(s - fd) == np.abs(other.astype(np.float64) - s))
+        side = np.where(zs > 0, np.minimum(f, other), np.maximum(f, other))
+        p[small] = np.where(tie, side, f)
+    return p
 
 
 # --------------------------------------------------------------------------- #
@@ -304,33 +345,40 @@ def rowwise_sum_product(A, B):
 # --------------------------------------------------------------------------- #
 def parallel_linear_forward(x, W, k, sorted_expert_idxs, sorted_scattered_idxs,
                             expert_offsets, b=None, gates=None,
-                            grouped_in=False, grouped_out=False):
+                            grouped_in=False, grouped_out=False, store=None):
     """ParallelLinear.forward (parallel_experts.py:34-68). W is logical [E, K, N].
 
     Returns (output, output_expanded) where output_expanded is the [T, k, N]
     per-slot output saved for backward when ``gates`` is given (:50-55).
+    ``store`` rounds where a bf16 path stores (see ``storage_rounder``): the expert
+    outputs (:41-47) and the gate-weighted combine (:50-52).
     """
-    out = scatter2scatter(x, W, sorted_expert_idxs, sorted_scattered_idxs, k, b=b,
-                          x_grouped=grouped_in, y_grouped=grouped_out)
+    r = storage_rounder(store)
+    out = r(scatter2scatter(x, W, sorted_expert_idxs, sorted_scattered_idxs, k, b=b,
+                            x_grouped=grouped_in, y_grouped=grouped_out))
     if gates is None:
         return out, None
     g = np.asarray(gates, dtype=_f())
     T, kk = g.shape
     expanded = out.reshape(T, kk, out.shape[-1])
-    return np.einsum("tj,tjn->tn", g, expanded), expanded
+    return r(np.einsum("tj,tjn->tn", g, expanded)), expanded
 
 
 def parallel_linear_backward(grad_out, x, W, k, sorted_expert_idxs, sorted_scattered_idxs,
                              expert_offsets, b=None, gates=None, output_expanded=None,
-                             grouped_in=False, grouped_out=False):
+                             grouped_in=False, grouped_out=False, store=None):
     """ParallelLinear.backward (parallel_experts.py:70-135).
 
     Returns (d_input, d_weights [E, K, N], d_biases or None, d_gates or None).
+    ``store`` rounds where a bf16 path stores: d_gates (in the gates' dtype, :82), the
+    gate-scaled grouped grad rows (:95-97), the weight and bias grads (:105-110), the
+    per-slot input grads (:112-120) and their k-sum (:125).
     """
+    r = storage_rounder(store)
     grad_out = np.asarray(grad_out, dtype=_f())
     E = np.asarray(W).shape[0]
     if gates is not None:
-        d_gates = rowwise_sum_product(output_expanded, grad_out)             # :82
+        d_gates = r(rowwise_sum_product(output_expanded, grad_out))          # :82
         gates_flat = np.asarray(gates, dtype=_f()).reshape(-1)
         gate_fan = np.asarray(gates).shape[1]
     else:
@@ -338,18 +386,20 @@ def parallel_linear_backward(grad_out, x, W, k, sorted_expert_idxs, sorted_scatt
     if grouped_out:
         grouped_grad_out = grad_out                                            # :93
     else:
-        grouped_grad_out = group(grad_out, sorted_scattered_idxs,              # :95-97
-                                 coeff=gates_flat, fan_out=gate_fan)
+        grouped_grad_out = r(group(grad_out, sorted_scattered_idxs,            # :95-97
+                                   coeff=gates_flat, fan_out=gate_fan))
     grouped_x = x if grouped_in else group(x, sorted_scattered_idxs, fan_out=k)  # :98-103
     d_w, d_b = group_bwd_w(grouped_grad_out, grouped_x, expert_offsets, E,       # :105-110
                            has_bias=b is not None)
+    d_w = r(d_w)
+    d_b = None if d_b is None else r(d_b)
     Wt = np.transpose(np.asarray(W, dtype=_f()), (0, 2, 1))
-    d_exp = scatter2scatter(grouped_grad_out, Wt, sorted_expert_idxs,            # :112-120
-                            sorted_scattered_idxs, 1, x_grouped=True, y_grouped=grouped_in)
+    d_exp = r(scatter2scatter(grouped_grad_out, Wt, sorted_expert_idxs,          # :112-120
+                              sorted_scattered_idxs, 1, x_grouped=True, y_grouped=grouped_in))
     if k == 1:
         d_input = d_exp
     else:
-        d_input = d_exp.reshape(np.asarray(x).shape[0], k, -1).sum(axis=1)      # :125
+        d_input = r(d_exp.reshape(np.asarray(x).shape[0], k, -1).sum(axis=1))  # :125
     return d_input, d_w, d_b, d_gates
 
 

@@ -74,6 +74,30 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert rc == 4
 
 
+def _header_define(name):
+    m = re.search(r"#define\s+" + name + r"\s+\(\(size_t\)(\d+) << (\d+)\)", open(HEADER).read())
+    assert m, name
+    return int(m.group(1)) << int(m.group(2))
+
+
+def test_noalloc_sort_rejects_sizes_above_its_scratch():
+    """The no-allocation sort refuses, on the host, a size whose workspace exceeds its
+    scratch array (ZMOE_SORT_NOALLOC_MAX_BYTES, read from the header). Every device
+    pointer but the offsets is null, so a regression in the size check would stop at the
+    null-pointer check (ERR_NULL) instead of launching."""
+    from zmoe import _lib
+
+    lib = _lib.load()
+    cap = _header_define("ZMOE_SORT_NOALLOC_MAX_BYTES")
+    E = 1024
+    header = lib.zmoe_sort_workspace_bytes(1024, E) - (E + 1) * 4  # workspace = header + tiles x (E + 1) x 4
+    R = ((cap - header) // ((E + 1) * 4) + 1) * 1024  # the smallest tile count the scratch cannot hold
+    assert lib.zmoe_sort_workspace_bytes(R, E) > cap
+    assert lib.zmoe_sort_workspace_bytes(R - 1024, E) <= cap
+    rc = lib.zmoe_flatten_sort_count_noalloc(None, R, E, None, None, ctypes.c_void_p(256), None, None, None)
+    assert rc == 5 and b"maximum" in lib.zmoe_last_error()
+
+
 def test_dense_wgrad_workspace_holds_every_split_offset():
     """The split offsets (one int64 per split, up to 64 splits) sit in a header ahead of the
     fp32 partials; the header must hold all 64 so that the offsets of splits 32..63 do not
@@ -108,12 +132,16 @@ def test_newton_schulz_workspace_is_sized_for_one_pass():
     assert lib.zmoe_newton_schulz5_workspace_bytes(1, 65536, 65536) == 0  # one matrix above 2 GiB
 
 
-def test_sigmoid_table_matches_oracle(tmp_path):
+def test_sigmoid_table_matches_torch_and_oracle(tmp_path):
     """The build's routing-probability table (kSigmoidBf16, one entry per bf16 logit) equals
-    the oracle's bf16(fp32(sigmoid in float64)) for all 65536 bit patterns, NaNs included."""
+    torch's own bf16 sigmoid (what the reference's gate computes under bf16 autocast,
+    modeling/moe_gate.py:27) for all 65536 bit patterns, NaNs included, and so does the
+    oracle's bf16(sigmoid_f32); the saturated logits (-89 ... -92.5, where float32 exp(-z)
+    overflows) are 0 on all three."""
     import sys
 
     import numpy as np
+    import torch
 
     import oracle as O
 
@@ -127,8 +155,12 @@ def test_sigmoid_table_matches_oracle(tmp_path):
     assert bits.size == 65536
     with np.errstate(all="ignore"):
         z = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
-        ref = O.bf16_round(O.sigmoid_f32(z))
+        orc = O.bf16_round(O.sigmoid_f32(z))
+    ref = torch.sigmoid(torch.from_numpy(z).to(torch.bfloat16)).float().numpy()
     got = (bits << 16).view(np.float32)
-    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
-    ok = ~np.isnan(ref)
-    np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
+    for other in (ref, orc):
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(other))
+        ok = ~np.isnan(other)
+        np.testing.assert_array_equal(got[ok].view(np.uint32), other[ok].view(np.uint32))
+    sat = (z <= -89.0) & (z >= -92.5)
+    assert sat.sum() == 8 and not got[sat].any()

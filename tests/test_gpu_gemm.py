@@ -104,13 +104,14 @@ def test_group_bwd_w_gather_dy(hip_device, T, K, N, E, k, skew):
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
 
 
-def test_group_bwd_w_gather_dy_small_expert_split(hip_device):
+@pytest.mark.parametrize("k", [2, 3, 6])
+def test_group_bwd_w_gather_dy_small_expert_split(hip_device, k):
     """The DY gather on both sides of the few-rows split and its k-step bounds (0, 1, 5, 16,
-    17, 63, 64, 65 rows)."""
+    17, 63, 64, 65 rows); k = 3 and 6 divide the gathered slot ids by a non-power of two."""
     from zmoe import ops
 
     counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0, 16, 17, 5])
-    E, k, N, K = len(counts), 2, 256, 320
+    E, N, K = len(counts), 256, 320
     off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
     R = int(counts.sum())
     g = gen(R + K)
@@ -144,16 +145,17 @@ def test_glu_w1_forward_scaled(hip_device, T, d, f, E, k, skew):
     assert_close(np64(A), ref.astype(np.float64), **TOL[torch.bfloat16], what="scaled A")
 
 
-@pytest.mark.parametrize("gather", [False, True])
-def test_group_bwd_w_small_expert_split(hip_device, gather):
+@pytest.mark.parametrize("gather,k", [(False, 2), (True, 2), (True, 3), (True, 6)])
+def test_group_bwd_w_small_expert_split(hip_device, gather, k):
     """bf16 weight grads with 256 x 256 tiles and fewer than 1024 rows per expert on average:
     experts of at most 64 rows go to the write-bound few-rows kernel (one to four 16-deep
     k-steps). Row counts at each k-step bound and on both sides of the split (0, 1, 5, 16,
-    17, 63, 64, 65) beside large experts; K = 320 leaves a partial 256-column tile."""
+    17, 63, 64, 65) beside large experts; K = 320 leaves a partial 256-column tile. With the
+    x gather, k = 3 and 6 divide the slot ids by a non-power of two."""
     from zmoe import ops
 
     counts = np.array([0, 1, 64, 65, 700, 2000, 300, 1000, 63, 0, 16, 17, 5])
-    E, k, N, K = len(counts), 2, 256, 320
+    E, N, K = len(counts), 256, 320
     off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
     R = int(counts.sum())
     g = gen(R + N)

@@ -61,20 +61,68 @@ def test_route_topk_bf16_logits_fp32_probs(hip_device, T, E, k):
     assert_close(w.cpu().numpy()[ok], rw[ok], rtol=1e-6, atol=1e-7, what="topk_weight")
 
 
-@pytest.mark.parametrize("bias_std", [0.0, 0.3])
-def test_route_topk_every_bf16_logit(hip_device, bias_std):
-    """Every one of the 65536 bf16 values as a logit (NaNs, infinities, subnormals and both
-    zeros included), all selected (k = E = 64): each probability equals the oracle's
-    bf16(fp32(sigmoid in float64)) bit for bit, whichever evaluation the kernel used."""
+@pytest.mark.parametrize("bias_std,rb", [(0.0, True), (0.3, True), (0.3, False)])
+def test_route_topk_every_bf16_logit(hip_device, bias_std, rb):
+    """Every one of the 65536 bf16 values as a logit (NaNs, infinities, subnormals, both
+    zeros and the saturated logits included), all selected (k = E = 64): each probability
+    equals the oracle's bf16(fp32(sigmoid in float64)) (or, with rb False, the fp32 value)
+    bit for bit, whichever evaluation the kernel used."""
     from zmoe import ops
 
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
     logits = bits.view(torch.bfloat16).reshape(1024, 64)
     bias = torch.randn(64, generator=gen(9)) * bias_std
-    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), 64, round_probs_bf16=True)
-    ridx, rw, rp = O.route_topk(logits.float().numpy(), bias.numpy(), 64, round_probs_bf16=True)
+    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), 64, round_probs_bf16=rb)
+    ridx, rw, rp = O.route_topk(logits.float().numpy(), bias.numpy(), 64, round_probs_bf16=rb)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
     np.testing.assert_array_equal(p.cpu().numpy(), rp)
+
+
+def _hard_fp32_logits(n_mid: int, seed: int) -> np.ndarray:
+    """fp32 logits where a bf16 probability is hardest to get right from fp32 arithmetic:
+    z = logit(midpoint between two adjacent bf16 probabilities), nudged by -24..24 fp32 ulps,
+    so sigmoid(z) lies within a few fp32 ulps of a bf16 rounding midpoint; |z| around 80
+    (where the kernel's fp32 evaluation hands over to double); the saturation edge
+    (-88.7228...: fp32 exp(-z) overflows from there on, p = 0); and NaN / +-inf."""
+    r = np.random.default_rng(seed)
+    m = O.bf16_round(r.uniform(1e-6, 0.99, n_mid).astype(np.float32))  # stays below 1 after rounding
+    ulp = (m.view(np.uint32) & 0x7F800000).view(np.float32) * np.float32(2.0 ** -7)  # bf16 ulp of m
+    mid = m.astype(np.float64) + ulp.astype(np.float64) / 2
+    z0 = np.log(mid / (1.0 - mid)).astype(np.float32)
+    nudge = r.integers(-24, 25, n_mid).astype(np.int64)
+    z = (z0.view(np.int32).astype(np.int64) + np.where(z0 < 0, -nudge, nudge)).astype(np.int32).view(np.float32)
+    edge = np.float32(O.SIGMOID_ZERO_BELOW)
+    around = [np.nextafter(edge, np.float32(0)), edge, np.nextafter(edge, np.float32(-200))]
+    special = np.array([80.0, -80.0, 79.99999, -79.99999, 80.00001, -80.00001, 88.0, -88.0, 88.75, -88.75,
+                        -89.0, -92.5, -103.0, -110.0, 110.0, 0.0, -0.0, np.inf, -np.inf, np.nan] + around,
+                       dtype=np.float32)
+    band = r.uniform(-90.0, -78.0, 400).astype(np.float32)
+    return np.concatenate([z, special, band, -band[:100]])
+
+
+@pytest.mark.parametrize("k,rb", [(64, True), (8, True), (64, False)])
+def test_route_topk_fp32_logits_hard_cases(hip_device, k, rb):
+    """fp32 logits at the hard cases. With bf16-rounded probabilities (round_probs_bf16=True,
+    as a bf16 gate over an fp32 projection) the kernel's fp32 sigmoid with its guard band
+    around bf16 midpoints and its double fallback must give the oracle's bf16(fp32(sigmoid))
+    bit for bit, and so the same selection; with fp32 probabilities the double evaluation,
+    0 from the saturation edge on."""
+    from zmoe import ops
+
+    E = 64
+    z = _hard_fp32_logits(64 * 300, seed=k)
+    n = (z.size // E) * E
+    logits = torch.from_numpy(z[:n].copy()).reshape(-1, E)
+    perm = torch.randperm(n, generator=gen(k)).reshape(-1, E)  # mix the kinds within rows
+    logits = logits.reshape(-1)[perm.reshape(-1)].reshape(-1, E).contiguous()
+    bias = torch.zeros(E) if k == E else torch.randn(E, generator=gen(5)) * 1e-3
+    idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), k, round_probs_bf16=rb)
+    ridx, rw, rp = O.route_topk(logits.numpy(), bias.numpy(), k, round_probs_bf16=rb)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    got, ref = p.cpu().numpy(), rp
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
 
 
 def test_route_equal_scores_and_forced_bias(hip_device):

@@ -41,6 +41,48 @@ def test_sigmoid_closed_forms():
         assert O.sigmoid_f32(np.array([v]))[0] == np.float32(1.0 / (1.0 + math.exp(-v)))
 
 
+def _sigmoid_correctly_rounded_f32(z: float) -> np.float32:
+    """sigmoid(z) to 50 digits (decimal), then the nearest float32 (ties impossible but
+    at z = 0), by comparing the candidate and its neighbours exactly."""
+    import decimal
+
+    ctx = decimal.Context(prec=50)
+    d = ctx.divide(1, ctx.add(1, ctx.exp(decimal.Decimal(-z))))
+    f = np.float32(float(d))
+    cands = [np.nextafter(f, np.float32(-1)), f, np.nextafter(f, np.float32(2))]
+    return min(cands, key=lambda c: abs(decimal.Decimal(float(c)) - d))
+
+
+def test_sigmoid_is_correctly_rounded():
+    """Against a 50-digit evaluation rounded to the nearest float32: every bf16 logit (the
+    small ones land on fp32 rounding ties of 0.5 + z/4 that a float64 evaluation cannot
+    resolve) and a sample of float32 logits, outside the saturated range."""
+    z16 = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    r = rng(21)
+    zf = np.concatenate([(r.standard_normal(3000) * 6).astype(np.float32),
+                         (r.standard_normal(3000) * 1e-4).astype(np.float32),
+                         np.float32(2.0 ** -12) * np.array([0.999999, 1.0, -0.999999, -1.0], np.float32)])
+    for z in (z16, zf):
+        z = z[np.isfinite(z) & (z > O.SIGMOID_ZERO_BELOW)]
+        got = O.sigmoid_f32(z)
+        ref = np.array([_sigmoid_correctly_rounded_f32(float(v)) for v in z], np.float32)
+        bad = got.view(np.uint32) != ref.view(np.uint32)
+        assert not bad.any(), (z[bad][:5], got[bad][:5], ref[bad][:5])
+
+
+def test_sigmoid_saturates_where_torch_does():
+    """Every float32 logit in [-100, -85]: the oracle's p is 0 exactly where torch's float32
+    sigmoid is 0 (its exp(-z) overflows), and subnormal-or-larger elsewhere."""
+    lo, hi = np.float32(-85.0).view(np.uint32), np.float32(-100.0).view(np.uint32)
+    z = np.arange(lo, hi, dtype=np.uint32).view(np.float32)
+    t = torch.sigmoid(torch.from_numpy(z)).numpy()
+    p = O.sigmoid_f32(z)
+    np.testing.assert_array_equal(p == 0, t == 0)
+    assert (z[p == 0] <= O.SIGMOID_ZERO_BELOW).all() and (p[z > O.SIGMOID_ZERO_BELOW] > 0).all()
+    # away from saturation the two differ by at most an ulp of float32
+    np.testing.assert_allclose(p[p > 0], t[p > 0], rtol=2.4e-7, atol=0)
+
+
 # ----------------------------------------------------------------- routing
 def _brute_route(logits, bias, k, round_bf16=False):
     T, E = logits.shape
@@ -184,6 +226,179 @@ def test_group_bwd_w_outer_products_and_empty_expert():
         np.testing.assert_allclose(DW[e], ref, atol=1e-12)
         start = off[e]
     assert not DW[1].any() and not DW[4].any() and not Db[1].any()
+
+
+# ----------------------------------------------------------------- ParallelLinear
+# The modes a caller of ParallelLinear can use (reference parallel_experts.py:34-135).
+# A gathered input fans each token out to its ``fan`` slots (k = fan). A grouped input
+# is already one row per slot, so it is called with k = 1, as GLUMLP's W2 is (mlp.py:89);
+# the reference's k-sum at :124-125 would not fit any other k. Gates [T, fan] combine
+# the slot rows of a token, so they go with slot-order output (:50-52).
+_PL_MODES = [
+    # (fan, grouped_in, grouped_out, gates, bias)
+    (3, False, False, False, False),
+    (1, False, False, False, True),
+    (3, False, True, False, True),
+    (3, False, False, True, False),
+    (3, False, False, True, True),
+    (3, True, False, False, True),
+    (3, True, True, False, False),
+    (3, True, False, True, True),
+]
+
+
+def _pl_case(seed, fan, grouped_in, gates, bias, T=5, E=4, K=6, N=5):
+    r = rng(seed)
+    idx = np.stack([r.choice(E, fan, replace=False) for _ in range(T)])
+    se, ss, off = O.flatten_sort_count(idx, E)
+    R = T * fan
+    C = dict(
+        x=r.standard_normal((R if grouped_in else T, K)),
+        W=r.standard_normal((E, K, N)),
+        b=r.standard_normal((E, N)) if bias else None,
+        gates=(r.random((T, fan)) + 0.2) if gates else None,
+    )
+    return C, se, ss, off, (1 if grouped_in else fan)
+
+
+def _pl_torch(C, se, ss, k, grouped_in, grouped_out):
+    """ParallelLinear written slot by slot in torch float64 (autograd supplies the
+    backward): sorted position i applies expert se[i] to row i of a grouped input, or
+    to token ss[i] // k of a gathered one, and writes the slot's row ss[i], or row i
+    when the output is grouped; gates then weight the fan rows of each token."""
+    t = lambda a: None if a is None else torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    x, W, b, g = t(C["x"]), t(C["W"]), t(C["b"]), t(C["gates"])
+    R = se.size
+    rows = [None] * R
+    for i in range(R):
+        slot = int(ss[i])
+        xin = x[i] if grouped_in else x[slot // k]
+        y = xin @ W[int(se[i])]
+        if b is not None:
+            y = y + b[int(se[i])]
+        rows[i if grouped_out else slot] = y
+    Y = torch.stack(rows)
+    if g is not None:
+        fan = g.shape[1]
+        out = torch.stack([sum(g[tt, j] * Y[tt * fan + j] for j in range(fan)) for tt in range(g.shape[0])])
+    else:
+        out = Y
+    return out, (x, W, b, g)
+
+
+@pytest.mark.parametrize("fan,grouped_in,grouped_out,gates,bias", _PL_MODES)
+def test_parallel_linear_vs_torch_autograd(fan, grouped_in, grouped_out, gates, bias):
+    C, se, ss, off, k = _pl_case(30 + fan, fan, grouped_in, gates, bias)
+    out, expanded = O.parallel_linear_forward(C["x"], C["W"], k, se, ss, off, b=C["b"], gates=C["gates"],
+                                              grouped_in=grouped_in, grouped_out=grouped_out)
+    tout, (x, W, b, g) = _pl_torch(C, se, ss, k, grouped_in, grouped_out)
+    np.testing.assert_allclose(out, tout.detach().numpy(), rtol=1e-12, atol=1e-12)
+    assert (expanded is None) == (not gates)
+    dy = rng(40).standard_normal(out.shape)
+    dx, dW, db, dg = O.parallel_linear_backward(dy, C["x"], C["W"], k, se, ss, off, b=C["b"], gates=C["gates"],
+                                                output_expanded=expanded, grouped_in=grouped_in,
+                                                grouped_out=grouped_out)
+    (tout * torch.from_numpy(dy)).sum().backward()
+    np.testing.assert_allclose(dx, x.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dW, W.grad.numpy(), rtol=1e-12, atol=1e-12)
+    if bias:
+        np.testing.assert_allclose(db, b.grad.numpy(), rtol=1e-12, atol=1e-12)
+    else:
+        assert db is None
+    if gates:
+        np.testing.assert_allclose(dg, g.grad.numpy(), rtol=1e-12, atol=1e-12)
+    else:
+        assert dg is None
+
+
+@pytest.mark.parametrize("fan,grouped_in,grouped_out,gates,bias", [_PL_MODES[2], _PL_MODES[4], _PL_MODES[7]])
+def test_parallel_linear_finite_differences(fan, grouped_in, grouped_out, gates, bias):
+    """Central differences in float64 of <out, dy> against the oracle's backward."""
+    C, se, ss, off, k = _pl_case(50 + fan, fan, grouped_in, gates, bias, T=4, E=3, K=4, N=3)
+    kw = dict(grouped_in=grouped_in, grouped_out=grouped_out)
+    out, expanded = O.parallel_linear_forward(C["x"], C["W"], k, se, ss, off, b=C["b"], gates=C["gates"], **kw)
+    dy = rng(51).standard_normal(out.shape)
+    grads = O.parallel_linear_backward(dy, C["x"], C["W"], k, se, ss, off, b=C["b"], gates=C["gates"],
+                                       output_expanded=expanded, **kw)
+    named = dict(zip(("x", "W", "b", "gates"), grads))
+
+    def loss():
+        y, _ = O.parallel_linear_forward(C["x"], C["W"], k, se, ss, off, b=C["b"], gates=C["gates"], **kw)
+        return float((y * dy).sum())
+
+    eps = 1e-6
+    for name in ("x", "W", "b", "gates"):
+        if C[name] is None:
+            continue
+        flat = C[name].reshape(-1)
+        for q in range(flat.size):
+            old = flat[q]
+            flat[q] = old + eps
+            lp = loss()
+            flat[q] = old - eps
+            lm = loss()
+            flat[q] = old
+            num = (lp - lm) / (2 * eps)
+            assert abs(num - named[name].reshape(-1)[q]) < 1e-7 * max(1.0, abs(num)), (name, q)
+
+
+def _torch_bf16_parallel_linear(C, se, ss, k, grouped_in, grouped_out, dy):
+    """The reference's ParallelLinear composition in torch's own bf16 tensor arithmetic
+    (CPU autograd): per-expert bf16 matmuls (fp32 accumulation, one rounding; addmm adds
+    the bias before it, as the reference's kernel does, ops.py:181-183), the slot rows assembled in a bf16 buffer and combined by a
+    bf16 bmm with bf16 gates (parallel_experts.py:50-52). A gathered x comes from a float32
+    leaf cast after the gather, so its k slots' grads are summed in fp32 and rounded once
+    (as the path's k-sum does)."""
+    bf = torch.bfloat16
+    x = torch.tensor(C["x"], dtype=torch.float32).requires_grad_(True)
+    W = torch.tensor(C["W"]).to(bf).requires_grad_(True)
+    b = None if C["b"] is None else torch.tensor(C["b"]).to(bf).requires_grad_(True)
+    g = None if C["gates"] is None else torch.tensor(C["gates"]).to(bf).requires_grad_(True)
+    R, N = se.size, C["W"].shape[2]
+    Y = torch.zeros(R, N, dtype=bf)
+    for e in range(C["W"].shape[0]):
+        pos = np.nonzero(se == e)[0]
+        if pos.size == 0:
+            continue
+        rows_in = torch.from_numpy(pos if grouped_in else ss[pos] // k)
+        ye = x[rows_in].to(bf) @ W[e] if b is None else torch.addmm(b[e], x[rows_in].to(bf), W[e])
+        Y = Y.index_copy(0, torch.from_numpy(pos if grouped_out else ss[pos]), ye)
+    out = Y if g is None else (g.unsqueeze(1) @ Y.view(g.shape[0], g.shape[1], N)).squeeze(1)
+    (out.float() * torch.from_numpy(dy).float()).sum().backward()
+    return out, x.grad.to(bf), W.grad, None if b is None else b.grad, None if g is None else g.grad
+
+
+@pytest.mark.parametrize("fan,grouped_in,grouped_out,gates,bias", _PL_MODES)
+def test_parallel_linear_bf16_store_matches_torch_bf16_arithmetic(fan, grouped_in, grouped_out, gates, bias):
+    """store="bf16" rounds where the reference's composition in bf16 tensor arithmetic
+    stores: bit for bit but for rare accumulation-order flips (torch sums in float32, the
+    oracle in float64), and far closer to torch's results than the exact mode, so a rounding
+    point left out, added or misplaced fails."""
+    T, E, K, N = 48, 4, 64, 40
+    C, se, ss, off, k = _pl_case(70 + fan, fan, grouped_in, gates, bias, T=T, E=E, K=K, N=N)
+    b16 = lambda a: None if a is None else O.bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
+    C = {key: b16(v) for key, v in C.items()}
+    dy = b16(rng(71).standard_normal((T, N) if gates else (T * fan, N)))
+    tres = [None if t is None else t.detach().double().numpy()
+            for t in _torch_bf16_parallel_linear(C, se, ss, k, grouped_in, grouped_out, dy)]
+    got = {}
+    for store in (None, "bf16"):
+        out, exp = O.parallel_linear_forward(C["x"], C["W"], k, se, ss, off, b=C["b"], gates=C["gates"],
+                                             grouped_in=grouped_in, grouped_out=grouped_out, store=store)
+        dx, dW, db, dg = O.parallel_linear_backward(dy, C["x"], C["W"], k, se, ss, off, b=C["b"],
+                                                    gates=C["gates"], output_expanded=exp, grouped_in=grouped_in,
+                                                    grouped_out=grouped_out, store=store)
+        got[store] = (out, O.bf16_round(dx) if store is None else dx, dW, db, dg)
+    for i, name in enumerate(("out", "dx", "dW", "db", "d_gates")):
+        ref = tres[i]
+        if ref is None:
+            assert got["bf16"][i] is None
+            continue
+        same = np.mean(got["bf16"][i] == ref)
+        assert same >= 0.99, (name, same)
+        assert np.all(np.abs(got["bf16"][i] - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30), name
+        eb, ee = _rel_fro(got["bf16"][i], ref), _rel_fro(got[None][i], ref)
+        assert eb <= 0.25 * ee or eb == 0.0, (name, eb, ee)
 
 
 def test_rowwise_sum_product():
