@@ -1428,6 +1428,53 @@ __device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* 
   }
 }
 
+// fp32 weight grads (fp32 master weights) through the wave's staging area: 32 rows of the
+// wave's block at a time, staged as fp32 rows of WN * 4 + 16 bytes (within the bf16 staging
+// area of a block of at least 64 rows), then written row-contiguously, 16 bytes per lane, so
+// every store covers whole 128-byte lines (from the MFMA layout directly, a store would be 16
+// bytes of each of 32 rows). Wave-local: LDS operations of one wave complete in order.
+template <int MI, int NI>
+__device__ __forceinline__ void wgrad_epilogue_f32_staged(const WgradParams& p, char* st,
+                                                          const f32x16_t (&acc)[MI][NI], int e, int m0, int n0,
+                                                          int wm0, int wn0) {
+  static_assert(MI >= 2, "the fp32 rows of one 32-row block fit the staging area of two");
+  constexpr int WN = NI * 32;
+  constexpr int PITCH = WN * 4 + 16;  // bytes per staged fp32 row
+  constexpr int CPR = WN / 4;         // 16-byte chunks per row
+  constexpr int ITERS = 32 * CPR / 64;
+  constexpr int B = ITERS < EPI_BATCH ? ITERS : EPI_BATCH;
+  static_assert(ITERS % B == 0, "batches tile the staged rows");
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31, g = lane >> 5;
+  float* DW = reinterpret_cast<float*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = 32 * ni + 8 * q + 4 * g;
+        *reinterpret_cast<float4*>(st + r * PITCH + col * 4) =
+            make_float4(acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
+      }
+#pragma unroll
+    for (int i0 = 0; i0 < ITERS; i0 += B) {
+      uint4 v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int idx = lane + 64 * (i0 + u);
+        v[u] = *reinterpret_cast<const uint4*>(st + (idx / CPR) * PITCH + (idx % CPR) * 16);
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int idx = lane + 64 * (i0 + u);
+        const int m = m0 + wm0 + 32 * mi + idx / CPR, n = n0 + wn0 + (idx % CPR) * 4;
+        if (m < p.Ndy && n < p.Kx) st_out(DW + (int64_t)m * p.Kx + n, v[u]);
+      }
+    }
+  }
+}
+
 // Wave layout of the bf16 kernels: NW = 4 waves in a 2 x 2 grid, 8 in a 2 x 4 grid or 16
 // in a 4 x 4 grid (waves w, w + 4, ... share SIMD w % 4).
 template <int BM, int BN, int NW>
@@ -1573,30 +1620,6 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
                                   nt, wm0, wn0, tile.mt, scale_table);
 }
 
-// fp32 output straight from the accumulators (split-K partials; no rounding): lane
-// (r, g) stores columns 32 ni + 8 q + 4 g .. + 3 of row 32 mi + r as one 16-byte write.
-template <int MI, int NI>
-__device__ __forceinline__ void wgrad_epilogue_f32(const WgradParams& p, const f32x16_t (&acc)[MI][NI], int e,
-                                                   int m0, int n0, int wm0, int wn0) {
-  const int lane = threadIdx.x & 63;
-  const int r = lane & 31, g = lane >> 5;
-  float* DW = reinterpret_cast<float*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const int m = m0 + wm0 + 32 * mi + r;
-    if (m >= p.Ndy) continue;
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn0 + 32 * ni + 8 * q + 4 * g;
-        if (n < p.Kx)
-          *reinterpret_cast<float4*>(DW + (int64_t)m * p.Kx + n) =
-              make_float4(acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
-      }
-  }
-}
-
 // GATHER: 0 = x rows in sorted order; 1 = gathered, row = index >> shift; 2 = gathered,
 // row = index / x_div. Both gathered forms keep the K loop free of branches. DYG: the
 // gather applies to the DY rows instead (x rows then in sorted order).
@@ -1738,10 +1761,11 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   };
   kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
+  char* st = smem + wave * 32 * MI * WaveStage<WN>::PITCH;
   if constexpr (OUT_F32)
-    wgrad_epilogue_f32(p, acc, e, m0, n0, wm0, wn0);
+    wgrad_epilogue_f32_staged(p, st, acc, e, m0, n0, wm0, wn0);
   else
-    wgrad_epilogue_bf16(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, acc, e, m0, n0, wm0, wn0);
+    wgrad_epilogue_bf16(p, st, acc, e, m0, n0, wm0, wn0);
 }
 
 // ------------------------------------------------------------------ weight grads of small experts
@@ -1758,7 +1782,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
 constexpr int kFewRows = 64;
 constexpr int kFewBM = 128, kFewBN = 256;
 
-template <int GATHER, bool DYG>
+template <int GATHER, bool DYG, bool OUT_F32 = false>
 __global__ __launch_bounds__(256, 2) void wgrad_few_rows_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
   constexpr int BM = kFewBM, BN = kFewBN, KT = kFewRows;
@@ -1849,7 +1873,11 @@ __global__ __launch_bounds__(256, 2) void wgrad_few_rows_kernel(WgradParams p) {
         acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ni].value(), fa[mi].value(), acc[mi][ni], 0, 0, 0);
   }
   __syncthreads();  // every wave has read the operand tiles; LDS becomes the staging areas
-  wgrad_epilogue_bf16(p, smem + wave * 32 * MI * WaveStage<WG::WN>::PITCH, acc, e, m0, n0, wm0, wn0);
+  char* st = smem + wave * 32 * MI * WaveStage<WG::WN>::PITCH;
+  if constexpr (OUT_F32)
+    wgrad_epilogue_f32_staged(p, st, acc, e, m0, n0, wm0, wn0);
+  else
+    wgrad_epilogue_bf16(p, st, acc, e, m0, n0, wm0, wn0);
 }
 
 constexpr int few_rows_lds_bytes() {
@@ -2450,29 +2478,32 @@ extern "C" int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k,
 namespace {
 // bf16 weight grads: 256 x 256 tiles when the experts are large enough, 128 x 128 otherwise,
 // and the small experts split off under a skewed routing. DYG: the gather is on DY's rows.
-template <bool DYG>
+template <bool DYG, bool OUT_F32 = false>
 int group_bwd_w_bf16(WgradParams p, int64_t M, int E, int64_t N, int64_t K, hipStream_t s) {
   const bool big = use_big_tiles(M, E, N) && K >= 256;
   const int gather = p.x_rows ? (p.x_div_shift >= 0 ? 1 : 2) : 0;
   if (DYG && gather == 0) return zmoe::set_error(ZMOE_ERR_NULL, "group_bwd_w: the DY gather needs indices");
   auto small_tiles = [&](const WgradParams& q) -> int {
     if (gather == 1)
-      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1, false, 4, DYG>, bf16_lds_bytes<128, 128>(), 128, 128,
-                                 q, s);
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 1, OUT_F32, 4, DYG>, bf16_lds_bytes<128, 128>(), 128,
+                                 128, q, s);
     if (gather == 2)
-      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2, false, 4, DYG>, bf16_lds_bytes<128, 128>(), 128, 128,
-                                 q, s);
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 2, OUT_F32, 4, DYG>, bf16_lds_bytes<128, 128>(), 128,
+                                 128, q, s);
     if constexpr (!DYG)
-      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
+      return launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0, OUT_F32>, bf16_lds_bytes<128, 128>(), 128, 128, q, s);
     return (int)ZMOE_ERR_NULL;  // not reached (checked above)
   };
   auto few_rows_tiles = [&](const WgradParams& q) -> int {
     if (gather == 1)
-      return launch_wgrad_kernel(wgrad_few_rows_kernel<1, DYG>, few_rows_lds_bytes(), kFewBM, kFewBN, q, s, 256);
+      return launch_wgrad_kernel(wgrad_few_rows_kernel<1, DYG, OUT_F32>, few_rows_lds_bytes(), kFewBM, kFewBN, q, s,
+                                 256);
     if (gather == 2)
-      return launch_wgrad_kernel(wgrad_few_rows_kernel<2, DYG>, few_rows_lds_bytes(), kFewBM, kFewBN, q, s, 256);
+      return launch_wgrad_kernel(wgrad_few_rows_kernel<2, DYG, OUT_F32>, few_rows_lds_bytes(), kFewBM, kFewBN, q, s,
+                                 256);
     if constexpr (!DYG)
-      return launch_wgrad_kernel(wgrad_few_rows_kernel<0, false>, few_rows_lds_bytes(), kFewBM, kFewBN, q, s, 256);
+      return launch_wgrad_kernel(wgrad_few_rows_kernel<0, false, OUT_F32>, few_rows_lds_bytes(), kFewBM, kFewBN, q,
+                                 s, 256);
     return (int)ZMOE_ERR_NULL;  // not reached (checked above)
   };
   const int split = big ? wgrad_small_rows(M, E) : 0;
@@ -2485,18 +2516,28 @@ int group_bwd_w_bf16(WgradParams p, int64_t M, int E, int64_t N, int64_t K, hipS
   }
   if (rc) return rc;
   if (!big) return small_tiles(p);
-  if (gather == 1) return launch_wgrad_big<1, false, DYG>(p, s);
-  if (gather == 2) return launch_wgrad_big<2, false, DYG>(p, s);
-  if constexpr (!DYG) return launch_wgrad_big<0, false>(p, s);
+  if (gather == 1) return launch_wgrad_big<1, OUT_F32, DYG>(p, s);
+  if (gather == 2) return launch_wgrad_big<2, OUT_F32, DYG>(p, s);
+  if constexpr (!DYG) return launch_wgrad_big<0, OUT_F32>(p, s);
   return (int)ZMOE_ERR_NULL;  // not reached
+}
+
+// bf16 operands, bf16 or fp32 output (fp32 straight from the accumulators: the grads of
+// fp32 master weights under bf16 autocast)
+template <bool DYG>
+int group_bwd_w_bf16_out(WgradParams p, int64_t M, int E, int64_t N, int64_t K, int out_dtype, hipStream_t s) {
+  return out_dtype == ZMOE_DTYPE_F32 ? group_bwd_w_bf16<DYG, true>(p, M, E, N, K, s)
+                                     : group_bwd_w_bf16<DYG, false>(p, M, E, N, K, s);
 }
 }  // namespace
 
 extern "C" int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m, const int64_t* dy_gather_idxs,
                                           int dy_gather_div, const void* X, int64_t x_stride_m,
                                           const int64_t* expert_offsets, int64_t M, int64_t N, int64_t K, int E,
-                                          int dtype, void* DWt, void* stream) {
+                                          int dtype, int out_dtype, void* DWt, void* stream) {
   ZMOE_REQUIRE(dtype == ZMOE_DTYPE_BF16, ZMOE_ERR_DTYPE, "group_bwd_w_gather_dy: bf16 only (dtype %d)", dtype);
+  ZMOE_REQUIRE(out_dtype == ZMOE_DTYPE_BF16 || out_dtype == ZMOE_DTYPE_F32, ZMOE_ERR_DTYPE,
+               "group_bwd_w_gather_dy: out_dtype %d", out_dtype);
   ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && E >= 1 && E <= kGemmMaxE && dy_gather_div >= 1, ZMOE_ERR_SHAPE,
                "group_bwd_w_gather_dy: bad sizes");
   ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30), ZMOE_ERR_SHAPE, "group_bwd_w_gather_dy: N/K too large");
@@ -2527,15 +2568,19 @@ extern "C" int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m, c
   p.dy_bytes = (uint32_t)dy_span;
   p.x_bytes = (uint32_t)x_span;
   if (M == 0) p.x_rows = nullptr;  // no rows: every expert's tiles write zeros (no gather)
-  return M == 0 ? group_bwd_w_bf16<false>(p, M, E, N, K, as_stream(stream))
-                : group_bwd_w_bf16<true>(p, M, E, N, K, as_stream(stream));
+  return M == 0 ? group_bwd_w_bf16_out<false>(p, M, E, N, K, out_dtype, as_stream(stream))
+                : group_bwd_w_bf16_out<true>(p, M, E, N, K, out_dtype, as_stream(stream));
 }
 
 extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m,
                                 const int64_t* x_gather_idxs, int x_gather_div, const int64_t* expert_offsets,
-                                int64_t M, int64_t N, int64_t K, int E, int dtype, void* DWt, void* Db,
-                                void* stream) {
+                                int64_t M, int64_t N, int64_t K, int E, int dtype, int out_dtype, void* DWt,
+                                void* Db, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "group_bwd_w: dtype %d", dtype);
+  ZMOE_REQUIRE(out_dtype == dtype || (dtype == ZMOE_DTYPE_BF16 && out_dtype == ZMOE_DTYPE_F32), ZMOE_ERR_DTYPE,
+               "group_bwd_w: out_dtype %d with operands of dtype %d (fp32 output of bf16 operands, or the "
+               "operands' dtype)", out_dtype, dtype);
+  ZMOE_REQUIRE(Db == nullptr || out_dtype == dtype, ZMOE_ERR_DTYPE, "group_bwd_w: the bias grad is in DY's dtype");
   ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && E >= 1 && E <= kGemmMaxE && x_gather_div >= 1, ZMOE_ERR_SHAPE,
                "group_bwd_w: bad sizes");
   ZMOE_REQUIRE(N < (1 << 30) && K < (1 << 30), ZMOE_ERR_SHAPE, "group_bwd_w: N/K too large");
@@ -2570,7 +2615,7 @@ extern "C" int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void*
   hipStream_t s = as_stream(stream);
   int rc;
   if (dtype == ZMOE_DTYPE_BF16) {
-    rc = group_bwd_w_bf16<false>(p, M, E, N, K, s);
+    rc = group_bwd_w_bf16_out<false>(p, M, E, N, K, out_dtype, s);
   } else {
     rc = launch_wgrad_kernel(grouped_wgrad_kernel<float, 128, 128>, rows_lds_bytes<float, 128, 128>(), 128, 128, p,
                              s);
@@ -2598,9 +2643,11 @@ extern "C" size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int spl
 }
 
 extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void* X, int64_t x_stride_m, int64_t M,
-                                int64_t N, int64_t K, int dtype, int splits, void* DW, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+                                int64_t N, int64_t K, int dtype, int out_dtype, int splits, void* DW,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "dense_wgrad: dtype %d", dtype);
+  ZMOE_REQUIRE(out_dtype == dtype || (dtype == ZMOE_DTYPE_BF16 && out_dtype == ZMOE_DTYPE_F32), ZMOE_ERR_DTYPE,
+               "dense_wgrad: out_dtype %d with operands of dtype %d", out_dtype, dtype);
   ZMOE_REQUIRE(M >= 0 && N >= 1 && K >= 1 && splits >= 1 && splits <= kDenseMaxSplits, ZMOE_ERR_SHAPE,
                "dense_wgrad: bad sizes (M=%lld N=%lld K=%lld splits=%d)", (long long)M, (long long)N, (long long)K,
                splits);
@@ -2621,8 +2668,8 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
     hipLaunchKernelGGL(split_offsets_kernel, dim3(1), dim3(64), 0, s, off, M, S);
     rc = check_launch("split_offsets_kernel");
     if (rc) return rc;
-    return zmoe_group_bwd_w(DY, dy_stride_m, X, x_stride_m, nullptr, 1, off, M, N, K, 1, dtype, DW, nullptr,
-                            stream);
+    return zmoe_group_bwd_w(DY, dy_stride_m, X, x_stride_m, nullptr, 1, off, M, N, K, 1, dtype, out_dtype, DW,
+                            nullptr, stream);
   }
   WgradParams p{};
   p.dy = DY;
@@ -2648,7 +2695,11 @@ extern "C" int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void*
     rc = launch_wgrad_kernel(wgrad_bf16_kernel<128, 128, 0, true>, bf16_lds_bytes<128, 128>(), 128, 128, p, s);
   if (rc) return rc;
   const int64_t n = N * K;  // multiple of 8
-  hipLaunchKernelGGL(reduce_splits_kernel<uint16_t>, dim3((unsigned)cdiv(n / 4, 256)), dim3(256), 0, s,
-                     reinterpret_cast<const float*>(p.dw), S, n, reinterpret_cast<uint16_t*>(DW));
+  if (out_dtype == ZMOE_DTYPE_F32)
+    hipLaunchKernelGGL(reduce_splits_kernel<float>, dim3((unsigned)cdiv(n / 4, 256)), dim3(256), 0, s,
+                       reinterpret_cast<const float*>(p.dw), S, n, reinterpret_cast<float*>(DW));
+  else
+    hipLaunchKernelGGL(reduce_splits_kernel<uint16_t>, dim3((unsigned)cdiv(n / 4, 256)), dim3(256), 0, s,
+                       reinterpret_cast<const float*>(p.dw), S, n, reinterpret_cast<uint16_t*>(DW));
   return check_launch("reduce_splits_kernel");
 }

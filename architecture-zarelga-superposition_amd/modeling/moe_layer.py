@@ -56,15 +56,27 @@ class _FusedMoELayer(torch.autograd.Function):
     with pad_rows (int64 [T]) the padded [pad_total, d] whose row pad_rows[t] is token t's.
     Every launch is a ``zmoe::`` custom op, so torch.compile traces through the function
     without a graph break.
+
+    The weights and x may be fp32 (the reference's fp32 master weights and residual stream
+    under bf16 autocast, main.py:595, :746): the function then computes on bf16 copies made
+    once per forward (kept for its backward), writes the weight grads in fp32 straight from
+    the kernels' fp32 accumulators (no bf16 grad and no cast pass) and returns x's grad in
+    x's dtype. The output is bf16 either way, as the reference's under autocast.
     """
 
     @staticmethod
     def forward(ctx, x, gate_w, expert_biases, W1, W2, Ws_gate, Ws_up, Ws_down, k: int, E: int, pad_rows=None,
                 pad_total: int = 0):
-        logits = F.linear(x, gate_w)                                                 # moe_gate.py:26
-        idx, w, p = _zl.route_topk(logits, expert_biases, k, logits.dtype == torch.bfloat16)
+        bf = torch.bfloat16
+        ctx.f32_grads = W1.dtype == torch.float32
+        ctx.x_dtype = x.dtype
+        x = x.to(bf)
+        # [up | gate | router] rows in one operand (cast with the concatenation)
+        W3 = torch.cat([Ws_up, Ws_gate, gate_w], dim=0).to(bf)  # [2fs + E, d]; rows :2fs = [up | gate]
+        W1, W2, Ws_down = W1.to(bf), W2.to(bf), Ws_down.to(bf)
         fs = Ws_up.shape[0]
-        W3 = torch.cat([Ws_up, Ws_gate, gate_w], dim=0)     # [2fs + E, d]; rows :2fs = [up | gate]
+        logits = F.linear(x, W3[2 * fs:])                                            # moe_gate.py:26
+        idx, w, p = _zl.route_topk(logits, expert_biases, k, True)
         Hs = F.linear(x, W3[:2 * fs])
         As = _zl.swiglu(Hs)
         S = F.linear(As, Ws_down)                                                    # expert_layer.py:23-24
@@ -87,6 +99,7 @@ class _FusedMoELayer(torch.autograd.Function):
         x, W1, W2, W3, Ws_down, Hs, As, p, idx, w_sorted, se, ss, off, H, A_s, pad_rows = ctx.saved_tensors
         k, E, fs = ctx.k, ctx.E, ctx.fs
         need = ctx.needs_input_grad
+        f32 = ctx.f32_grads  # fp32 weight grads from the accumulators (fp32 master weights)
         dout = dout.to(x.dtype).contiguous()
         # the grad of the combine's inputs: dout for the shared expert's output (the addend),
         # gates * dout[t] for the routed rows, <dout[t], Y> for the gates
@@ -97,17 +110,17 @@ class _FusedMoELayer(torch.autograd.Function):
         dA = _zl.grouped_mm(dS, W2, se, ss, k, False, True, off, "glu_w2_backward_dh")
         dH, d_gates = _zl.swiglu_backward_gates(dA, H, w_sorted, ss)
         d_gates = d_gates.view(-1, k)
-        dW2 = _zl.group_bwd_w_gather_dy(dS, ss, k, A_s, off, E) if need[4] else None     # sum dout[t]^T (w A)
-        dW1 = _zl.group_bwd_w(dH, x, off, E, ss, k) if need[3] else None
+        dW2 = _zl.group_bwd_w_gather_dy(dS, ss, k, A_s, off, E, f32) if need[4] else None  # sum dout[t]^T (w A)
+        dW1 = _zl.group_bwd_w(dH, x, off, E, ss, k, f32) if need[3] else None
         dXe = _zl.grouped_mm(dH, W1, se, ss, 1, True, False, off, "scatter2scatter")
         # shared expert, and the gate projection through the routing's analytic backward:
         # [d up | d gate | d_logits] side by side, one product for both input grads
         dAs = dS @ Ws_down
-        dWs_down = _zl.dense_wgrad(dS, As) if need[7] else None
+        dWs_down = _zl.dense_wgrad(dS, As, f32) if need[7] else None
         G = _zl.swiglu_route_backward(dAs, Hs, d_gates, p, idx, E)
         dx_dense = G @ W3                                   # shared expert + gate input grads
-        dW3 = _zl.dense_wgrad(G, x) if need[1] or need[5] or need[6] else None
-        dx = _zl.sum_k(dXe, k, dx_dense)
+        dW3 = _zl.dense_wgrad(G, x, f32) if need[1] or need[5] or need[6] else None
+        dx = _zl.sum_k(dXe, k, dx_dense).to(ctx.x_dtype)
         part = (lambda a, b: None) if dW3 is None else (lambda a, b: dW3[a:b])
         return (dx, part(2 * fs, 2 * fs + E), None, dW1, dW2, part(fs, 2 * fs), part(0, fs), dWs_down,
                 None, None, None, None)
@@ -146,14 +159,23 @@ class MoELayer(nn.Module):
         nn.init.normal_(self.routed_experts.output_experts.weight, mean=0.0, std=std)
 
     def _fused_weights(self, x):
-        """The layer's weights for _FusedMoELayer, or None where the module composition runs
-        (not bf16 on the device, autocast, the routed experts' unfused path)."""
+        """The layer's weights for _FusedMoELayer, or None where the module composition runs.
+
+        The function runs in bf16 on the device: with bf16 weights and input, or under bf16
+        autocast with fp32 or bf16 weights and input (the reference's training mode: fp32
+        master weights and residual stream, main.py:595, :746). Other cases (fp32 without
+        autocast, the routed experts' unfused path) run the module composition."""
         se = self.shared_experts
         ws = (self.gate.weight, self.routed_experts.experts.weight, self.routed_experts.output_experts.weight,
               se.gate_proj.weight, se.up_proj.weight, se.down_proj.weight)
-        ok = (self.fused_layer and self.routed_experts.fused and not torch.is_autocast_enabled()
-              and x.dim() == 3 and x.is_cuda and x.dtype == torch.bfloat16
-              and all(w.is_cuda and w.dtype == torch.bfloat16 for w in ws)
+        bf, f32 = torch.bfloat16, torch.float32
+        if torch.is_autocast_enabled("cuda"):
+            dtypes_ok = (torch.get_autocast_dtype("cuda") == bf and x.dtype in (bf, f32)
+                         and ws[0].dtype in (bf, f32) and all(w.dtype == ws[0].dtype for w in ws))
+        else:
+            dtypes_ok = x.dtype == bf and all(w.dtype == bf for w in ws)
+        ok = (self.fused_layer and self.routed_experts.fused and dtypes_ok
+              and x.dim() == 3 and x.is_cuda and all(w.is_cuda for w in ws)
               and self.gate.top_k == self.routed_experts.top_k
               and ws[4].shape[0] % 8 == 0 and ws[0].shape[0] % 8 == 0)    # 16-byte rows of the dH | d_logits buffer
         return ws if ok else None

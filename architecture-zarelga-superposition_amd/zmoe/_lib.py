@@ -47,10 +47,10 @@ SIGNATURES = {
     "zmoe_group": (I32, [P, I64, I64, I32, P, I64, I32, P, I32, P, I64, P]),
     "zmoe_scatter2scatter": (I32, [P, I64, P, I64, I64, I64, P, I64, P, P, P, I64, I64, I64, I32, I32, I32, I32,
                                    I32, P, I64, P]),
-    "zmoe_group_bwd_w": (I32, [P, I64, P, I64, P, I32, P, I64, I64, I64, I32, I32, P, P, P]),
-    "zmoe_group_bwd_w_gather_dy": (I32, [P, I64, P, I32, P, I64, P, I64, I64, I64, I32, I32, P, P]),
+    "zmoe_group_bwd_w": (I32, [P, I64, P, I64, P, I32, P, I64, I64, I64, I32, I32, I32, P, P, P]),
+    "zmoe_group_bwd_w_gather_dy": (I32, [P, I64, P, I32, P, I64, P, I64, I64, I64, I32, I32, I32, P, P]),
     "zmoe_dense_wgrad_workspace_bytes": (SZ, [I64, I64, I32]),
-    "zmoe_dense_wgrad": (I32, [P, I64, P, I64, I64, I64, I64, I32, I32, P, P, SZ, P]),
+    "zmoe_dense_wgrad": (I32, [P, I64, P, I64, I64, I64, I64, I32, I32, I32, P, P, SZ, P]),
     "zmoe_rowwise_sum_product": (I32, [P, I32, P, I32, I64, I32, I64, P, I32, P]),
     "zmoe_glu_w1_forward": (I32, [P, I64, P, P, P, P, I64, I64, I64, I32, I32, I32, P, P, P]),
     "zmoe_glu_w1_forward_scaled": (I32, [P, I64, P, P, P, P, I64, I64, I64, I32, I32, I32, P, P, P, P]),
@@ -98,7 +98,7 @@ def load():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.zmoe_abi_version() != 2:
+        if lib.zmoe_abi_version() != 3:
             raise ImportError("libzmoe_hip.so ABI version mismatch")
         _lib = lib
     return _lib

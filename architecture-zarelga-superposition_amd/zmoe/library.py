@@ -129,16 +129,22 @@ def _(dYg, W2, H, sorted_expert_idxs, expert_offsets):
     return _empty(H.shape, dYg)
 
 
+def _wdt(DY: torch.Tensor, out_f32: bool) -> torch.dtype:
+    return torch.float32 if out_f32 else DY.dtype
+
+
 @torch.library.custom_op("zmoe::group_bwd_w", mutates_args=())
 def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor, num_experts: int,
-                x_gather: Optional[torch.Tensor], x_div: int) -> torch.Tensor:
-    """group_bwd_W (ops.py:263-271): DWt [E, N, K] (the parameter layout)."""
-    return _z.group_bwd_w(DY, X, expert_offsets, num_experts, x_gather=x_gather, x_div=x_div)[0]
+                x_gather: Optional[torch.Tensor], x_div: int, out_f32: bool = False) -> torch.Tensor:
+    """group_bwd_W (ops.py:263-271): DWt [E, N, K] (the parameter layout); ``out_f32``: fp32
+    from the accumulators (bf16 operands, fp32 master weights)."""
+    return _z.group_bwd_w(DY, X, expert_offsets, num_experts, x_gather=x_gather, x_div=x_div,
+                          out_dtype=_wdt(DY, out_f32))[0]
 
 
 @group_bwd_w.register_fake
-def _(DY, X, expert_offsets, num_experts, x_gather, x_div):
-    return _empty((num_experts, DY.shape[1], X.shape[1]), DY)
+def _(DY, X, expert_offsets, num_experts, x_gather, x_div, out_f32=False):
+    return _empty((num_experts, DY.shape[1], X.shape[1]), DY, _wdt(DY, out_f32))
 
 
 @torch.library.custom_op("zmoe::group_bwd_w_bias", mutates_args=())
@@ -155,25 +161,26 @@ def _(DY, X, expert_offsets, num_experts, x_gather, x_div):
 
 @torch.library.custom_op("zmoe::group_bwd_w_gather_dy", mutates_args=())
 def group_bwd_w_gather_dy(DY: torch.Tensor, dy_gather: torch.Tensor, dy_div: int, X: torch.Tensor,
-                          expert_offsets: torch.Tensor, num_experts: int) -> torch.Tensor:
+                          expert_offsets: torch.Tensor, num_experts: int, out_f32: bool = False) -> torch.Tensor:
     """Weight grads with DY's rows gathered in the kernel: DWt [E, N, K]."""
-    return _z.group_bwd_w_gather_dy(DY, dy_gather, dy_div, X, expert_offsets, num_experts)
+    return _z.group_bwd_w_gather_dy(DY, dy_gather, dy_div, X, expert_offsets, num_experts,
+                                    out_dtype=_wdt(DY, out_f32))
 
 
 @group_bwd_w_gather_dy.register_fake
-def _(DY, dy_gather, dy_div, X, expert_offsets, num_experts):
-    return _empty((num_experts, DY.shape[1], X.shape[1]), DY)
+def _(DY, dy_gather, dy_div, X, expert_offsets, num_experts, out_f32=False):
+    return _empty((num_experts, DY.shape[1], X.shape[1]), DY, _wdt(DY, out_f32))
 
 
 @torch.library.custom_op("zmoe::dense_wgrad", mutates_args=())
-def dense_wgrad(DY: torch.Tensor, X: torch.Tensor) -> torch.Tensor:
+def dense_wgrad(DY: torch.Tensor, X: torch.Tensor, out_f32: bool = False) -> torch.Tensor:
     """DW [N, K] = DY^T X (the F.linear weight grad, split-K)."""
-    return _z.dense_wgrad(DY, X)
+    return _z.dense_wgrad(DY, X, out_dtype=_wdt(DY, out_f32))
 
 
 @dense_wgrad.register_fake
-def _(DY, X):
-    return _empty((DY.shape[1], X.shape[1]), DY)
+def _(DY, X, out_f32=False):
+    return _empty((DY.shape[1], X.shape[1]), DY, _wdt(DY, out_f32))
 
 
 # ------------------------------------------------------------------ row passes

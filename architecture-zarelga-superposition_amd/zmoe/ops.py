@@ -202,13 +202,23 @@ def scatter2scatter(X: torch.Tensor, W: torch.Tensor, sorted_expert_idxs: torch.
     return out
 
 
+def _wgrad_out_dtype(DY: torch.Tensor, out_dtype: Optional[torch.dtype], what: str) -> torch.dtype:
+    """The weight grad's dtype: DY's (the reference's, ops.py:264-265), or float32 for bf16
+    operands (the fp32 accumulators written unrounded: grads of fp32 master weights)."""
+    od = DY.dtype if out_dtype is None else out_dtype
+    if od != DY.dtype and not (DY.dtype == torch.bfloat16 and od == torch.float32):
+        raise ValueError(f"{what}: out_dtype {od} with {DY.dtype} operands")
+    return od
+
+
 def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor, E: int, has_bias: bool = False,
                 x_gather: Optional[torch.Tensor] = None, x_div: int = 1, out: Optional[torch.Tensor] = None,
-                out_bias: Optional[torch.Tensor] = None):
+                out_bias: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None):
     """scattermoe/kernels/ops.py:263-271 -> (DWt [E, N, K] contiguous, Db [E, N] or None).
 
     ``x_gather`` makes row i of X read X[x_gather[i] // x_div] (no grouped copy).
-    ``out`` / ``out_bias`` may supply the contiguous result buffers.
+    ``out`` / ``out_bias`` may supply the contiguous result buffers. ``out_dtype``
+    float32 with bf16 operands: DWt unrounded from the fp32 accumulators (no bias grad).
     """
     dev = _require_cuda(DY, X, expert_offsets, x_gather)
     DY = _rows(DY)
@@ -224,8 +234,11 @@ def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor,
             raise ValueError("group_bwd_w: x_gather must have DY.size(0) entries")
     elif X.shape[0] != M:
         raise ValueError("group_bwd_w: X and DY row counts differ")
-    DWt = torch.empty((E, N, K), dtype=DY.dtype, device=dev) if out is None else out
-    if DWt.shape != (E, N, K) or DWt.dtype != DY.dtype or not DWt.is_contiguous():
+    od = _wgrad_out_dtype(DY, out_dtype, "group_bwd_w")
+    if has_bias and od != DY.dtype:
+        raise ValueError("group_bwd_w: the bias grad comes in DY's dtype only")
+    DWt = torch.empty((E, N, K), dtype=od, device=dev) if out is None else out
+    if DWt.shape != (E, N, K) or DWt.dtype != od or not DWt.is_contiguous():
         raise ValueError("group_bwd_w: bad out tensor")
     Db = None
     if has_bias:
@@ -235,14 +248,15 @@ def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor,
     off = _idx64(expert_offsets)
     with profiling.region("group_bwd_w", dev):
         L.call("zmoe_group_bwd_w", _ptr(DY), DY.stride(0), _ptr(X), X.stride(0), _ptr(g), x_div, _ptr(off), M, N, K,
-               E, _dtype_code(DY), _ptr(DWt), _ptr(Db), _stream(dev))
+               E, _dtype_code(DY), _DT[od], _ptr(DWt), _ptr(Db), _stream(dev))
     return DWt, Db
 
 
 def group_bwd_w_gather_dy(DY: torch.Tensor, dy_gather: torch.Tensor, dy_div: int, X: torch.Tensor,
-                          expert_offsets: torch.Tensor, E: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          expert_offsets: torch.Tensor, E: int, out: Optional[torch.Tensor] = None,
+                          out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """group_bwd_w with the gather on DY (bf16): sorted row i of DY is DY[dy_gather[i] // dy_div],
-    X [R, K] in sorted order. Returns DWt [E, N, K]."""
+    X [R, K] in sorted order. Returns DWt [E, N, K] (bf16, or float32 with ``out_dtype``)."""
     dev = _require_cuda(DY, dy_gather, X, expert_offsets)
     DY = _rows(DY)
     X = _rows(X)
@@ -253,13 +267,14 @@ def group_bwd_w_gather_dy(DY: torch.Tensor, dy_gather: torch.Tensor, dy_div: int
     N = DY.shape[1]
     if g.numel() != M or DY.shape[0] * dy_div < M:
         raise ValueError("group_bwd_w_gather_dy: dy_gather must have X.size(0) entries, into DY's rows")
-    DWt = torch.empty((E, N, K), dtype=DY.dtype, device=dev) if out is None else out
-    if DWt.shape != (E, N, K) or DWt.dtype != DY.dtype or not DWt.is_contiguous():
+    od = _wgrad_out_dtype(DY, out_dtype, "group_bwd_w_gather_dy")
+    DWt = torch.empty((E, N, K), dtype=od, device=dev) if out is None else out
+    if DWt.shape != (E, N, K) or DWt.dtype != od or not DWt.is_contiguous():
         raise ValueError("group_bwd_w_gather_dy: bad out tensor")
     off = _idx64(expert_offsets)
     with profiling.region("group_bwd_w", dev):
         L.call("zmoe_group_bwd_w_gather_dy", _ptr(DY), DY.stride(0), _ptr(g), int(dy_div), _ptr(X), X.stride(0),
-               _ptr(off), M, N, K, E, _dtype_code(DY), _ptr(DWt), _stream(dev))
+               _ptr(off), M, N, K, E, _dtype_code(DY), _DT[od], _ptr(DWt), _stream(dev))
     return DWt
 
 
@@ -283,8 +298,9 @@ def dense_wgrad_splits(M: int, N: int, K: int, cus: int = 256) -> int:
 
 
 def dense_wgrad(DY: torch.Tensor, X: torch.Tensor, splits: Optional[int] = None,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """DW [N, K] = DY[M, N]^T X[M, K]: the weight grad of an nn.Linear (F.linear backward)."""
+                out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """DW [N, K] = DY[M, N]^T X[M, K]: the weight grad of an nn.Linear (F.linear backward);
+    ``out_dtype`` float32 with bf16 operands writes the fp32 sum unrounded."""
     dev = _require_cuda(DY, X)
     DY = _rows(DY)
     X = _rows(X)
@@ -294,14 +310,15 @@ def dense_wgrad(DY: torch.Tensor, X: torch.Tensor, splits: Optional[int] = None,
     K = X.shape[1]
     if splits is None:
         splits = dense_wgrad_splits(M, N, K)
-    DW = torch.empty((N, K), dtype=DY.dtype, device=dev) if out is None else out
-    if DW.shape != (N, K) or DW.dtype != DY.dtype or not DW.is_contiguous():
+    od = _wgrad_out_dtype(DY, out_dtype, "dense_wgrad")
+    DW = torch.empty((N, K), dtype=od, device=dev) if out is None else out
+    if DW.shape != (N, K) or DW.dtype != od or not DW.is_contiguous():
         raise ValueError("dense_wgrad: bad out tensor")
     nbytes = L.load().zmoe_dense_wgrad_workspace_bytes(N, K, splits if DY.dtype == torch.bfloat16 else 0)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     with profiling.region("dense_wgrad", dev):
-        L.call("zmoe_dense_wgrad", _ptr(DY), DY.stride(0), _ptr(X), X.stride(0), M, N, K, _dtype_code(DY), splits,
-               _ptr(DW), _ptr(ws), nbytes, _stream(dev))
+        L.call("zmoe_dense_wgrad", _ptr(DY), DY.stride(0), _ptr(X), X.stride(0), M, N, K, _dtype_code(DY), _DT[od],
+               splits, _ptr(DW), _ptr(ws), nbytes, _stream(dev))
     return DW
 
 

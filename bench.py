@@ -129,7 +129,9 @@ def zipf_bias(logits, k: int, s: float = 1.1, seed: int = 0):
     return (best * base).to(logits.device), best, ks(best)
 
 
-def build_layer(T, d, E, k, f, fs, dev, seed=0):
+def build_layer(T, d, E, k, f, fs, dev, seed=0, fp32_params=False):
+    """The MoE layer at the workload's shape: bf16 parameters, or with ``fp32_params`` fp32
+    master weights (run under bf16 autocast, the reference's training mode)."""
     import torch
 
     from modeling.model_config import ModelConfig
@@ -141,7 +143,9 @@ def build_layer(T, d, E, k, f, fs, dev, seed=0):
     torch.manual_seed(seed)
     cfg = ModelConfig(hidden_size=d, intermediate_size=f, n_experts=E + ns, n_shared_experts=ns,
                       n_experts_per_token=k)
-    layer = MoELayer(cfg).to(dev).to(torch.bfloat16)
+    layer = MoELayer(cfg).to(dev)
+    if not fp32_params:
+        layer = layer.to(torch.bfloat16)
     layer.gate.expert_biases.data = layer.gate.expert_biases.data.float()
     return layer
 
@@ -403,6 +407,10 @@ def main(argv=None):
     ap.add_argument("--muon", action="store_true",
                     help="time the MuonMD Newton-Schulz step on the C3 routed-expert stacks instead of the layer")
     ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 --pmc CSVs under DIR and exit")
+    ap.add_argument("--autocast-fp32-params", action="store_true",
+                    help="the reference's training mode (main.py:595, :746): fp32 master weights and an fp32 "
+                         "input under torch.autocast(bf16); the step includes the weights' bf16 copies and "
+                         "writes fp32 weight grads")
     args = ap.parse_args(argv)
     if args.pmc_summary:
         return pmc_summary(args.pmc_summary)
@@ -424,32 +432,37 @@ def main(argv=None):
     T, d, E, k, f, fs, backward = WORKLOADS[args.workload]
     if args.tokens:
         T = args.tokens
-    layer = build_layer(T, d, E, k, f, fs, dev)
+    amp = args.autocast_fp32_params
+    layer = build_layer(T, d, E, k, f, fs, dev, fp32_params=amp)
     # the reference layer always runs a shared expert; n_shared_experts = 0 gives width f
     fs = layer.shared_experts.intermediate_size
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
-    x = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16).requires_grad_(backward)
+    x = torch.randn(1, T, d, device=dev, generator=g)
+    x = (x if amp else x.to(torch.bfloat16)).requires_grad_(backward)   # fp32 residual stream under autocast
     dout = torch.randn(1, T, d, device=dev, generator=g).to(torch.bfloat16)
     skew = None
     if args.workload == "c4":  # Zipf(1.1)-skewed expert popularity through the selection bias
         with torch.no_grad():
-            logits = torch.nn.functional.linear(x.detach().view(T, d), layer.gate.weight)
+            logits = torch.nn.functional.linear(x.detach().view(T, d).to(torch.bfloat16),
+                                                layer.gate.weight.to(torch.bfloat16))
         bias, c, ks = zipf_bias(logits, k)
         layer.gate.expert_biases.data = bias
         skew = {"zipf_s": 1.1, "bias_scale": c, "ks_distance": ks}
     params = list(layer.parameters())
 
     def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+            if backward:
+                for p in params:
+                    p.grad = None
+                x.grad = None
+                out, _ = layer(x)
+            else:
+                with torch.no_grad():
+                    layer(x)
         if backward:
-            for p in params:
-                p.grad = None
-            x.grad = None
-            out, _ = layer(x)
             out.backward(dout)
-        else:
-            with torch.no_grad():
-                layer(x)
 
     for _ in range(args.warmup):
         step()
@@ -548,6 +561,8 @@ def main(argv=None):
                          f"k={k} SwiGLU f={f} + shared SwiGLU {fs}"),
             "tokens": T, "d_model": d, "experts": E, "top_k": k, "ffn": f, "shared_ffn": fs,
             "parallelism": "single GPU",
+            "params": ("fp32 master weights, fp32 input, under torch.autocast(bf16): bf16 compute copies made "
+                       "each forward, fp32 weight grads" if amp else "bf16"),
             **({"routing_skew": skew} if skew else {}),
         },
         "grouped_gemm_mfma_util_pct": 100.0 * util,

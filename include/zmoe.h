@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define ZMOE_ABI_VERSION 2
+#define ZMOE_ABI_VERSION 3
 
 /* element types */
 enum { ZMOE_DTYPE_F32 = 0, ZMOE_DTYPE_BF16 = 1 };
@@ -48,8 +48,10 @@ const char* zmoe_last_error(void);
  * modeling/moe_gate.py:27-34 (sigmoid, +expert_biases, topk, gather,
  * F.normalize(p=1)).
  *   logits [T, E] (row stride E), dtype F32 or BF16; expert_biases [E] f32.
- *   p = fp32(sigmoid_f64(logit)); if round_probs_bf16, p = bf16(p) (the
- *   reference under bf16 autocast). s = p + bias. Slots ordered by
+ *   p = sigmoid(logit) correctly rounded to fp32, 0 for logits at or below
+ *   -88.72283935546875 (where torch's fp32 exp(-z) overflows and its sigmoid
+ *   returns 0); if round_probs_bf16, p = bf16(p) (the reference under bf16
+ *   autocast). s = p + bias. Slots ordered by
  *   (s desc, expert asc); NaN ranks above all numbers.
  *   Outputs: topk_idx [T, k] int64, topk_weight [T, k] f32 =
  *   p_sel / max(sum p_sel, 1e-12), topk_prob [T, k] f32 = p_sel (may be NULL).
@@ -159,12 +161,15 @@ int zmoe_scatter2scatter(const void* X, int64_t x_stride_m, const void* W,
  *   (the gather replaces the reference's group() copy, parallel_experts.py:102).
  * DWt [E, N, K] contiguous = the reference's DWt (its DW is DWt.permute(0,2,1));
  * experts with no rows get exact zeros. Db [E, N] (may be NULL) = row sums.
+ * out_dtype: DWt's element type, `dtype` (the reference's, ops.py:264-265) or
+ * F32 for BF16 operands: the fp32 accumulators written unrounded, the grads of
+ * fp32 master weights under bf16 autocast (Db then NULL).
  * ------------------------------------------------------------------------- */
 int zmoe_group_bwd_w(const void* DY, int64_t dy_stride_m, const void* X,
                      int64_t x_stride_m, const int64_t* x_gather_idxs,
                      int x_gather_div, const int64_t* expert_offsets, int64_t M,
-                     int64_t N, int64_t K, int E, int dtype, void* DWt, void* Db,
-                     void* stream);
+                     int64_t N, int64_t K, int E, int dtype, int out_dtype, void* DWt,
+                     void* Db, void* stream);
 
 /* The same with the gather on DY's rows instead (parallel_experts.py:102 applied to
  * the output grad; bf16 only): DYrow(i) = DY[dy_gather_idxs[i] / dy_gather_div],
@@ -174,7 +179,8 @@ int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m,
                                const int64_t* dy_gather_idxs, int dy_gather_div,
                                const void* X, int64_t x_stride_m,
                                const int64_t* expert_offsets, int64_t M, int64_t N,
-                               int64_t K, int E, int dtype, void* DWt, void* stream);
+                               int64_t K, int E, int dtype, int out_dtype, void* DWt,
+                               void* stream);
 
 /* ---------------------------------------------------------------------------
  * Dense weight gradient DW[N, K] = DY^T X over M rows (DY [M, N], X [M, K]), for
@@ -185,12 +191,13 @@ int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m,
  * split into `splits` ranges computed by the grouped wgrad kernel into fp32
  * partials, then summed in a fixed order and rounded once (deterministic).
  * workspace: zmoe_dense_wgrad_workspace_bytes(N, K, splits) bytes, 16-byte
- * aligned. fp32 runs unsplit.
+ * aligned. fp32 runs unsplit. out_dtype: `dtype`, or F32 for BF16 operands
+ * (the fp32 sum written unrounded: fp32 master weights under bf16 autocast).
  * ------------------------------------------------------------------------- */
 size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int splits);
 int zmoe_dense_wgrad(const void* DY, int64_t dy_stride_m, const void* X,
                      int64_t x_stride_m, int64_t M, int64_t N, int64_t K,
-                     int dtype, int splits, void* DW, void* workspace,
+                     int dtype, int out_dtype, int splits, void* DW, void* workspace,
                      size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -495,7 +495,7 @@ def summand_rss(sum_of_products, a, b):
     return np.sqrt(sum_of_products(np.asarray(a, dtype=_f()) ** 2, np.asarray(b, dtype=_f()) ** 2))
 
 
-def glu_mlp_backward(dy, cache, rss=False):
+def glu_mlp_backward(dy, cache, rss=False, round_wgrads=True):
     """Autograd of GLUMLP (mlp.py:74-95 through parallel_experts.py:70-135), at the
     rounding points of ``glu_mlp_forward``'s ``store``.
 
@@ -503,10 +503,12 @@ def glu_mlp_backward(dy, cache, rss=False):
     the per-slot input grads, parallel_experts.py:125) and d_gates (fp32 in the path) are
     not rounded: the caller adds its other input-grad terms before the one rounding.
     With ``rss=True`` a fifth item maps "W1", "W2", "d_gates" to the root-sum-square of
-    each element's summands (``summand_rss``).
+    each element's summands (``summand_rss``). ``round_wgrads=False`` leaves dW1 and dW2
+    unrounded (fp32 grads of fp32 master weights, summed over the stored summands).
     """
     c = cache
     r = storage_rounder(c["store"])
+    rw = r if round_wgrads else storage_rounder(None)
     dy = np.asarray(dy, dtype=_f())
     se, ss, off, k = c["se"], c["ss"], c["off"], c["k"]
     E = c["W1l"].shape[0]
@@ -532,7 +534,7 @@ def glu_mlp_backward(dy, cache, rss=False):
     W1t = np.transpose(c["W1l"], (0, 2, 1))
     dXe = r(scatter2scatter(dH, W1t, se, ss, 1, x_grouped=True, y_grouped=False))
     dx = dXe.reshape(T, k, -1).sum(axis=1)                                     # :125
-    out = (dx, r(np.transpose(dW1l, (0, 2, 1))), r(np.transpose(dW2l, (0, 2, 1))), d_gates)
+    out = (dx, rw(np.transpose(dW1l, (0, 2, 1))), rw(np.transpose(dW2l, (0, 2, 1))), d_gates)
     if not rss:
         return out
     wsum = lambda a, b: group_bwd_w(a, b, off, E)[0]  # noqa: E731
@@ -560,23 +562,24 @@ def shared_expert_forward(x, Wg, Wu, Wd, store=None):
     return r(a @ np.asarray(Wd, dtype=_f()).T), (x, g, u, a)
 
 
-def shared_expert_backward(dy, cache, Wg, Wu, Wd, store=None, rss=False):
+def shared_expert_backward(dy, cache, Wg, Wu, Wd, store=None, rss=False, round_wgrads=True):
     """Returns (dx, dWg, dWu, dWd); dx is not rounded (the caller adds its other terms).
     With ``rss=True`` a fifth item maps "gate", "up", "down" to the weight grads'
-    summand root-sum-squares."""
+    summand root-sum-squares. ``round_wgrads=False`` leaves the weight grads unrounded."""
     r = storage_rounder(store)
+    rw = r if round_wgrads else storage_rounder(None)
     x, g, u, a = cache
     dy = np.asarray(dy, dtype=_f())
     Wg = np.asarray(Wg, dtype=_f())
     Wu = np.asarray(Wu, dtype=_f())
     Wd = np.asarray(Wd, dtype=_f())
-    dWd = r(dy.T @ a)
+    dWd = rw(dy.T @ a)
     da = r(dy @ Wd)
     s = 1.0 / (1.0 + np.exp(-g))
     du = r(da * g * s)
     dg = r(da * u * s * (1.0 + g * (1.0 - s)))
     dx = dg @ Wg + du @ Wu
-    out = (dx, r(dg.T @ x), r(du.T @ x), dWd)
+    out = (dx, rw(dg.T @ x), rw(du.T @ x), dWd)
     if not rss:
         return out
     tsum = lambda a, b: a.T @ b  # noqa: E731
@@ -605,11 +608,13 @@ class MoELayerOracle:
     and shared-expert input grads are formed by one product and rounded, then added to
     the routed k-sum and rounded once more; with ``"Y"`` (the module composition) the
     three terms are summed and rounded once (autograd's accumulation order is not
-    modelled; it moves the result by at most an ulp or two).
+    modelled; it moves the result by at most an ulp or two). ``f32_weight_grads``: the
+    weight grads (gate, routed, shared) are left unrounded, as the path writes them for
+    fp32 master weights under bf16 autocast; everything else rounds as ``store`` says.
     """
 
     def __init__(self, Wgate, expert_biases, W1, W2, k, shared=None, round_probs_bf16=False, store=None,
-                 gate_scale_on="Y", expert_ids=None):
+                 gate_scale_on="Y", expert_ids=None, f32_weight_grads=False):
         """``expert_ids`` (sorted, optional): W1 and W2 hold only these experts' weights
         (a compact stack for checks on a few tokens of a wide layer); the routing still
         runs over all gate rows, and tokens must select only these experts. dW1 / dW2
@@ -624,6 +629,7 @@ class MoELayerOracle:
         self.round_probs_bf16 = round_probs_bf16
         self.store = store
         self.gate_scale_on = gate_scale_on
+        self.round_wgrads = not f32_weight_grads
 
     def forward(self, x, logits=None):
         x = np.asarray(x, dtype=_f())
@@ -651,16 +657,18 @@ class MoELayerOracle:
         r = storage_rounder(self.store)
         c = self._cache
         dout = np.asarray(dout, dtype=_f())
-        res = glu_mlp_backward(dout, c["mcache"], rss=rss)
+        res = glu_mlp_backward(dout, c["mcache"], rss=rss, round_wgrads=self.round_wgrads)
         dx_routed, dW1, dW2, d_gates = res[:4]
         E = self.Wgate.shape[0]
         dz = r(route_topk_backward(d_gates, c["p_sel"], c["idx"], E))
-        grads = {"gate_weight": r(dz.T @ c["x"])}
+        rw = r if self.round_wgrads else storage_rounder(None)
+        grads = {"gate_weight": rw(dz.T @ c["x"])}
         if rss:
             grads["rss"] = dict(res[4], gate_weight=summand_rss(lambda a, b: a.T @ b, dz, c["x"]))
         dx_dense = dz @ self.Wgate
         if self.shared is not None:
-            sres = shared_expert_backward(dout, c["scache"], *self.shared, store=self.store, rss=rss)
+            sres = shared_expert_backward(dout, c["scache"], *self.shared, store=self.store, rss=rss,
+                                          round_wgrads=self.round_wgrads)
             dxs, dWg, dWu, dWd = sres[:4]
             dx_dense = dx_dense + dxs
             grads.update(shared_gate=dWg, shared_up=dWu, shared_down=dWd)

@@ -43,7 +43,7 @@ def test_pure_host_entry_points():
     from zmoe import _lib
 
     lib = _lib.load()
-    assert lib.zmoe_abi_version() == 2
+    assert lib.zmoe_abi_version() == 3
     assert lib.zmoe_status_string(0) == b"ok"
     assert lib.zmoe_status_string(4) == b"misaligned pointer or stride"
     # workspace sizing is host arithmetic: header + one int32 per (tile, bucket)
@@ -112,7 +112,7 @@ def test_dense_wgrad_workspace_holds_every_split_offset():
     assert lib.zmoe_dense_wgrad_workspace_bytes(8, 256, 64) == hdr + 64 * 8 * 256 * 4
     # more than 64 splits is refused before any launch
     p = ctypes.c_void_p(256)
-    rc = lib.zmoe_dense_wgrad(p, 8, p, 256, 65536, 8, 256, 1, 65, p, p, 1 << 30, None)
+    rc = lib.zmoe_dense_wgrad(p, 8, p, 256, 65536, 8, 256, 1, 1, 65, p, p, 1 << 30, None)
     assert rc == 2
 
 

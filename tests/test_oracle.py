@@ -688,6 +688,29 @@ def test_bf16_store_matches_torch_bf16_arithmetic(gate_scale_on, seed):
         assert eb <= 0.25 * ee, (name, eb, ee)
 
 
+@pytest.mark.parametrize("gate_scale_on", ["Y", "A"])
+def test_f32_weight_grads_are_the_unrounded_bf16_store_grads(gate_scale_on):
+    """f32_weight_grads leaves the weight grads unrounded and changes nothing else: rounding
+    them to bf16 gives the bf16 storage model's grads bit for bit (that mode is pinned against
+    torch's bf16 arithmetic above), the other grads and the output are identical, and the
+    unrounded grads are not already bf16 values."""
+    P = _bf16_inputs(41)
+    kw = dict(shared=P["shared"], round_probs_bf16=True, store="bf16", gate_scale_on=gate_scale_on)
+    got = {}
+    for f32 in (False, True):
+        orc = O.MoELayerOracle(P["Wg"], P["bias"], P["W1"], P["W2"], P["k"], f32_weight_grads=f32, **kw)
+        out, idx, _ = orc.forward(P["x"], logits=P["logits"])
+        got[f32] = (out, idx, orc.backward(P["dy"]))
+    np.testing.assert_array_equal(got[True][0], got[False][0])
+    np.testing.assert_array_equal(got[True][1], got[False][1])
+    g32, g16 = got[True][2], got[False][2]
+    for name in ("gate_weight", "W1", "W2", "shared_gate", "shared_up", "shared_down"):
+        np.testing.assert_array_equal(O.bf16_round(g32[name].astype(np.float32)), g16[name], err_msg=name)
+        assert np.mean(O.bf16_round(g32[name].astype(np.float32)) != g32[name]) > 0.5, name
+    for name in ("x", "d_gates", "d_logits"):
+        np.testing.assert_array_equal(g32[name], g16[name], err_msg=name)
+
+
 def test_bf16_store_shared_expert_matches_torch():
     P = _bf16_inputs(33)
     bf = torch.bfloat16
