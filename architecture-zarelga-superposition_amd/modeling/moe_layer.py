@@ -60,8 +60,9 @@ class _FusedMoELayer(torch.autograd.Function):
     The weights and x may be fp32 (the reference's fp32 master weights and residual stream
     under bf16 autocast, main.py:595, :746): the function then computes on bf16 copies made
     once per forward (kept for its backward), writes the weight grads in fp32 straight from
-    the kernels' fp32 accumulators (no bf16 grad and no cast pass) and returns x's grad in
-    x's dtype. The output is bf16 either way, as the reference's under autocast.
+    the kernels' fp32 accumulators (no bf16 grad and no cast pass) and returns x's grad as
+    the k-sum pass's fp32 sum. The output is bf16 either way, as the reference's under
+    autocast.
     """
 
     @staticmethod
@@ -70,10 +71,12 @@ class _FusedMoELayer(torch.autograd.Function):
         bf = torch.bfloat16
         ctx.f32_grads = W1.dtype == torch.float32
         ctx.x_dtype = x.dtype
-        x = x.to(bf)
+        # bf16 compute copies of fp32 operands (one HIP pass each)
+        cast = lambda t: t if t.dtype == bf else _zl.cast_bf16(t)  # noqa: E731
+        x, W1, W2 = cast(x), cast(W1), cast(W2)
         # [up | gate | router] rows in one operand (cast with the concatenation)
         W3 = torch.cat([Ws_up, Ws_gate, gate_w], dim=0).to(bf)  # [2fs + E, d]; rows :2fs = [up | gate]
-        W1, W2, Ws_down = W1.to(bf), W2.to(bf), Ws_down.to(bf)
+        Ws_down = Ws_down.to(bf)
         fs = Ws_up.shape[0]
         logits = F.linear(x, W3[2 * fs:])                                            # moe_gate.py:26
         idx, w, p = _zl.route_topk(logits, expert_biases, k, True)
@@ -120,7 +123,7 @@ class _FusedMoELayer(torch.autograd.Function):
         G = _zl.swiglu_route_backward(dAs, Hs, d_gates, p, idx, E)
         dx_dense = G @ W3                                   # shared expert + gate input grads
         dW3 = _zl.dense_wgrad(G, x, f32) if need[1] or need[5] or need[6] else None
-        dx = _zl.sum_k(dXe, k, dx_dense).to(ctx.x_dtype)
+        dx = _zl.sum_k(dXe, k, dx_dense, ctx.x_dtype == torch.float32)  # fp32 input: the fp32 sum
         part = (lambda a, b: None) if dW3 is None else (lambda a, b: dW3[a:b])
         return (dx, part(2 * fs, 2 * fs + E), None, dW1, dW2, part(fs, 2 * fs), part(0, fs), dWs_down,
                 None, None, None, None)

@@ -61,7 +61,8 @@ SIGNATURES = {
     "zmoe_combine_backward": (I32, [P, P, P, P, I64, I32, I64, I32, P, P, P]),
     "zmoe_combine_rows": (I32, [P, P, P, I64, I32, I64, I32, P, I64, P, P]),
     "zmoe_combine_backward_rows": (I32, [P, P, P, I64, P, P, I64, I32, I64, I32, P, P, P]),
-    "zmoe_sum_k": (I32, [P, I64, I32, I64, I32, P, P, P, P]),
+    "zmoe_sum_k": (I32, [P, I64, I32, I64, I32, P, P, I32, P, P]),
+    "zmoe_cast_f32_bf16": (I32, [P, I64, P, P]),
     "zmoe_swiglu": (I32, [P, I64, I64, I32, P, P]),
     "zmoe_swiglu_backward": (I32, [P, P, I64, I64, I32, P, I64, P]),
     "zmoe_swiglu_backward_gates": (I32, [P, P, I64, I64, P, P, I32, P, P, P]),

@@ -213,14 +213,26 @@ def _(Y, grad_out, gates, inverse, grad_rows):
 
 
 @torch.library.custom_op("zmoe::sum_k", mutates_args=())
-def sum_k(Xe: torch.Tensor, k: int, add0: Optional[torch.Tensor]) -> torch.Tensor:
-    """out[t] = sum_j Xe[t*k + j] (+ add0[t]) (parallel_experts.py:125)."""
-    return _z.sum_k(Xe, k, add0=add0)
+def sum_k(Xe: torch.Tensor, k: int, add0: Optional[torch.Tensor], out_f32: bool = False) -> torch.Tensor:
+    """out[t] = sum_j Xe[t*k + j] (+ add0[t]) (parallel_experts.py:125); ``out_f32``: the fp32
+    sum unrounded."""
+    return _z.sum_k(Xe, k, add0=add0, out_dtype=torch.float32 if out_f32 else None)
 
 
 @sum_k.register_fake
-def _(Xe, k, add0):
-    return _empty((Xe.shape[0] // k, Xe.shape[1]), Xe)
+def _(Xe, k, add0, out_f32=False):
+    return _empty((Xe.shape[0] // k, Xe.shape[1]), Xe, torch.float32 if out_f32 else None)
+
+
+@torch.library.custom_op("zmoe::cast_bf16", mutates_args=())
+def cast_bf16(src: torch.Tensor) -> torch.Tensor:
+    """The bf16 compute copy of an fp32 tensor (fp32 master weights under bf16 autocast)."""
+    return _z.cast_bf16(src).clone() if src.dtype == torch.bfloat16 else _z.cast_bf16(src)
+
+
+@cast_bf16.register_fake
+def _(src):
+    return _empty(src.shape, src, torch.bfloat16)
 
 
 @torch.library.custom_op("zmoe::swiglu", mutates_args=())

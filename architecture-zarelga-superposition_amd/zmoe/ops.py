@@ -451,17 +451,37 @@ def combine_backward(Y: Optional[torch.Tensor], grad_out: torch.Tensor, gates: t
 
 
 def sum_k(Xe: torch.Tensor, k: int, add0: Optional[torch.Tensor] = None,
-          add1: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out[t] = sum_j Xe[t*k + j] (+ add0[t] + add1[t])."""
+          add1: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """out[t] = sum_j Xe[t*k + j] (+ add0[t] + add1[t]), summed in fp32; ``out_dtype`` float32
+    with bf16 rows writes the sum unrounded."""
     dev = _require_cuda(Xe, add0, add1)
     Xe = Xe.contiguous()
     d = Xe.shape[-1]
     T = Xe.numel() // (d * k)
+    od = Xe.dtype if out_dtype is None else out_dtype
+    if od != Xe.dtype and not (Xe.dtype == torch.bfloat16 and od == torch.float32):
+        raise ValueError(f"sum_k: out_dtype {od} with {Xe.dtype} rows")
     a0 = None if add0 is None else add0.reshape(T, d).to(Xe.dtype).contiguous()
     a1 = None if add1 is None else add1.reshape(T, d).to(Xe.dtype).contiguous()
-    out = torch.empty((T, d), dtype=Xe.dtype, device=dev)
+    out = torch.empty((T, d), dtype=od, device=dev)
     with profiling.region("sum_k", dev):
-        L.call("zmoe_sum_k", _ptr(Xe), T, k, d, _dtype_code(Xe), _ptr(a0), _ptr(a1), _ptr(out), _stream(dev))
+        L.call("zmoe_sum_k", _ptr(Xe), T, k, d, _dtype_code(Xe), _ptr(a0), _ptr(a1), _DT[od], _ptr(out),
+               _stream(dev))
+    return out
+
+
+def cast_bf16(src: torch.Tensor) -> torch.Tensor:
+    """The bf16 copy of an fp32 tensor (round to nearest even), as ``src.to(torch.bfloat16)``,
+    in one HIP pass; a bf16 tensor is returned as it is."""
+    if src.dtype == torch.bfloat16:
+        return src
+    dev = _require_cuda(src)
+    if src.dtype != torch.float32:
+        raise ValueError(f"cast_bf16: float32 input expected, got {src.dtype}")
+    src = src.contiguous()
+    out = torch.empty(src.shape, dtype=torch.bfloat16, device=dev)
+    with profiling.region("cast_bf16", dev):
+        L.call("zmoe_cast_f32_bf16", _ptr(src), src.numel(), _ptr(out), _stream(dev))
     return out
 
 

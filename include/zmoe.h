@@ -299,9 +299,16 @@ int zmoe_combine_backward_rows(const void* Y, const void* grad_out, const int64_
 
 /* scattermoe/parallel_experts.py:125 (d_expanded_input.view(T,k,d).sum(-2))
  * plus up to two addends (gate and shared-expert input grads):
- *   out[t, :] = sum_j Xe[t*k + j, :] + add0[t, :] + add1[t, :]               */
+ *   out[t, :] = sum_j Xe[t*k + j, :] + add0[t, :] + add1[t, :]
+ * summed in fp32; out_dtype `dtype`, or F32 for BF16 rows (the sum unrounded: the
+ * input grad of an fp32 residual stream under bf16 autocast).                 */
 int zmoe_sum_k(const void* Xe, int64_t T, int k, int64_t d, int dtype,
-               const void* add0, const void* add1, void* out, void* stream);
+               const void* add0, const void* add1, int out_dtype, void* out, void* stream);
+
+/* The bf16 compute copy of fp32 master weights (the cast torch autocast applies to
+ * fp32 parameters, main.py:595, :746): dst[i] = bf16(src[i]), round to nearest
+ * even, NaN kept. src and dst 16-byte aligned. */
+int zmoe_cast_f32_bf16(const float* src, int64_t n, void* dst, void* stream);
 
 /* scattermoe/mlp.py:86 stand-alone (shapes the fused kernels reject):
  * A = silu(H[:, f:]) * H[:, :f]; and its backward dH from (dA, H), rows of dH

@@ -104,8 +104,9 @@ def test_layer_autocast_fp32_master_weights(hip_device, param_dtype, with_norm, 
 
 def test_layer_autocast_matches_bf16_layer(hip_device):
     """Under autocast with fp32 weights the layer's forward equals the pure-bf16 layer built
-    from the rounded weights bit for bit (same kernels on the same bf16 operands), and its fp32
-    weight grads round to the bf16 layer's grads but for rare accumulation flips."""
+    from the rounded weights bit for bit (same kernels on the same bf16 operands); its fp32
+    input grad is the same fp32 k-sum unrounded, and its fp32 weight grads round to the bf16
+    layer's grads but for rare accumulation flips."""
     from modeling.model_config import ModelConfig
     from modeling.moe_layer import MoELayer
 
@@ -130,7 +131,7 @@ def test_layer_autocast_matches_bf16_layer(hip_device):
     o16, i16 = l16(x16)
     o16.backward(dout)
     assert torch.equal(i32, i16) and torch.equal(o32, o16)
-    assert torch.equal(x32.grad, x16.grad.float())
+    assert x32.grad.dtype == torch.float32 and torch.equal(x32.grad.to(torch.bfloat16), x16.grad)
     for (n, p32), (_, p16) in zip(l32.named_parameters(), l16.named_parameters()):
         r = p32.grad.to(torch.bfloat16)
         same = (r == p16.grad).float().mean().item()

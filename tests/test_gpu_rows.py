@@ -81,6 +81,46 @@ def test_sum_k_and_rowwise(hip_device, dtype):
     assert_close(rs.cpu().numpy(), O.rowwise_sum_product(np64(A), np64(B)), rtol=1e-5, atol=1e-5, what="rowwise")
 
 
+@pytest.mark.parametrize("k", [8, 3])
+def test_sum_k_fp32_out_of_bf16_rows(hip_device, k):
+    """bf16 rows summed into fp32 output (the input grad of an fp32 residual stream): the fp32
+    sum unrounded, within fp32 rounding of the float64 sum; its bf16 rounding is the bf16-output
+    launch's result bit for bit."""
+    from zmoe import ops
+
+    T, d = 301, 768
+    g = gen(19 + k)
+    Xe = torch.randn(T * k, d, generator=g).to(torch.bfloat16).to(hip_device)
+    a0 = torch.randn(T, d, generator=g).to(torch.bfloat16).to(hip_device)
+    out = ops.sum_k(Xe, k, a0, out_dtype=torch.float32)
+    assert out.dtype == torch.float32
+    ref = np64(Xe).reshape(T, k, d).sum(1) + np64(a0)
+    assert_close(np64(out), ref, rtol=1e-6, atol=1e-6, what="sum_k fp32 out")
+    assert torch.equal(out.to(torch.bfloat16), ops.sum_k(Xe, k, a0))
+
+
+@pytest.mark.parametrize("n", [0, 5, 8, 4099, 1 << 20])
+def test_cast_bf16_matches_torch(hip_device, n):
+    """The compute-copy cast equals torch's fp32 -> bf16 conversion bit for bit (round to
+    nearest even, ties, subnormals, infinities; NaN stays NaN), tails of n % 8 included."""
+    from zmoe import ops
+
+    g = gen(n + 1)
+    x = torch.randn(n, generator=g) * torch.exp2(torch.randint(-140, 120, (n,), generator=g).float())
+    if n >= 8:
+        # exact ties at bf16 rounding midpoints (both parities), the largest finite values, specials
+        x[:8] = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 3.3895e38, -3.3895e38,
+                              float("inf"), float("-inf"), float("nan")])
+    xd = x.to(hip_device)
+    got = ops.cast_bf16(xd)
+    ref = xd.to(torch.bfloat16)
+    assert got.shape == ref.shape and got.dtype == torch.bfloat16
+    gi, ri = got.view(torch.int16), ref.view(torch.int16)
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(gi[~nan], ri[~nan])
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_swiglu(hip_device, dtype):
     from zmoe import ops
