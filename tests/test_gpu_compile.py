@@ -5,7 +5,8 @@ implementation (``zmoe/library.py``), so Dynamo traces the whole forward into on
 (no graph break) and AOT autograd traces the backward through the fake shapes. The
 compiled step must equal the eager one bit for bit (the same kernels run on the same
 inputs). The backend is ``aot_eager``: it runs Dynamo and AOT autograd, and executes the
-captured graphs op by op, without generating code for torch's own glue ops."""
+captured graphs op by op, without generating code for torch's own glue ops. The last test
+uses the default inductor backend, as the reference does."""
 
 import pytest
 import torch
@@ -14,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _layer(dev, fused_layer=True, fused_experts=True):
+    """A small bf16 layer (C3-like structure) and a zero-centred RMSNorm."""
     from modeling.model_config import ModelConfig
     from modeling.moe_layer import MoELayer
     from modeling.zRMSNorm import ZeroCenteredRMSNorm
@@ -122,3 +124,50 @@ def test_glumlp_compiles(hip_device):
     got = step(torch.compile(mlp, backend="aot_eager", dynamic=True, fullgraph=True))
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+def _amp_layer(dev):
+    """The reference's training mode: fp32 master weights, run under bf16 autocast."""
+    from modeling.model_config import ModelConfig
+    from modeling.moe_layer import MoELayer
+
+    torch.manual_seed(13)
+    cfg = ModelConfig(hidden_size=256, intermediate_size=128, n_experts=18, n_shared_experts=2, n_experts_per_token=4)
+    layer = MoELayer(cfg).to(dev)
+    layer.gate.expert_biases.data = (0.1 * torch.randn(16)).to(dev)
+    return layer
+
+
+@pytest.mark.parametrize("mode", ["bf16", "autocast fp32 weights"])
+def test_inductor_compiled_step(hip_device, mode):
+    """torch.compile with the default (inductor) backend and dynamic shapes, as main.py:929
+    compiles headless_forward, here around the layer with unpad indices; in the reference's
+    own mode the forward runs under bf16 autocast with fp32 weights and an fp32 input.
+    Inductor generates code for the glue ops around the ``zmoe::`` custom ops (which it calls
+    as extern kernels); the glue is exact (casts, gathers, concatenation), so the compiled
+    step equals eager bit for bit: routing, output, the input grad and every weight grad."""
+    import torch._dynamo
+
+    amp = mode != "bf16"
+    if amp:
+        layer = _amp_layer(hip_device)
+    else:
+        layer, _ = _layer(hip_device)
+    h, dout, valid = _inputs(hip_device)
+    if amp:
+        h = h.float()
+    params = list(layer.parameters())
+
+    def fn(x):
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+            return layer(x, unpad_indices=valid)
+
+    ref = _step(fn, h, dout, params)
+    torch._dynamo.reset()
+    compiled = torch.compile(fn, dynamic=True)
+    for _ in range(2):
+        got = _step(compiled, h, dout, params)
+        assert torch.equal(got[1], ref[1]), "routing differs from eager"
+        names = ["out", "d hidden"] + [n for n, _ in layer.named_parameters()]
+        for what, a, b in zip(names, [got[0], got[2]] + got[3], [ref[0], ref[2]] + ref[3]):
+            assert a.dtype == b.dtype and torch.equal(a, b), f"{what}: {int((a != b).sum())} elements differ"
