@@ -180,7 +180,8 @@ class MoELayer(nn.Module):
         ok = (self.fused_layer and self.routed_experts.fused and dtypes_ok
               and x.dim() == 3 and x.is_cuda and all(w.is_cuda for w in ws)
               and self.gate.top_k == self.routed_experts.top_k
-              and ws[4].shape[0] % 8 == 0 and ws[0].shape[0] % 8 == 0)    # 16-byte rows of the dH | d_logits buffer
+              and ws[4].shape[0] % 8 == 0 and ws[0].shape[0] % 8 == 0     # 16-byte rows of the dH | d_logits buffer
+              and x.shape[-1] % 8 == 0 and ws[2].shape[2] % 8 == 0)      # and of the d- and f-wide operands
         return ws if ok else None
 
     def forward(self, hidden_states, unpad_indices=None, norm=None):

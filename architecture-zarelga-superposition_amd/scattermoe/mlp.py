@@ -28,6 +28,14 @@ def _compute_dtype(x: torch.Tensor) -> torch.dtype:
     return torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled() else x.dtype
 
 
+def _fused_widths_ok(d: int, f: int, dtype: torch.dtype) -> bool:
+    """The fused GLU kernels move rows as 16-byte chunks: d and f must be multiples of 8
+    (bf16) or 4 (fp32) elements. Other widths run the module composition, whose ops take
+    any width (through zero-padded copies)."""
+    v = 8 if dtype == torch.bfloat16 else 4
+    return d % v == 0 and f % v == 0
+
+
 class GLUExpertsFunction(torch.autograd.Function):
     """y = sum_j gates[:, j] * W2[e_j] silu(W1g[e_j] x) * (W1h[e_j] x) for every token.
 
@@ -131,7 +139,7 @@ class GLUMLP(nn.Module):
         is token t's (moe_layer.py:55-56), written by the combine in place."""
         x_shape = x.size()
         x = x.view(-1, x_shape[-1])
-        if self.fused:
+        if self.fused and _fused_widths_ok(x_shape[-1], self.hidden_size, _compute_dtype(x)):
             dtype = _compute_dtype(x)
             res = None if residual is None else residual.reshape(-1, residual.shape[-1]).to(dtype)
             rows, total = (None, 0) if pad is None else (pad[0], int(pad[1]))

@@ -9,8 +9,8 @@ which one library launch spreads over only a few dozen tiles — run as the spli
 expert's SwiGLU is one fused HIP pass each way (``zmoe_swiglu`` /
 ``zmoe_swiglu_backward``) and its up and gate projections run as one GEMM.
 
-bf16 CUDA tensors take these paths; other dtypes use plain torch ops, as the
-reference does.
+bf16 CUDA tensors with 16-byte rows take these paths; other dtypes and widths use plain
+torch ops, as the reference does.
 """
 
 from __future__ import annotations
@@ -23,8 +23,11 @@ import torch.nn.functional as F
 from . import library as zl
 
 
-def _fused(*ts) -> bool:
-    return all(t.is_cuda and t.dtype == torch.bfloat16 for t in ts)
+def _fused(x, *ws) -> bool:
+    """bf16 CUDA operands whose widths are whole 16-byte chunks (8 elements) take the HIP path:
+    x's last dim and both dims of each [out, in] weight."""
+    return (all(t.is_cuda and t.dtype == torch.bfloat16 for t in (x, *ws)) and x.shape[-1] % 8 == 0
+            and all(w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0 for w in ws))
 
 
 class _Linear(torch.autograd.Function):

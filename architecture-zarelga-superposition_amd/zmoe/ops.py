@@ -61,6 +61,44 @@ def _idx64(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+# Feature widths the kernels cannot take directly. Their rows move as 16-byte chunks, so a
+# width must be a multiple of 8 bf16 or 4 fp32 elements. The reference's kernels mask any
+# width (scattermoe/kernels/ops.py:159-179, :404-435, :504-519); here the wrappers of the ops
+# its module composition uses (group, scatter2scatter, group_bwd_w, combine, sum_k) copy an
+# unaligned operand into a zero-padded one of the next aligned width, run the kernels, and
+# return the unpadded columns. Zero columns add exact zeros to every sum, so the results are
+# those of the unpadded arithmetic; the price is the copies (a slower path for such widths).
+def _vec(dtype: torch.dtype) -> int:
+    return 8 if dtype == torch.bfloat16 else 4
+
+
+def _aligned(n: int, dtype: torch.dtype) -> bool:
+    return n % _vec(dtype) == 0
+
+
+def _up(n: int, dtype: torch.dtype) -> int:
+    v = _vec(dtype)
+    return -(-n // v) * v
+
+
+def _pad_cols(t: Optional[torch.Tensor], n: int) -> Optional[torch.Tensor]:
+    """``t`` [..., m] zero-padded to [..., n] (a new contiguous tensor), or ``t`` when m == n."""
+    if t is None or t.shape[-1] == n:
+        return t
+    out = t.new_zeros(*t.shape[:-1], n)
+    out[..., :t.shape[-1]] = t
+    return out
+
+
+def _unpad_into(full: torch.Tensor, n: int, out: Optional[torch.Tensor]) -> torch.Tensor:
+    """The first n columns of ``full``, copied into ``out`` when given."""
+    part = full[..., :n]
+    if out is None:
+        return part.contiguous()
+    out.copy_(part)
+    return out
+
+
 # --------------------------------------------------------------------- routing
 def route_topk(logits: torch.Tensor, expert_biases: torch.Tensor, k: int, round_probs_bf16: bool = False):
     """modeling/moe_gate.py:27-34 on given logits [T, E] -> (idx, weight, prob) [T, k]."""
@@ -145,6 +183,9 @@ def group(A: torch.Tensor, sorted_idxs: torch.Tensor, coeff: Optional[torch.Tens
     """scattermoe/kernels/ops.py:449-458: Y[n] = A[idx[n] // fan_out] * coeff[idx[n]]."""
     dev = _require_cuda(A, sorted_idxs, coeff, out)
     A = _rows(A)
+    if not _aligned(A.shape[1], A.dtype):  # unaligned width: through a padded copy
+        Kp = _up(A.shape[1], A.dtype)
+        return _unpad_into(group(_pad_cols(A, Kp), sorted_idxs, coeff, fan_out), A.shape[1], out)
     idx = _idx64(sorted_idxs)
     N, K = idx.numel(), A.shape[1]
     if A.shape[0] * fan_out != N:
@@ -176,10 +217,21 @@ def scatter2scatter(X: torch.Tensor, W: torch.Tensor, sorted_expert_idxs: torch.
     if W.dim() != 3:
         raise ValueError("scatter2scatter: W must be [E, K, N]")
     E, K, N = W.shape
-    if W.stride(1) != 1 and W.stride(2) != 1:
-        W = W.contiguous()
     if W.dtype != X.dtype:
         raise ValueError("scatter2scatter: X and W dtypes differ")
+    if not (_aligned(K, X.dtype) and _aligned(N, X.dtype)):  # unaligned widths: padded copies
+        if X.shape[1] != K:
+            raise ValueError("scatter2scatter: X.size(1) != W.size(1)")
+        Kp, Np = _up(K, X.dtype), _up(N, X.dtype)
+        # the padded weight in the nn.Linear layout [E, N, K] (the TN form), viewed [E, K, N]
+        Wt = W.new_zeros(E, Np, Kp)
+        Wt[:, :N, :K] = W.permute(0, 2, 1)
+        Yp = scatter2scatter(_pad_cols(X, Kp), Wt.permute(0, 2, 1), sorted_expert_idxs, sorted_scattered_idxs, k,
+                             b=_pad_cols(b, Np), x_grouped=x_grouped, y_grouped=y_grouped,
+                             expert_offsets=expert_offsets, region=region)
+        return _unpad_into(Yp, N, out)
+    if W.stride(1) != 1 and W.stride(2) != 1:
+        W = W.contiguous()
     se = _idx64(sorted_expert_idxs)
     ss = _idx64(sorted_scattered_idxs)
     R = se.numel()
@@ -227,6 +279,13 @@ def group_bwd_w(DY: torch.Tensor, X: torch.Tensor, expert_offsets: torch.Tensor,
         raise ValueError("group_bwd_w: DY and X dtypes differ")
     M, N = DY.shape
     K = X.shape[1]
+    if not (_aligned(N, DY.dtype) and _aligned(K, DY.dtype)):  # unaligned widths: padded copies
+        Np, Kp = _up(N, DY.dtype), _up(K, DY.dtype)
+        DWp, Dbp = group_bwd_w(_pad_cols(DY, Np), _pad_cols(X, Kp), expert_offsets, E, has_bias=has_bias,
+                               x_gather=x_gather, x_div=x_div, out_dtype=out_dtype)
+        DWt = DWp[:, :N, :K].contiguous() if out is None else out.copy_(DWp[:, :N, :K])
+        Db = None if Dbp is None else _unpad_into(Dbp, N, out_bias)
+        return DWt, Db
     g = None
     if x_gather is not None:
         g = _idx64(x_gather)
@@ -403,6 +462,11 @@ def combine(Y: torch.Tensor, gates: Optional[torch.Tensor], k: int, addend: Opti
     Y = Y.contiguous()
     d = Y.shape[-1]
     T = Y.numel() // (d * k)
+    if not _aligned(d, Y.dtype):  # unaligned width: padded copies
+        dp = _up(d, Y.dtype)
+        a = None if addend is None else addend.reshape(T, d)
+        full = combine(_pad_cols(Y.reshape(-1, d), dp), gates, k, _pad_cols(a, dp), out_rows, out_total)
+        return full[:, :d].contiguous()
     g = None if gates is None else gates.reshape(T, k).to(torch.float32).contiguous()
     if addend is not None:
         addend = addend.reshape(T, d).to(Y.dtype).contiguous()
@@ -458,6 +522,10 @@ def sum_k(Xe: torch.Tensor, k: int, add0: Optional[torch.Tensor] = None,
     Xe = Xe.contiguous()
     d = Xe.shape[-1]
     T = Xe.numel() // (d * k)
+    if not _aligned(d, Xe.dtype):  # unaligned width: padded copies
+        dp = _up(d, Xe.dtype)
+        pad = lambda a: None if a is None else _pad_cols(a.reshape(T, d), dp)  # noqa: E731
+        return sum_k(_pad_cols(Xe.reshape(-1, d), dp), k, pad(add0), pad(add1), out_dtype)[:, :d].contiguous()
     od = Xe.dtype if out_dtype is None else out_dtype
     if od != Xe.dtype and not (Xe.dtype == torch.bfloat16 and od == torch.float32):
         raise ValueError(f"sum_k: out_dtype {od} with {Xe.dtype} rows")
