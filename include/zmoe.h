@@ -248,8 +248,8 @@ int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const void* H,
                             int64_t f, int E, int dtype, void* dH, void* stream);
 
 /* The same with the weighted combine's backward folded in (parallel_experts.py:
- * 191-208 and the gate grads of :161-163 via ops.py:9-80, rowwise_sum_product),
- * bf16 only. The A rows are the output grad's rows, read in place:
+ * 80-97: the gate-scaled grouping of the output grad, and the gate grads of :82
+ * via ops.py:9-80, rowwise_sum_product), bf16 only. The A rows are the output grad's rows, read in place:
  *   dYg[i] = gates[s_i] * dout[s_i / k]   (s_i = sorted_scattered_idxs[i]), so
  *   dA[i]  = gates[s_i] * (dout[s_i / k] @ W2[e])   -> dH as above, and
  *   d_gates[s_i] = <dout[s_i / k], Y[s_i]> = <dout[s_i / k] @ W2[e], A_i>,
