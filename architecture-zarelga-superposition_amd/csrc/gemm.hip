@@ -1620,10 +1620,115 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
                                   nt, wm0, wn0, tile.mt, scale_table);
 }
 
+// ------------------------------------------------------------------ weight grads of small experts
+// DW_e for the experts holding at most kFewRows rows (the long tail of a skewed routing):
+// their whole reduction is at most four 16-deep MFMA k-steps, so a tile is write-bound:
+// its output against at most 48 KB of operands that the expert's other tiles also read
+// (from L2). The expert's rows of DY (BM columns) and X (BN columns) go to LDS as K-major
+// tiles, the rows past the expert's end up to the next multiple of 16 zeroed; each wave
+// runs MI x NI MFMAs per k-step, and the usual wave-staged epilogue writes full 128-byte
+// lines. GATHER / DYG as in wgrad_bf16_kernel. Two forms: wgrad_few_rows_kernel, 128 x 256
+// tiles on 4 waves, two workgroups per CU (one's stores in flight while the other loads;
+// 6.1 TB/s of dW writes on 250 experts of 2 rows at [4096, 7168], against 3.6 TB/s for the
+// 128 x 128 tiles of the K-loop kernel); and inside the 256 x 256 K-loop kernel
+// (wgrad_bf16_kernel<..., FEW>), so that one launch covers every expert and the write-bound
+// tiles of the rare experts run beside the compute-bound tiles of the popular ones.
+constexpr int kFewRows = 64;
+constexpr int kFewBM = 128, kFewBN = 256;
+
+template <int BM, int BN, int NW, int GATHER, bool DYG, bool OUT_F32>
+__device__ __forceinline__ void wgrad_few_rows_tile(const WgradParams& p, char* smem, int e, int64_t r_begin,
+                                                    int nrows, int m0, int n0) {
+  constexpr int KT = kFewRows;
+  constexpr int NTH = NW * 64;
+  using WG = WaveGrid<BM, BN, NW>;
+  constexpr int MI = WG::MI, NI = WG::NI;
+  constexpr int CA = BM / 8, CB = BN / 8;  // 16-byte chunks per k-row of each tile
+  constexpr int QA = KT * CA / NTH, QB = KT * CB / NTH;  // chunks per thread
+  static_assert(QA * NTH == KT * CA && QB * NTH == KT * CB, "the threads tile the operand tiles");
+  const int nks = (nrows + 15) >> 4;  // k-steps (uniform per workgroup)
+  const int tid = threadIdx.x;
+  const char* dy = reinterpret_cast<const char*>(p.dy);
+  const char* x = reinterpret_cast<const char*>(p.x);
+  // source row of k-row kr of the gathered operand (kr < nrows)
+  auto gathered = [&](int kr) -> int64_t {
+    const uint32_t v = reinterpret_cast<const uint32_t*>(p.x_rows)[2 * (r_begin + kr)];  // indices < 2^31
+    if constexpr (GATHER == 1) return (int64_t)(v >> p.x_div_shift);
+    else return (int64_t)(v / (uint32_t)p.x_div);
+  };
+  // K-major tiles in LDS: DY^T [KT][BM] then X [KT][BN], 16-byte chunks swizzled as t_off
+  // reads them; k-rows up to 16 nks are written (zeros past nrows), the rest never read
+  lds_char* lds = (lds_char*)smem;
+  char* ta = smem;
+  char* tb = smem + KT * BM * 2;
+  uint4 va[QA], vb[QB];
+#pragma unroll
+  for (int q = 0; q < QA; ++q) {
+    const int i = tid + NTH * q, kr = i / CA, c = i % CA;
+    va[q] = make_uint4(0, 0, 0, 0);
+    if (kr < nrows && m0 + 8 * c < p.Ndy) {
+      const int64_t row = DYG ? gathered(kr) : r_begin + kr;
+      va[q] = ldg16(dy + (row * p.lddy + m0 + 8 * c) * 2);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < QB; ++q) {
+    const int i = tid + NTH * q, kr = i / CB, c = i % CB;
+    vb[q] = make_uint4(0, 0, 0, 0);
+    if (kr < nrows && n0 + 8 * c < p.Kx) {
+      const int64_t row = (GATHER != 0 && !DYG) ? gathered(kr) : r_begin + kr;
+      vb[q] = ldg16(x + (row * p.ldx + n0 + 8 * c) * 2);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < QA; ++q) {
+    const int i = tid + NTH * q, kr = i / CA, c = i % CA;
+    if (kr < 16 * nks) *reinterpret_cast<uint4*>(ta + t_off(kr, 8 * c, BM * 2)) = va[q];
+  }
+#pragma unroll
+  for (int q = 0; q < QB; ++q) {
+    const int i = tid + NTH * q, kr = i / CB, c = i % CB;
+    if (kr < 16 * nks) *reinterpret_cast<uint4*>(tb + t_off(kr, 8 * c, BN * 2)) = vb[q];
+  }
+  __syncthreads();
+  const int wave = tid >> 6;
+  const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+  for (int s = 0; s < nks; ++s) {
+    Frag<true> fa[MI], fb[NI];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) fa[mi].template read<BM, KT>(lds, wm0 + 32 * mi, s);
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) fb[ni].template read<BN, KT>(lds + KT * BM * 2, wn0 + 32 * ni, s);
+    asm_wait_lgkm<0>();
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) fa[mi].tie();
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) fb[ni].tie();
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ni].value(), fa[mi].value(), acc[mi][ni], 0, 0, 0);
+  }
+  __syncthreads();  // every wave has read the operand tiles; LDS becomes the staging areas
+  char* st = smem + wave * 32 * MI * WaveStage<WG::WN>::PITCH;
+  if constexpr (OUT_F32)
+    wgrad_epilogue_f32_staged(p, st, acc, e, m0, n0, wm0, wn0);
+  else
+    wgrad_epilogue_bf16(p, st, acc, e, m0, n0, wm0, wn0);
+}
+
 // GATHER: 0 = x rows in sorted order; 1 = gathered, row = index >> shift; 2 = gathered,
 // row = index / x_div. Both gathered forms keep the K loop free of branches. DYG: the
 // gather applies to the DY rows instead (x rows then in sorted order).
-template <int BM, int BN, int GATHER, bool OUT_F32 = false, int NW = 4, bool DYG = false>
+template <int BM, int BN, int GATHER, bool OUT_F32 = false, int NW = 4, bool DYG = false, bool FEW = false>
 __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   static_assert(!DYG || GATHER != 0, "a DY gather needs a gather mode");
   extern __shared__ __align__(16) char smem[];
@@ -1650,6 +1755,12 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   if (nrows < p.rows_lo || nrows > p.rows_hi) return;  // the other launch of a split covers this expert
   const int m0 = mt * BM, n0 = nt * BN;
+  if constexpr (FEW) {  // an expert of at most kFewRows rows: the write-bound form, no K loop
+    if (nrows <= kFewRows) {
+      wgrad_few_rows_tile<BM, BN, NW, GATHER, DYG, OUT_F32>(p, smem, e, r_begin, nrows, m0, n0);
+      return;
+    }
+  }
   const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   lds_char* lds = (lds_char*)(smem);  // generic -> LDS address space
   const int nk = (nrows + KS - 1) / KS;
@@ -1768,27 +1879,9 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
     wgrad_epilogue_bf16(p, st, acc, e, m0, n0, wm0, wn0);
 }
 
-// ------------------------------------------------------------------ weight grads of small experts
-// DW_e for the experts holding at most kFewRows rows (the long tail of a skewed routing):
-// their whole reduction is at most four 16-deep MFMA k-steps, so a tile is write-bound:
-// 64 KB of output against at most 48 KB of operands that the expert's other tiles also
-// read (from L2). A 128 x 256 tile on 4 waves (2 x 2, 64 x 128 each): the expert's rows
-// of DY (128 columns) and X (256 columns) go to LDS as K-major tiles, the rows past the
-// expert's end up to the next multiple of 16 zeroed; each wave runs eight MFMAs per
-// k-step, and the usual wave-staged epilogue writes full 128-byte lines. Two workgroups
-// per CU keep one's stores in flight while the other loads. GATHER / DYG as in
-// wgrad_bf16_kernel. (Measured on 250 experts of 2 rows at [4096, 7168]: 6.1 TB/s of dW
-// writes, against 3.6 TB/s for the 128 x 128 tiles of the K-loop kernel.)
-constexpr int kFewRows = 64;
-constexpr int kFewBM = 128, kFewBN = 256;
-
 template <int GATHER, bool DYG, bool OUT_F32 = false>
 __global__ __launch_bounds__(256, 2) void wgrad_few_rows_kernel(WgradParams p) {
   extern __shared__ __align__(16) char smem[];
-  constexpr int BM = kFewBM, BN = kFewBN, KT = kFewRows;
-  using WG = WaveGrid<BM, BN, 4>;
-  constexpr int MI = WG::MI, NI = WG::NI;
-  constexpr int CA = BM / 8, CB = BN / 8;  // 16-byte chunks per k-row of each tile
   const int per_e = p.m_tiles * p.n_tiles;
   const int logical = slab_logical_tile(p.E * per_e);
   if (logical < 0) return;
@@ -1799,85 +1892,8 @@ __global__ __launch_bounds__(256, 2) void wgrad_few_rows_kernel(WgradParams p) {
   const int64_t r_end = wgrad_rows_end(p, e);
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   if (nrows < p.rows_lo || nrows > p.rows_hi) return;  // another launch covers this expert
-  const int nks = (nrows + 15) >> 4;                     // k-steps (uniform per workgroup)
-  const int m0 = mt * BM, n0 = nt * BN;
-  const int tid = threadIdx.x;
-  const char* dy = reinterpret_cast<const char*>(p.dy);
-  const char* x = reinterpret_cast<const char*>(p.x);
-  // source row of k-row kr of the gathered operand (kr < nrows)
-  auto gathered = [&](int kr) -> int64_t {
-    const uint32_t v = reinterpret_cast<const uint32_t*>(p.x_rows)[2 * (r_begin + kr)];  // indices < 2^31
-    if constexpr (GATHER == 1) return (int64_t)(v >> p.x_div_shift);
-    else return (int64_t)(v / (uint32_t)p.x_div);
-  };
-  // K-major tiles in LDS: DY^T [KT][BM] then X [KT][BN], 16-byte chunks swizzled as t_off
-  // reads them; k-rows up to 16 nks are written (zeros past nrows), the rest never read
-  lds_char* lds = (lds_char*)smem;
-  char* ta = smem;
-  char* tb = smem + KT * BM * 2;
-  constexpr int QA = KT * CA / 256, QB = KT * CB / 256;  // chunks per thread
-  uint4 va[QA], vb[QB];
-#pragma unroll
-  for (int q = 0; q < QA; ++q) {
-    const int i = tid + 256 * q, kr = i / CA, c = i % CA;
-    va[q] = make_uint4(0, 0, 0, 0);
-    if (kr < nrows && m0 + 8 * c < p.Ndy) {
-      const int64_t row = DYG ? gathered(kr) : r_begin + kr;
-      va[q] = ldg16(dy + (row * p.lddy + m0 + 8 * c) * 2);
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < QB; ++q) {
-    const int i = tid + 256 * q, kr = i / CB, c = i % CB;
-    vb[q] = make_uint4(0, 0, 0, 0);
-    if (kr < nrows && n0 + 8 * c < p.Kx) {
-      const int64_t row = (GATHER != 0 && !DYG) ? gathered(kr) : r_begin + kr;
-      vb[q] = ldg16(x + (row * p.ldx + n0 + 8 * c) * 2);
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < QA; ++q) {
-    const int i = tid + 256 * q, kr = i / CA, c = i % CA;
-    if (kr < 16 * nks) *reinterpret_cast<uint4*>(ta + t_off(kr, 8 * c, BM * 2)) = va[q];
-  }
-#pragma unroll
-  for (int q = 0; q < QB; ++q) {
-    const int i = tid + 256 * q, kr = i / CB, c = i % CB;
-    if (kr < 16 * nks) *reinterpret_cast<uint4*>(tb + t_off(kr, 8 * c, BN * 2)) = vb[q];
-  }
-  __syncthreads();
-  const int wave = tid >> 6;
-  const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
-  f32x16_t acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
-  for (int s = 0; s < nks; ++s) {
-    Frag<true> fa[MI], fb[NI];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) fa[mi].template read<BM, KT>(lds, wm0 + 32 * mi, s);
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) fb[ni].template read<BN, KT>(lds + KT * BM * 2, wn0 + 32 * ni, s);
-    asm_wait_lgkm<0>();
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) fa[mi].tie();
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) fb[ni].tie();
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ni].value(), fa[mi].value(), acc[mi][ni], 0, 0, 0);
-  }
-  __syncthreads();  // every wave has read the operand tiles; LDS becomes the staging areas
-  char* st = smem + wave * 32 * MI * WaveStage<WG::WN>::PITCH;
-  if constexpr (OUT_F32)
-    wgrad_epilogue_f32_staged(p, st, acc, e, m0, n0, wm0, wn0);
-  else
-    wgrad_epilogue_bf16(p, st, acc, e, m0, n0, wm0, wn0);
+  wgrad_few_rows_tile<kFewBM, kFewBN, 4, GATHER, DYG, OUT_F32>(p, smem, e, r_begin, nrows, mt * kFewBM,
+                                                               nt * kFewBN);
 }
 
 constexpr int few_rows_lds_bytes() {
@@ -2000,21 +2016,24 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   return check_launch("grouped wgrad kernel");
 }
 
-template <int GATHER, bool OUT_F32, bool DYG = false>
+template <int GATHER, bool OUT_F32, bool DYG = false, bool FEW = false>
 int launch_wgrad_big(const WgradParams& p, hipStream_t s) {
   constexpr int NW = kBigWaves;
-  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, NW, DYG>, bf16_lds_bytes<256, 256, NW>(),
-                             256, 256, p, s, NW * 64);
+  return launch_wgrad_kernel(wgrad_bf16_kernel<256, 256, GATHER, OUT_F32, NW, DYG, FEW>,
+                             bf16_lds_bytes<256, 256, NW>(), 256, 256, p, s, NW * 64);
 }
 
 // Large tiles when the average expert holds enough rows to fill them.
 inline bool use_big_tiles(int64_t R, int E, int64_t N) { return R >= (int64_t)E * 256 && N >= 256; }
 
-// Weight grads under a skewed routing: experts holding at most this many rows get a
-// launch of the write-bound few-rows kernel of their own (wgrad_few_rows_kernel), the rest
-// the 256 x 256 tiles; 0 = one launch. The row counts stay on the device: each launch
-// covers every expert's tiles and a workgroup whose expert belongs to the other launch
-// exits at once (~0.5 us of a workgroup slot each).
+// Weight grads under a skewed routing (fewer than 1024 rows per expert on average): the
+// experts holding at most kFewRows rows take the write-bound few-rows form. With X's rows
+// gathered (dW1) it runs inside the 256 x 256 K-loop launch: one launch over every expert,
+// each workgroup picking its form from its expert's row count (C4: dW1 6.27 -> 6.08 ms).
+// With DY's rows gathered (dW2) it is a launch of its own (wgrad_few_rows_kernel, 128 x 256
+// tiles, two workgroups per CU) before the K-loop launch, each launch covering every
+// expert's tiles and the workgroups of the other launch's experts exiting at once: the
+// inline form measured 10% slower there (3.13 -> 3.45 ms at C4).
 inline int wgrad_small_rows(int64_t R, int E) { return R < (int64_t)E * 1024 ? kFewRows : 0; }
 
 // ==================================================================== small-M streaming path
@@ -2507,6 +2526,13 @@ int group_bwd_w_bf16(WgradParams p, int64_t M, int E, int64_t N, int64_t K, hipS
     return (int)ZMOE_ERR_NULL;  // not reached (checked above)
   };
   const int split = big ? wgrad_small_rows(M, E) : 0;
+  if constexpr (!DYG) {
+    if (split > 0) {  // one launch: each workgroup picks its form
+      if (gather == 1) return launch_wgrad_big<1, OUT_F32, false, true>(p, s);
+      if (gather == 2) return launch_wgrad_big<2, OUT_F32, false, true>(p, s);
+      return launch_wgrad_big<0, OUT_F32, false, true>(p, s);
+    }
+  }
   int rc = 0;
   if (split > 0) {  // experts of at most `split` rows on the write-bound kernel, the rest below
     WgradParams q = p;

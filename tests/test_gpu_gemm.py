@@ -125,6 +125,36 @@ def test_group_bwd_w_gather_dy_small_expert_split(hip_device, k):
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
 
 
+@pytest.mark.parametrize("mode", ["x gather", "dy gather", "x gather f32"])
+def test_group_bwd_w_skewed_expert_rounds(hip_device, mode):
+    """Skewed routing (fewer than 1024 rows per expert on average) with at least 32 tiles per
+    expert (N = 1024, K = 2048: 4 x 8 tiles of 256 x 256): one launch covers every expert,
+    experts of at most 64 rows on the few-rows form, and the slabs are dealt round-robin over
+    the experts. Row counts on both sides of the split and empty experts."""
+    from zmoe import ops
+
+    counts = np.array([0, 3, 64, 65, 1500, 17, 0, 700, 1, 2200, 63, 16, 5, 300, 129, 0])
+    E, k, N, K = len(counts), 3, 1024, 2048
+    off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
+    R = int(counts.sum())
+    g = gen(R + 17)
+    ss = torch.from_numpy(np.random.default_rng(11).permutation(R)).to(hip_device)
+    if mode == "dy gather":
+        DY = torch.randn(R // k + 1, N, generator=g).to(torch.bfloat16)
+        X = torch.randn(R, K, generator=g).to(torch.bfloat16)
+        DWt = ops.group_bwd_w_gather_dy(DY.to(hip_device), ss, k, X.to(hip_device), off, E)
+        ref, _ = O.group_bwd_w(O.group(np64(DY), ss.cpu().numpy(), fan_out=k), np64(X), off.cpu().numpy(), E)
+    else:
+        DY = torch.randn(R, N, generator=g).to(torch.bfloat16)
+        X = torch.randn(R // k + 1, K, generator=g).to(torch.bfloat16)
+        od = torch.float32 if mode.endswith("f32") else None
+        DWt, _ = ops.group_bwd_w(DY.to(hip_device), X.to(hip_device), off, E, x_gather=ss, x_div=k, out_dtype=od)
+        ref, _ = O.group_bwd_w(np64(DY), O.group(np64(X), ss.cpu().numpy(), fan_out=k), off.cpu().numpy(), E)
+    assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[torch.bfloat16], what=f"group_bwd_w {mode}")
+    for e in np.nonzero(counts == 0)[0]:
+        assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
+
+
 @pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
                                             (1200, 200, 136, 4, 2, 0.3), (128, 512, 136, 64, 4, 1.5),
                                             (32, 256, 256, 32, 8, 0.0)])
