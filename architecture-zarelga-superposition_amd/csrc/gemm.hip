@@ -259,6 +259,8 @@ __device__ __forceinline__ int xcd_logical_tile(int total) {
 // slab of ceil(total / 8) tiles per XCD, i.e. the contiguous ranges, so no XCD sits idle.
 // The launches round their grids up to whole slabs on every XCD.
 constexpr int kSlab = 32;
+// Inner-index band of the rows kernels' tile order within one expert (decode_rows_tile).
+constexpr int kBand = 8;
 __host__ __device__ __forceinline__ int slab_size(int64_t total) {
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   return per_xcd < kSlab ? (int)(per_xcd > 0 ? per_xcd : 1) : kSlab;
@@ -412,12 +414,22 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
     const int tiles_e = ntl[q] * p.n_tiles;
     if (logical >= run && logical < run + tiles_e) {  // (ntl[q] is 0 past the last expert)
       const int loc = logical - run;
-      // serpentine: the inner index runs backwards on odd outer steps, so consecutive
-      // tiles across a turn share an operand block too (0.3-0.8% per launch)
-      const int outer = p.n_major ? loc / ntl[q] : loc / p.n_tiles;
-      const int inner = p.n_major ? loc % ntl[q] : loc % p.n_tiles;
-      const int ninner = p.n_major ? ntl[q] : p.n_tiles;
-      const int in2 = (outer & 1) ? ninner - 1 - inner : inner;
+      // The inner index runs over bands of at most kBand tiles: an expert with more
+      // inner tiles than 2 * kBand (a dense-sized expert) is cut into bands, so the ~32
+      // tiles an XCD runs at once span about 8 x 4 tiles, not one column of 32 (one
+      // n-tile over 32 m-tiles made every XCD stream the whole A operand: 8x its bytes
+      // from HBM in a one-expert GEMM of 262144 x 2048 x 2048).
+      const int ninner_all = p.n_major ? ntl[q] : p.n_tiles;
+      const int nouter = p.n_major ? p.n_tiles : ntl[q];
+      const int band = ninner_all > 2 * kBand ? kBand : ninner_all;
+      const int b = loc / (band * nouter), lb = loc - b * band * nouter;
+      const int ninner = min(band, ninner_all - b * band);
+      // serpentine: the inner index runs backwards on odd outer steps, and the outer index
+      // on odd bands, so consecutive tiles across a turn share an operand block too
+      // (0.3-0.8% per launch)
+      const int outer0 = lb / ninner, inner = lb % ninner;
+      const int outer = (b & 1) ? nouter - 1 - outer0 : outer0;
+      const int in2 = b * band + ((outer0 & 1) ? ninner - 1 - inner : inner);
       const int mt = p.n_major ? in2 : outer;
       const int64_t r0 = ebeg[q] + (int64_t)mt * BM;
       found[0] = e0 + q;

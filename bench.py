@@ -394,6 +394,68 @@ def muon_bench(args) -> int:
     return 0
 
 
+def dense_gemm_bench(args) -> int:
+    """The grouped GEMM kernel run as a plain dense GEMM (one expert, no gather or scatter:
+    Y = X W^T with X [M, K], W [N, K], M = 262144 = C3's routed rows, N = K = 2048), beside
+    torch's matmul (hipBLASLt) on the same operands. Isolates the K loop from the grouping.
+    Prints one JSON line."""
+    import torch
+
+    from zmoe import ops
+
+    dev = torch.device("cuda:0")
+    M, N, K = 262144, 2048, 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    X = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    W = (torch.randn(1, N, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+    se = torch.zeros(M, dtype=torch.int64, device=dev)
+    ss = torch.arange(M, dtype=torch.int64, device=dev)
+    off = torch.tensor([M], dtype=torch.int64, device=dev)
+    Wl = W.permute(0, 2, 1)  # the logical [E, K, N] view of the nn.Linear layout
+
+    def ours():
+        return ops.scatter2scatter(X, Wl, se, ss, 1, x_grouped=True, y_grouped=True, expert_offsets=off)
+
+    def lib():
+        return X @ W[0].T
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    reps = max(5, args.steps)
+    y0, y1 = ours(), lib()
+    max_rel = float(((y0.float() - y1.float()).abs().max() / y1.float().abs().max()).item())
+    # two rounds in alternation, best of each: the core clock drifts under sustained MFMA load,
+    # and a fixed order would hand the drift to one side
+    ms, ms_lib = timed(ours, reps), timed(lib, reps)
+    ms, ms_lib = min(ms, timed(ours, reps)), min(ms_lib, timed(lib, reps))
+    flops = 2.0 * M * N * K
+    tf, tf_lib = flops / (ms * 1e-3) / 1e12, flops / (ms_lib * 1e-3) / 1e12
+    out = {
+        "metric": "grouped GEMM kernel as a dense bf16 GEMM (E=1, M=262144, N=K=2048), TFLOP/s",
+        "value": tf, "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "dense: Y[262144, 2048] = X[262144, 2048] W^T, W [2048, 2048] (nn.Linear layout)"},
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tf / PEAK_BF16_TFLOPS, "traffic": None},
+        "hipblaslt_ms": ms_lib, "hipblaslt_tflops": tf_lib, "ratio_to_hipblaslt": tf / tf_lib,
+        "max_rel_diff_vs_hipblaslt": max_rel,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -407,6 +469,8 @@ def main(argv=None):
     ap.add_argument("--muon", action="store_true",
                     help="time the MuonMD Newton-Schulz step on the C3 routed-expert stacks instead of the layer")
     ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 --pmc CSVs under DIR and exit")
+    ap.add_argument("--dense-gemm", action="store_true",
+                    help="time the grouped GEMM kernel as a plain dense GEMM beside hipBLASLt and exit")
     ap.add_argument("--autocast-fp32-params", action="store_true",
                     help="the reference's training mode (main.py:595, :746): fp32 master weights and an fp32 "
                          "input under torch.autocast(bf16); the step includes the weights' bf16 copies and "
@@ -423,6 +487,8 @@ def main(argv=None):
         return copy_probe()
     if args.muon:
         return muon_bench(args)
+    if args.dense_gemm:
+        return dense_gemm_bench(args)
 
     import torch
 

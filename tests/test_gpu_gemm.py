@@ -62,6 +62,53 @@ def test_scatter2scatter(hip_device, dtype, T, K, N, E, k, skew, xg, yg, w_layou
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("w_layout", ["param", "contiguous"])
+@pytest.mark.parametrize("case", ["many m-tiles, grouped A", "many n-tiles, gathered A"])
+def test_scatter2scatter_banded_tile_order(hip_device, dtype, w_layout, case):
+    """Experts with more than 16 m-tiles (A rows contiguous: n-tiles outer) or more than 16
+    n-tiles (A rows gathered: m-tiles outer) take their inner tiles in bands of 8, odd bands
+    reversed; every output tile must still be computed exactly once."""
+    from zmoe import ops
+
+    g = gen(41)
+    if case.startswith("many m"):
+        T, K, N, k, xg = 5300, 256, 520, 1, True
+        idx = torch.zeros(T, k, dtype=torch.int64)
+        idx[torch.randperm(T, generator=g)[:300]] = 1  # expert 0: 5000 rows (20 m-tiles of 256)
+    else:
+        T, K, N, k, xg = 700, 128, 4360, 2, False  # 18 n-tiles of 256 (35 of 128)
+        idx = torch.stack([torch.zeros(T, dtype=torch.int64), torch.ones(T, dtype=torch.int64)], 1)
+        idx[torch.randperm(T, generator=g)[:200]] = torch.tensor([1, 0])
+    E = 2
+    se, ss, off, _ = ops.flatten_sort_count(idx.to(hip_device), E)
+    X = torch.randn(T * k if xg else T, K, generator=g).to(dtype)
+    Wp = (torch.randn(E, N, K, generator=g) / K ** 0.5).to(dtype)
+    W = Wp.to(hip_device).permute(0, 2, 1) if w_layout == "param" else Wp.permute(0, 2, 1).contiguous().to(hip_device)
+    Y = ops.scatter2scatter(X.to(hip_device), W, se, ss, 1 if xg else k, x_grouped=xg, y_grouped=True,
+                            expert_offsets=off)
+    ref = O.scatter2scatter(np64(X), np64(Wp).transpose(0, 2, 1), se.cpu().numpy(), ss.cpu().numpy(),
+                            1 if xg else k, x_grouped=xg, y_grouped=True)
+    assert_close(np64(Y), ref, **TOL[dtype], what=f"scatter2scatter {case}")
+
+
+def test_glu_w1_forward_banded_pair_tiles(hip_device):
+    """SwiGLU W1 forward with f = 2200 (18 pair-column tiles of 128 pairs): banded n order."""
+    from zmoe import ops
+
+    T, d, f, E, k = 600, 128, 2200, 2, 2
+    idx, se, ss, off, _ = _routing(T, E, k, 0.0, hip_device, seed=77)
+    g = gen(78)
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    W1 = (torch.randn(E, 2 * f, d, generator=g) / d ** 0.5).to(torch.bfloat16)
+    H, A = ops.glu_w1_forward(x.to(hip_device), W1.to(hip_device), se, ss, off, k)
+    refH = O.scatter2scatter(np64(x), np64(W1).transpose(0, 2, 1), se.cpu().numpy(), ss.cpu().numpy(), k,
+                             x_grouped=False, y_grouped=True)
+    tol = TOL[torch.bfloat16]
+    assert_close(np64(H), refH, **tol, what="H")
+    assert_close(np64(A), O.swiglu(np64(H)), **tol, what="A")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("T,K,N,E,k,skew", SHAPES)
 @pytest.mark.parametrize("gather", [False, True])
 def test_group_bwd_w(hip_device, dtype, T, K, N, E, k, skew, gather):
