@@ -259,8 +259,25 @@ __device__ __forceinline__ int xcd_logical_tile(int total) {
 // slab of ceil(total / 8) tiles per XCD, i.e. the contiguous ranges, so no XCD sits idle.
 // The launches round their grids up to whole slabs on every XCD.
 constexpr int kSlab = 32;
-// Inner-index band of the rows kernels' tile order within one expert (decode_rows_tile).
+// Tile order within one expert, for position `loc` of its ninner x nouter tiles: the
+// inner index (the tiles sharing the outer operand block) runs fastest, in serpentine order
+// (backwards on odd outer steps, so the tiles either side of a turn share a block too:
+// 0.3-0.8% per launch). An expert with at least 2 * kBand inner tiles takes its inner index
+// in bands of kBand, the outer index reversed on odd bands, so that the ~32 tiles an XCD
+// runs at once span about kBand x 4 tiles instead of one or two outer steps of 16-32:
+// a one-expert 262144 x 2048 x 2048 GEMM with one n-tile per column of 32 read X once per
+// XCD (8.86 GB from HBM for 1.08 GB of operands; banded 3.23 GB, 2.02 -> 1.84 ms), and
+// C4's W1 forward (16 pair-column tiles) read each expert's weights once per two m-tiles
+// (banded 4.46 -> 4.30 ms).
 constexpr int kBand = 8;
+__device__ __forceinline__ void expert_tile_order(int loc, int ninner_all, int nouter, int& inner, int& outer) {
+  const int band = ninner_all >= 2 * kBand ? kBand : ninner_all;
+  const int b = loc / (band * nouter), lb = loc - b * band * nouter;
+  const int ninner = min(band, ninner_all - b * band);
+  const int outer0 = lb / ninner, in0 = lb % ninner;
+  outer = (b & 1) ? nouter - 1 - outer0 : outer0;
+  inner = b * band + ((outer0 & 1) ? ninner - 1 - in0 : in0);
+}
 __host__ __device__ __forceinline__ int slab_size(int64_t total) {
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   return per_xcd < kSlab ? (int)(per_xcd > 0 ? per_xcd : 1) : kSlab;
@@ -413,23 +430,8 @@ __device__ __forceinline__ bool decode_rows_tile(const RowsParams& p, char* smem
   for (int q = 0; q < 4; ++q) {
     const int tiles_e = ntl[q] * p.n_tiles;
     if (logical >= run && logical < run + tiles_e) {  // (ntl[q] is 0 past the last expert)
-      const int loc = logical - run;
-      // The inner index runs over bands of at most kBand tiles: an expert with more
-      // inner tiles than 2 * kBand (a dense-sized expert) is cut into bands, so the ~32
-      // tiles an XCD runs at once span about 8 x 4 tiles, not one column of 32 (one
-      // n-tile over 32 m-tiles made every XCD stream the whole A operand: 8x its bytes
-      // from HBM in a one-expert GEMM of 262144 x 2048 x 2048).
-      const int ninner_all = p.n_major ? ntl[q] : p.n_tiles;
-      const int nouter = p.n_major ? p.n_tiles : ntl[q];
-      const int band = ninner_all > 2 * kBand ? kBand : ninner_all;
-      const int b = loc / (band * nouter), lb = loc - b * band * nouter;
-      const int ninner = min(band, ninner_all - b * band);
-      // serpentine: the inner index runs backwards on odd outer steps, and the outer index
-      // on odd bands, so consecutive tiles across a turn share an operand block too
-      // (0.3-0.8% per launch)
-      const int outer0 = lb / ninner, inner = lb % ninner;
-      const int outer = (b & 1) ? nouter - 1 - outer0 : outer0;
-      const int in2 = b * band + ((outer0 & 1) ? ninner - 1 - inner : inner);
+      int in2, outer;
+      expert_tile_order(logical - run, p.n_major ? ntl[q] : p.n_tiles, p.n_major ? p.n_tiles : ntl[q], in2, outer);
       const int mt = p.n_major ? in2 : outer;
       const int64_t r0 = ebeg[q] + (int64_t)mt * BM;
       found[0] = e0 + q;
@@ -1755,11 +1757,8 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   if (logical < 0) return;
   const int e = logical / per_e;
   const int rem = logical % per_e;
-  // tiles of the expert in serpentine order (the inner index runs backwards on odd outer steps)
-  const int w_outer = p.n_major ? rem / p.m_tiles : rem / p.n_tiles;
-  const int w_inner0 = p.n_major ? rem % p.m_tiles : rem % p.n_tiles;
-  const int w_ninner = p.n_major ? p.m_tiles : p.n_tiles;
-  const int w_inner = (w_outer & 1) ? w_ninner - 1 - w_inner0 : w_inner0;
+  int w_inner, w_outer;
+  expert_tile_order(rem, p.n_major ? p.m_tiles : p.n_tiles, p.n_major ? p.n_tiles : p.m_tiles, w_inner, w_outer);
   const int mt = p.n_major ? w_inner : w_outer;
   const int nt = p.n_major ? w_outer : w_inner;
   const int64_t r_begin = e ? wgrad_rows_end(p, e - 1) : 0;

@@ -132,6 +132,36 @@ def test_group_bwd_w(hip_device, dtype, T, K, N, E, k, skew, gather):
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
 
 
+@pytest.mark.parametrize("E", [4, 8])
+@pytest.mark.parametrize("mode", ["x gather", "dy gather", "x gather f32"])
+def test_group_bwd_w_banded_tile_order(hip_device, E, mode):
+    """Weight grads with 17 (256-wide tiles, E = 4) or 33 (128-wide, E = 8) column tiles per
+    expert and more than 64 tiles: m-tiles outer, the column index in bands of 8, odd bands
+    reversed. Every [N, K] tile of every expert must still be computed exactly once."""
+    from zmoe import ops
+
+    T, k, N, K = 600, 2, 1096, 4104
+    idx, se, ss, off, _ = _routing(T, E, k, 0.3, hip_device, seed=E + 50)
+    g = gen(E * 9 + 1)
+    dt = torch.bfloat16
+    if mode == "dy gather":
+        DY = torch.randn(T, N, generator=g).to(dt)
+        X = torch.randn(T * k, K, generator=g).to(dt)
+        DWt = ops.group_bwd_w_gather_dy(DY.to(hip_device), ss, k, X.to(hip_device), off, E)
+        ref, _ = O.group_bwd_w(O.group(np64(DY), ss.cpu().numpy(), fan_out=k), np64(X), off.cpu().numpy(), E)
+    else:
+        DY = torch.randn(T * k, N, generator=g).to(dt)
+        X = torch.randn(T, K, generator=g).to(dt)
+        DWt, _ = ops.group_bwd_w(DY.to(hip_device), X.to(hip_device), off, E, x_gather=ss, x_div=k,
+                                 out_dtype=torch.float32 if mode.endswith("f32") else None)
+        ref, _ = O.group_bwd_w(np64(DY), O.group(np64(X), ss.cpu().numpy(), fan_out=k), off.cpu().numpy(), E)
+    if mode.endswith("f32"):
+        assert DWt.dtype == torch.float32
+        assert_close_fro(np64(DWt), ref.transpose(0, 2, 1), what="group_bwd_w banded f32")
+    else:
+        assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[dt], what=f"group_bwd_w banded {mode}")
+
+
 @pytest.mark.parametrize("T,K,N,E,k,skew", SHAPES[:10])
 def test_group_bwd_w_gather_dy(hip_device, T, K, N, E, k, skew):
     """bf16 weight grads with the gather on DY's rows: sorted row i of DY is
