@@ -13,9 +13,11 @@ the timed region.
 
 Prints ONE JSON line. ``roofline`` covers the dominant grouped-GEMM launch,
 timed live with HIP events on the stream it runs on; ``cpu_baseline`` times the
-numpy oracle (float32) on a bounded sample of the same workload, and, under
+reference layer as eager torch (float32) on a bounded sample of the same workload,
+under ``numpy_oracle`` the numpy oracle (float32) on the same sample, and, under
 ``c1_fwd_torch_eager``, the reference forward as eager torch at BASELINE.json's
-CPU config C1.
+CPU config C1. ``--dense-gemm`` times the grouped GEMM kernel as a plain dense GEMM
+beside hipBLASLt instead.
 """
 
 from __future__ import annotations
@@ -196,6 +198,48 @@ def cpu_baseline(T, d, E, k, f, fs, backward=True, budget_s=20.0, sample_T=1024)
                    f"of the same shape "
                    f"(d={d}, E={E}, k={k}, f={f}, shared={fs}); mean of {len(timed)} steps after 1 warmup, "
                    f"{sec:.2f} s/step"),
+    }
+
+
+def cpu_baseline_torch(T, d, E, k, f, fs, backward=True, budget_s=12.0, sample_T=1024):
+    """Time the reference layer as eager torch (float32, oracle/torch_eager.py) fwd (+bwd) on
+    ``sample_T`` tokens of the workload's shape, on the host cores."""
+    import torch
+
+    from oracle.torch_eager import moe_forward, moe_step
+
+    g = torch.Generator().manual_seed(0)
+    std = d ** -0.5
+    x = torch.randn(sample_T, d, generator=g)
+    dout = torch.randn(sample_T, d, generator=g)
+    Wg = torch.randn(E, d, generator=g) * std
+    W1 = torch.randn(E, 2 * f, d, generator=g) * std
+    W2 = torch.randn(E, d, f, generator=g) * std
+    shared = tuple(torch.randn(s, generator=g) * std for s in ((fs, d), (fs, d), (d, fs))) if fs else None
+    bias = torch.zeros(E)
+
+    def run():
+        if backward:
+            moe_step(x, Wg, bias, W1, W2, k, dout, shared=shared)
+        else:
+            moe_forward(x, Wg, bias, W1, W2, k, shared=shared)
+
+    run()  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 20 and (time.perf_counter() - t_start < budget_s or len(times) < 2):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[len(times) // 2]
+    return {
+        "value": sample_T / sec,
+        "unit": "tokens/s",
+        "cores": int(torch.get_num_threads()),
+        "kind": "port",
+        "sample": (f"the reference layer as eager torch (float32, oracle/torch_eager.py) "
+                   f"{'fwd+bwd' if backward else 'fwd'} on {sample_T} tokens of the same shape (d={d}, E={E}, "
+                   f"k={k}, f={f}, shared={fs}); median of {len(times)} steps after 1 warmup, {sec:.3f} s/step"),
     }
 
 
@@ -604,7 +648,9 @@ def main(argv=None):
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(T, d, E, k, f, fs, backward=backward, sample_T=min(1024, T))
+        cpu = cpu_baseline_torch(T, d, E, k, f, fs, backward=backward, sample_T=min(1024, T))
+        cpu["numpy_oracle"] = cpu_baseline(T, d, E, k, f, fs, backward=backward, sample_T=min(1024, T),
+                                           budget_s=12.0)
         cpu["c1_fwd_torch_eager"] = cpu_baseline_c1()
     traffic, traffic_source = (traffic_c3(dom_name) if args.workload == "c3"
                                else (None, "measured for the c3 workload only"))

@@ -917,3 +917,34 @@ def test_torch_eager_forward_equals_numpy_oracle(shared):
     np.testing.assert_allclose(out.numpy(), rout, rtol=1e-6, atol=1e-7)
     out32, _, _ = moe_forward(x, Wg, bias, W1, W2, 3, shared=sh)
     assert np.linalg.norm(out32.double().numpy() - rout) <= 1e-5 * np.linalg.norm(rout)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_torch_eager_step_equals_numpy_oracle_backward(shared):
+    """oracle/torch_eager.py's moe_step (the C3 CPU baseline: the reference layer as eager
+    torch under autograd) gives the numpy oracle's backward: dx, the gate weight's grad
+    (through the gathered, normalised probabilities), dW1, dW2 and the shared expert's
+    grads, in float64 up to the oracle's float32 routing probabilities (relative 1e-6)."""
+    from oracle.torch_eager import moe_step
+
+    g = torch.Generator().manual_seed(11)
+    T, d, E, k, f = 80, 48, 7, 3, 24
+    x = torch.randn(T, d, generator=g, dtype=torch.float64)
+    Wg = torch.randn(E, d, generator=g, dtype=torch.float64) * 0.1
+    bias = (torch.randn(E, generator=g) * 0.1).to(torch.float32)
+    W1 = torch.randn(E, 2 * f, d, generator=g, dtype=torch.float64) * d ** -0.5
+    W2 = torch.randn(E, d, f, generator=g, dtype=torch.float64) * f ** -0.5
+    sh = tuple(torch.randn(s, generator=g, dtype=torch.float64) * 0.15 for s in ((16, d), (16, d), (d, 16))) \
+        if shared else None
+    dout = torch.randn(T, d, generator=g, dtype=torch.float64)
+    out, grads = moe_step(x, Wg, bias.double(), W1, W2, k, dout, shared=sh)
+    orc = O.MoELayerOracle(Wg.numpy(), bias.numpy(), W1.numpy(), W2.numpy(), k,
+                           shared=tuple(t.numpy() for t in sh) if shared else None)
+    rout, _, _ = orc.forward(x.numpy())
+    ref = orc.backward(dout.numpy())
+    np.testing.assert_allclose(out.numpy(), rout, rtol=1e-6, atol=1e-7)
+    keys = ["x", "gate_weight", "W1", "W2"] + (["shared_gate", "shared_up", "shared_down"] if shared else [])
+    assert sorted(grads) == sorted(keys)
+    for n in keys:
+        a, b = grads[n].numpy(), ref[n]
+        assert np.linalg.norm(a - b) <= 1e-6 * np.linalg.norm(b), n
