@@ -1650,11 +1650,32 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
 constexpr int kFewRows = 64;
 constexpr int kFewBM = 128, kFewBN = 256;
 
+// The weight-grad tile of an expert with no rows: exact zeros, written straight to the output
+// (no operand loads, LDS or MFMA), 16 bytes per lane so that 8 lanes cover a 128-byte line.
+template <int BM, int BN, int NTH, bool OUT_F32>
+__device__ __forceinline__ void wgrad_zero_tile(const WgradParams& p, int e, int m0, int n0) {
+  constexpr int ES = OUT_F32 ? 4 : 2;        // output element bytes
+  constexpr int CPR = BN * ES / 16;          // 16-byte chunks per tile row
+  static_assert((BM * CPR) % NTH == 0, "the threads tile the output tile");
+  char* DW = reinterpret_cast<char*>(p.dw) + (int64_t)e * p.Ndy * p.Kx * ES;
+  const uint4 z = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int it = 0; it < BM * CPR / NTH; ++it) {
+    const int idx = (int)threadIdx.x + NTH * it;
+    const int m = m0 + idx / CPR, n = n0 + (idx % CPR) * (16 / ES);
+    if (m < p.Ndy && n < p.Kx) st_out(DW + ((int64_t)m * p.Kx + n) * ES, z);
+  }
+}
+
 template <int BM, int BN, int NW, int GATHER, bool DYG, bool OUT_F32>
 __device__ __forceinline__ void wgrad_few_rows_tile(const WgradParams& p, char* smem, int e, int64_t r_begin,
                                                     int nrows, int m0, int n0) {
   constexpr int KT = kFewRows;
   constexpr int NTH = NW * 64;
+  if (nrows == 0) {
+    wgrad_zero_tile<BM, BN, NTH, OUT_F32>(p, e, m0, n0);
+    return;
+  }
   using WG = WaveGrid<BM, BN, NW>;
   constexpr int MI = WG::MI, NI = WG::NI;
   constexpr int CA = BM / 8, CB = BN / 8;  // 16-byte chunks per k-row of each tile
@@ -1766,6 +1787,10 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   const int nrows = r_end > r_begin ? (int)(r_end - r_begin) : 0;
   if (nrows < p.rows_lo || nrows > p.rows_hi) return;  // the other launch of a split covers this expert
   const int m0 = mt * BM, n0 = nt * BN;
+  if (nrows == 0) {
+    wgrad_zero_tile<BM, BN, NW * 64, OUT_F32>(p, e, m0, n0);
+    return;
+  }
   if constexpr (FEW) {  // an expert of at most kFewRows rows: the write-bound form, no K loop
     if (nrows <= kFewRows) {
       wgrad_few_rows_tile<BM, BN, NW, GATHER, DYG, OUT_F32>(p, smem, e, r_begin, nrows, m0, n0);
