@@ -56,14 +56,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "24d29f500389bd50ba66b27e6d4b0c56d856be3b526a2583ce0f3a8b1509b354"
+TRAFFIC_C3_GEMM_SHA256 = "95574c015cc1b9a61813846634cd53615fdbe2cecba03675c7d35fd39695d24d"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6023311690,
-    "scatter2scatter#0": 2910775530,
-    "glu_w2_backward_dh#0": 2315163178,
-    "scatter2scatter#1": 5798577493,
-    "group_bwd_w#0": 2164114133,
-    "group_bwd_w#1": 3650146965,
+    "glu_w1_forward#0": 5909908842,
+    "scatter2scatter#0": 2892473941,
+    "glu_w2_backward_dh#0": 2286488832,
+    "scatter2scatter#1": 5796118314,
+    "group_bwd_w#0": 2164770837,
+    "group_bwd_w#1": 3661663274,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")

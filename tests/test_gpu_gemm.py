@@ -232,6 +232,34 @@ def test_group_bwd_w_skewed_expert_rounds(hip_device, mode):
         assert not DWt[e].any(), f"empty expert {e} must get exact zeros"
 
 
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_group_bwd_w_empty_experts_on_the_k_loop_launch(hip_device, out_f32):
+    """At least 1024 rows per expert on average (no few-rows split): the empty experts' tiles of
+    the K-loop launch write their zeros directly; every other expert's grad is unchanged."""
+    from zmoe import ops
+
+    counts = np.array([0, 3000, 5000, 0, 2100, 1])
+    E, k, N, K = len(counts), 2, 512, 768
+    off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
+    R = int(counts.sum())
+    assert R >= 1024 * E
+    g = gen(R + 3)
+    ss = torch.from_numpy(np.random.default_rng(5).permutation(R)).to(hip_device)
+    DY = torch.randn(R, N, generator=g).to(torch.bfloat16)
+    X = torch.randn(R // k + 1, K, generator=g).to(torch.bfloat16)
+    DWt = torch.full((E, N, K), float("nan"), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                     device=hip_device)  # the zeros must be written, not left from the buffer
+    ops.group_bwd_w(DY.to(hip_device), X.to(hip_device), off, E, x_gather=ss, x_div=k, out=DWt,
+                    out_dtype=torch.float32 if out_f32 else None)
+    ref, _ = O.group_bwd_w(np64(DY), O.group(np64(X), ss.cpu().numpy(), fan_out=k), off.cpu().numpy(), E)
+    if out_f32:
+        assert_close_fro(np64(DWt), ref.transpose(0, 2, 1), what="group_bwd_w f32")
+    else:
+        assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[torch.bfloat16], what="group_bwd_w")
+    for e in np.nonzero(counts == 0)[0]:
+        assert (DWt[e] == 0).all(), f"empty expert {e} must get exact zeros"
+
+
 @pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
                                             (1200, 200, 136, 4, 2, 0.3), (128, 512, 136, 64, 4, 1.5),
                                             (32, 256, 256, 32, 8, 0.0)])
