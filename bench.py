@@ -524,7 +524,7 @@ def main(argv=None):
         return pmc_summary(args.pmc_summary)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the MoE layer would shard experts across GPUs; see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the MoE layer would shard its experts: expert parallelism over RCCL all-to-all)", file=sys.stderr)
         return 2
 
     if args.copy_probe:
