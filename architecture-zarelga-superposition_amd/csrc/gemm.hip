@@ -2347,8 +2347,8 @@ int glu_w1_forward_impl(const void* X, int64_t x_stride_m, const void* W1, const
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "glu_w1_forward: dtype %d", dtype);
   ZMOE_REQUIRE(T >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE && k >= 1, ZMOE_ERR_SHAPE,
                "glu_w1_forward: bad sizes");
-  ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w1_forward: d/f too large");
-  ZMOE_REQUIRE(T * k < kMaxRows, ZMOE_ERR_SHAPE, "glu_w1_forward: T*k must be below 2^31");
+  ZMOE_REQUIRE(d < (1 << 30) && f < (1 << 29), ZMOE_ERR_SHAPE, "glu_w1_forward: d/f too large");
+  ZMOE_REQUIRE(T < kMaxRows && T * k < kMaxRows, ZMOE_ERR_SHAPE, "glu_w1_forward: T*k must be below 2^31");
   const int64_t R = T * k;
   if (R == 0) return ZMOE_OK;
   ZMOE_REQUIRE(X && W1 && H && A && sorted_scattered_idxs && expert_offsets, ZMOE_ERR_NULL,
@@ -2400,7 +2400,7 @@ extern "C" int zmoe_glu_w1_forward_scaled(const void* X, int64_t x_stride_m, con
                                           void* stream) {
   (void)sorted_expert_idxs;
   ZMOE_REQUIRE(dtype == ZMOE_DTYPE_BF16, ZMOE_ERR_DTYPE, "glu_w1_forward_scaled: bf16 only (dtype %d)", dtype);
-  ZMOE_REQUIRE(T * k == 0 || row_scale != nullptr, ZMOE_ERR_NULL, "glu_w1_forward_scaled: null row_scale");
+  ZMOE_REQUIRE(T <= 0 || k <= 0 || row_scale != nullptr, ZMOE_ERR_NULL, "glu_w1_forward_scaled: null row_scale");
   return glu_w1_forward_impl(X, x_stride_m, W1, sorted_scattered_idxs, expert_offsets, T, d, f, E, k, dtype,
                              row_scale, H, A, stream);
 }
@@ -2412,7 +2412,7 @@ extern "C" int zmoe_glu_w2_backward_dh(const void* dYg, const void* W2, const vo
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "glu_w2_backward_dh: dtype %d", dtype);
   ZMOE_REQUIRE(R >= 0 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE, ZMOE_ERR_SHAPE,
                "glu_w2_backward_dh: bad sizes");
-  ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w2_backward_dh: d/f too large");
+  ZMOE_REQUIRE(d < (1 << 30) && f < (1 << 29), ZMOE_ERR_SHAPE, "glu_w2_backward_dh: d/f too large");
   ZMOE_REQUIRE(R < kMaxRows, ZMOE_ERR_SHAPE, "glu_w2_backward_dh: R must be below 2^31");
   if (R == 0) return ZMOE_OK;
   ZMOE_REQUIRE(dYg && W2 && H && dH && expert_offsets, ZMOE_ERR_NULL, "glu_w2_backward_dh: null pointer");
@@ -2477,9 +2477,9 @@ extern "C" int zmoe_glu_w2_backward_dh_gates(const void* dout, int64_t T, int k,
                                              void* stream) {
   (void)sorted_expert_idxs;
   ZMOE_REQUIRE(dtype == ZMOE_DTYPE_BF16, ZMOE_ERR_DTYPE, "glu_w2_backward_dh_gates: bf16 only (dtype %d)", dtype);
-  ZMOE_REQUIRE(T >= 0 && k >= 1 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE, ZMOE_ERR_SHAPE,
+  ZMOE_REQUIRE(T >= 0 && T < kMaxRows && k >= 1 && d >= 1 && f >= 1 && E >= 1 && E <= kGemmMaxE, ZMOE_ERR_SHAPE,
                "glu_w2_backward_dh_gates: bad sizes");
-  ZMOE_REQUIRE(d < (1 << 30) && 2 * f < (1 << 30), ZMOE_ERR_SHAPE, "glu_w2_backward_dh_gates: d/f too large");
+  ZMOE_REQUIRE(d < (1 << 30) && f < (1 << 29), ZMOE_ERR_SHAPE, "glu_w2_backward_dh_gates: d/f too large");
   const int64_t R = T * k;
   ZMOE_REQUIRE(R < kMaxRows, ZMOE_ERR_SHAPE, "glu_w2_backward_dh_gates: T * k must be below 2^31");
   if (R == 0) return ZMOE_OK;
@@ -2701,6 +2701,7 @@ constexpr size_t kDenseHeaderBytes = kDenseMaxSplits * sizeof(int64_t);
 
 extern "C" size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int splits) {
   if (N < 1 || K < 1 || splits < 1) return kDenseHeaderBytes;
+  if (N >= (1 << 30) || K >= (1 << 30) || splits > kDenseMaxSplits) return 0;  // sizes dense_wgrad rejects
   return kDenseHeaderBytes + (size_t)splits * (size_t)N * (size_t)K * 4u;
 }
 

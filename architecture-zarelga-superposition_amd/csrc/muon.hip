@@ -134,7 +134,7 @@ int64_t ns_chunk(int64_t E, int64_t m, int64_t n) {
 using namespace zmoe;
 
 extern "C" size_t zmoe_newton_schulz5_workspace_bytes(int64_t E, int64_t m, int64_t n) {
-  if (E < 1 || m < 1 || n < 1 || m * n * 2 > kNsMaxSpan) return 0;
+  if (E < 1 || m < 1 || n < 1 || m > kNsMaxSpan / 2 / n) return 0;
   return ns_layout(ns_chunk(E, m, n), m, n).total;
 }
 

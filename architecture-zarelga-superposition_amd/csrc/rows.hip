@@ -619,7 +619,7 @@ extern "C" int zmoe_swiglu_backward_gates(const void* dA, const void* H, int64_t
 extern "C" int zmoe_swiglu_backward(const void* dA, const void* H, int64_t R, int64_t f, int dtype, void* dH,
                                     int64_t ld_dh, void* stream) {
   ZMOE_REQUIRE(dtype_ok(dtype), ZMOE_ERR_DTYPE, "swiglu_backward: dtype");
-  ZMOE_REQUIRE(R >= 0 && f >= 0 && ld_dh >= 2 * f, ZMOE_ERR_SHAPE, "swiglu_backward: bad sizes");
+  ZMOE_REQUIRE(R >= 0 && f >= 0 && f < (1 << 30) && ld_dh >= 2 * f, ZMOE_ERR_SHAPE, "swiglu_backward: bad sizes");
   if (R == 0 || f == 0) return ZMOE_OK;
   ZMOE_REQUIRE(dA && H && dH, ZMOE_ERR_NULL, "swiglu_backward: null pointer");
   ZMOE_REQUIRE(f % vec_of(dtype) == 0 && ld_dh % vec_of(dtype) == 0 && aligned16(H) && aligned16(dA) &&

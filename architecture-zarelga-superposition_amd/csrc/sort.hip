@@ -462,6 +462,7 @@ __global__ void offsets_from_sorted_kernel(const int64_t* __restrict__ sorted, i
 using namespace zmoe;
 
 extern "C" size_t zmoe_sort_workspace_bytes(int64_t R, int E) {
+  if (E < 1 || E > kSortMaxE || R >= (int64_t)0x7fffffff) return 0;  // sizes the sort rejects
   const int64_t ntiles = cdiv(R > 0 ? R : 1, kSortTile);
   return kSortHeader + (size_t)ntiles * (size_t)(E + 1) * sizeof(int32_t);
 }
