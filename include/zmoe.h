@@ -78,7 +78,8 @@ int zmoe_route_topk_backward(const float* d_weight, const float* topk_prob,
 int zmoe_bincount(const int64_t* expert_idxs, int64_t R, int E, int64_t* counts,
                   void* stream);
 
-/* Bytes of device workspace zmoe_flatten_sort_count needs for (R, E). */
+/* Bytes of device workspace zmoe_flatten_sort_count needs for (R, E); 0 for sizes
+ * it rejects (E outside [1, 1024], R >= 2^31 - 1). */
 size_t zmoe_sort_workspace_bytes(int64_t R, int E);
 
 /* flatten_sort_count (parallel_experts.py:21-28), a stable counting sort:
@@ -191,7 +192,7 @@ int zmoe_group_bwd_w_gather_dy(const void* DY, int64_t dy_stride_m,
  * split into `splits` ranges computed by the grouped wgrad kernel into fp32
  * partials, then summed in a fixed order and rounded once (deterministic).
  * workspace: zmoe_dense_wgrad_workspace_bytes(N, K, splits) bytes, 16-byte
- * aligned. fp32 runs unsplit. out_dtype: `dtype`, or F32 for BF16 operands
+ * aligned (0 for sizes dense_wgrad rejects: N or K >= 2^30, splits > 64). fp32 runs unsplit. out_dtype: `dtype`, or F32 for BF16 operands
  * (the fp32 sum written unrounded: fp32 master weights under bf16 autocast).
  * ------------------------------------------------------------------------- */
 size_t zmoe_dense_wgrad_workspace_bytes(int64_t N, int64_t K, int splits);
@@ -368,7 +369,8 @@ int zmoe_rmsnorm_rows_backward(const void* dY, const void* X, int64_t x_stride, 
  * with bf16 rounding after every product and sum, as in bf16 tensor arithmetic.
  * Any E: the stack runs in passes of at most min(1024, (2 GiB - 64 KiB) / (2 m n))
  * matrices over one pass-sized workspace (one matrix must span less than that).
- * Workspace: zmoe_newton_schulz5_workspace_bytes(E, m, n), 256-byte aligned.      */
+ * Workspace: zmoe_newton_schulz5_workspace_bytes(E, m, n), 256-byte aligned (0 when
+ * one matrix spans 2 GiB - 64 KiB or more, or a size is below 1).                  */
 size_t zmoe_newton_schulz5_workspace_bytes(int64_t E, int64_t m, int64_t n);
 int zmoe_newton_schulz5(void* X, int64_t E, int64_t m, int64_t n, int steps, float a, float b, float c,
                         void* workspace, size_t workspace_bytes, void* stream);
