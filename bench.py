@@ -56,14 +56,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "95574c015cc1b9a61813846634cd53615fdbe2cecba03675c7d35fd39695d24d"
+TRAFFIC_C3_GEMM_SHA256 = "79bfd9aa75d99a76590d7de434bcc412db40ad9821e9da342c0bfe5d0cf89a4c"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 5909908842,
-    "scatter2scatter#0": 2892473941,
-    "glu_w2_backward_dh#0": 2286488832,
-    "scatter2scatter#1": 5796118314,
-    "group_bwd_w#0": 2164770837,
-    "group_bwd_w#1": 3661663274,
+    "glu_w1_forward#0": 5955267018,
+    "scatter2scatter#0": 2896164522,
+    "glu_w2_backward_dh#0": 2292509312,
+    "scatter2scatter#1": 5741998912,
+    "group_bwd_w#0": 2162030293,
+    "group_bwd_w#1": 3644248426,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
