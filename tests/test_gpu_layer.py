@@ -101,6 +101,14 @@ def test_layer_small_c3_bf16(hip_device, fused):
     run_and_compare(512, 512, 32, 8, 256, 2, torch.bfloat16, hip_device, fused=fused)
 
 
+@pytest.mark.parametrize("k,E,fused", [(64, 80, True), (32, 40, False), (17, 24, False)])
+def test_layer_large_top_k(hip_device, k, E, fused):
+    """The largest top-k each path takes: 64 through the whole-layer function (the routing
+    kernels' bound), 32 through the module composition, whose ParallelLinear backward forms
+    the gates' grad in the combine's backward (one register slot per k, up to 32)."""
+    run_and_compare(96, 128, E, k, 64, 1, torch.bfloat16, hip_device, fused=fused, seed=k)
+
+
 def test_layer_fused_matches_composition_fp32(hip_device):
     run_and_compare(700, 128, 16, 4, 96, 1, torch.float32, hip_device, fused=False, seed=3)
 

@@ -31,7 +31,9 @@ def _route_case(T, E, k, seed, dtype, bias_std, ties=False, nan=False):
                                    (513, 200, 8), (99, 136, 16), (50, 8, 8), (1001, 120, 3), (64, 256, 16),
                                    # eight tokens per wave (8-lane rows) for E <= 128 and k <= 8, 16-lane
                                    # rows of 8 experts for k in 9..16 at E <= 128
-                                   (301, 128, 12), (77, 64, 16), (263, 16, 5)])
+                                   (301, 128, 12), (77, 64, 16), (263, 16, 5),
+                                   # the largest k (one slot per lane of the one-row-per-wave kernel)
+                                   (40, 100, 64), (9, 64, 64)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_route_topk_bit_exact(hip_device, T, E, k, dtype):
     logits, bias = _route_case(T, E, k, seed=T + E, dtype=dtype, bias_std=0.1, ties=True, nan=T > 3)
@@ -140,10 +142,12 @@ def test_route_equal_scores_and_forced_bias(hip_device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_route_backward(hip_device, dtype):
+@pytest.mark.parametrize("E,k", [(64, 8), (100, 40), (128, 64)])
+def test_route_backward(hip_device, dtype, E, k):
+    """Up to 16 slots per token through scalar registers, more through lane shuffles."""
     from zmoe import ops
 
-    T, E, k = 500, 64, 8
+    T = 500
     logits, bias = _route_case(T, E, k, seed=5, dtype=dtype, bias_std=0.1)
     idx, w, p = ops.route_topk(logits.to(hip_device), bias.to(hip_device), k,
                                round_probs_bf16=dtype == torch.bfloat16)
