@@ -109,6 +109,14 @@ def test_layer_large_top_k(hip_device, k, E, fused):
     run_and_compare(96, 128, E, k, 64, 1, torch.bfloat16, hip_device, fused=fused, seed=k)
 
 
+@pytest.mark.parametrize("T,d,E,k,f,fused", [(1, 64, 1, 1, 32, True), (3, 64, 2, 2, 32, True),
+                                              (5, 64, 1, 1, 32, False), (64, 128, 1024, 4, 32, True)])
+def test_layer_extreme_small_shapes(hip_device, T, d, E, k, f, fused):
+    """One token, one expert, every expert selected, and 1024 experts for 64 tokens (most of
+    them empty) through the whole layer, forward and backward."""
+    run_and_compare(T, d, E, k, f, 1, torch.bfloat16, hip_device, fused=fused, seed=T + E)
+
+
 def test_layer_fused_matches_composition_fp32(hip_device):
     run_and_compare(700, 128, 16, 4, 96, 1, torch.float32, hip_device, fused=False, seed=3)
 
