@@ -141,8 +141,8 @@ def sigmoid_f32(logits):
 
     The HIP kernel evaluates the same two forms, so p agrees bit-for-bit.
     """
-    z = np.asarray(logits, dtype=np.float32).astype(np.float64)
-    with np.errstate(over="ignore", invalid="ignore"):
+    with np.errstate(over="ignore", invalid="ignore"):  # NaN and infinite logits are part of the contract
+        z = np.asarray(logits, dtype=np.float32).astype(np.float64)
         p = 1.0 / (1.0 + np.exp(-z))
     p = np.where(z <= SIGMOID_ZERO_BELOW, 0.0, p).astype(np.float32)
     small = np.abs(z) < SIGMOID_SERIES_BELOW

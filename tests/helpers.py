@@ -81,8 +81,10 @@ def close_dev(got: torch.Tensor, ref: torch.Tensor, what: str, rtol=2e-2, atol=2
     """assert_close on the device, in float64, over chunks of the leading dim (a C4 weight
     grad holds 7.5e9 elements). Returns the worst |err| / bound."""
     assert got.shape == ref.shape, (what, tuple(got.shape), tuple(ref.shape))
+    got, ref = got.detach(), ref.detach()
     if rss is not None:
         assert rss.shape == ref.shape, (what, "rss", tuple(rss.shape))
+        rss = rss.detach()
     lead = got.shape[0] if got.dim() else 1
     per = max(1, got.numel() // max(lead, 1))
     step = max(1, chunk_elems // per)
