@@ -21,10 +21,12 @@
 //     ds_read_b64_tr_b16 for operands whose reduction dimension is strided. Each
 //     stage has its own scalar buffer descriptor (the k advance and the tail
 //     clipping), so issuing a load costs no vector ALU.
-//   * v_mfma_f32_32x32x16_bf16 with the B tile as the first operand: each lane ends
-//     up holding 4 consecutive output columns of one output row. Every MFMA slot of
-//     the K loop is pinned with sched_barrier so loads, fragment reads and the one
-//     barrier per stage interleave with the MFMAs (kloop64).
+//   * v_mfma_f32_16x16x32_bf16 on 8 waves (kloop64_m16; the SwiGLU-backward and
+//     Newton-Schulz epilogues, 4-wave tiles and the DY-gathered weight grads keep
+//     v_mfma_f32_32x32x16_bf16, kloop64), with the B tile as the first operand: each
+//     lane ends up holding 4 consecutive output columns of one output row. Every MFMA
+//     slot of the K loop is pinned with sched_barrier so loads, fragment reads and the
+//     one barrier per stage interleave with the MFMAs.
 //   * Epilogue: each wave stages its block in LDS (rounded to the output type, as
 //     the reference stores its GEMM outputs) and writes full 128-byte lines to
 //     grouped or scattered rows, optionally through SwiGLU, its backward, or the
@@ -844,10 +846,13 @@ __device__ __forceinline__ int nt_swz(int row) {
   else return (row >> 2) & 3;
 }
 
-// K-major ("transposed") tile: [KS k-rows][COLS], 16-byte chunks XOR (row & 3) * 4:
-// the four k-rows one transpose-read touches land in four different 64-byte bank groups.
+// K-major ("transposed") tile: [KS k-rows][COLS], 16-byte chunks XOR (row & 3) * 4 ^
+// ((row >> 3) & 1) * 2: the four k-rows one transpose-read touches land in four different
+// 64-byte bank groups, and so do the 16-lane groups of a 16 x 16 x 32 fragment read, which
+// address k-rows 8 apart (without the second term those hit the same banks).
 __device__ __forceinline__ uint32_t t_off(int krow, int col, int row_bytes) {
-  return (uint32_t)(krow * row_bytes + ((((col >> 3) ^ ((krow & 3) << 2))) << 4) + ((col & 7) << 1));
+  return (uint32_t)(krow * row_bytes + ((((col >> 3) ^ ((krow & 3) << 2) ^ (((krow >> 3) & 1) << 1))) << 4) +
+                    ((col & 7) << 1));
 }
 
 // Fragment reads are inline asm: LLVM's waitcnt pass makes any LDS read it cannot
@@ -983,7 +988,7 @@ struct KLoad {
     for (int q = 0; q < NQ; ++q) {
       const int f = ((int)(threadIdx.x >> 6) * NQ + q) * 64 + (int)(threadIdx.x & 63);
       const int kr = f / CPR;
-      const int c = (f % CPR) ^ ((kr & 3) << 2);
+      const int c = (f % CPR) ^ ((kr & 3) << 2) ^ (((kr >> 3) & 1) << 1);
       const int col = mn0 + 8 * c;
       coff[q] = col < ncols ? (uint32_t)col * 2u : kOOB;
       voff[q] = col < ncols ? (uint32_t)((int64_t)kr * pitch_bytes) + coff[q] : kOOB;
@@ -1113,6 +1118,157 @@ __device__ __forceinline__ void kloop64(int nk, lds_char* lds, int wm0, int wn0,
   __builtin_amdgcn_s_setprio(0);
 }
 
+// One 16 x 16 x 32 operand fragment: lane (r = lane % 16, G = lane / 16) gets k = 32 j + 8 G + 0..7
+// of row mn0 + r: one 16-byte read of a row-major tile, or two transposing reads of a
+// K-major one (lane s16 of group G addresses k-row 32 j + 8 G + 4 q + s16 / 4, columns
+// mn0 + 4 (s16 % 4) .. +3; in each 16-lane group lane 4 a + b then receives column
+// mn0 + 4 a + b of those four k-rows).
+template <bool TR>
+struct Frag16 {
+  v4i32_t w;
+  v2i32_t lo, hi;
+  static constexpr int kReads = TR ? 2 : 1;
+  template <int BMN, int KS>
+  __device__ __forceinline__ void read_piece(const lds_char* base, int mn0, int j, int q) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (!TR) {
+      w = asm_ds_read_b128(lds_addr(base) + nt_off<KS>(mn0 + (lane & 15), 4 * j + (lane >> 4)));
+    } else {
+      const int G = lane >> 4, s16 = lane & 15;
+      const int krow = 32 * j + 8 * G + 4 * q + (s16 >> 2);
+      const v2i32_t v = asm_ds_read_tr16(lds_addr(base) + t_off(krow, mn0 + 4 * (s16 & 3), BMN * 2));
+      if (q == 0) lo = v;
+      else hi = v;
+    }
+  }
+  __device__ __forceinline__ void tie() {
+    if constexpr (!TR) {
+      asm_tie(w);
+    } else {
+      asm_tie(lo);
+      asm_tie(hi);
+    }
+  }
+  __device__ __forceinline__ bf16x8_t value() const {
+    if constexpr (!TR) return __builtin_bit_cast(bf16x8_t, w);
+    else return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
+  }
+};
+
+// The K loop of kloop64 on v_mfma_f32_16x16x32_bf16 (same LDS stages, loads, barrier and
+// waits). The accumulators are 16 x 16 blocks: acc[mi][ni][2 a + b] holds rows
+// 32 mi + 16 a + (lane % 16) and columns 32 ni + 16 b + 4 (lane / 16) + 0..3 of the wave's
+// block. A stage's four steps are (32-deep k-step j, half h) = (t / 2, t % 2), half h covering
+// the 32-row blocks h MI/2 .. (h + 1) MI/2 - 1: with 8 waves 16 MFMAs per step, as many
+// cycles as kloop64's 8. A step reads the next step's A fragments, and in the second half of
+// a k-step the next k-step's B fragments too (A held one step, B two). The smaller MFMA
+// interleaves better with the loads and fragment reads of the two waves of a SIMD: a probe
+// streaming the same loads and LDS reads ran 8-10% more MFMA work per second on it than on
+// 32 x 32 x 16, at the same clock.
+template <int LPS, int MI, int NI, bool A_T, bool B_T, int BM, int BN, typename Dma, typename Prefetch, typename Hook>
+__device__ __forceinline__ void kloop64_m16(int nk, lds_char* lds, int wm0, int wn0, f32x4_t (&acc)[MI][NI][4],
+                                            Dma dma, Prefetch prefetch, Hook after_prologue_loads) {
+  constexpr int KS = 64;
+  constexpr int kStage = (BM + BN) * KS * 2;
+  constexpr int HM = MI / 2;              // 32-row blocks per step
+  constexpr int NMMA = HM * 2 * NI * 2;   // MFMAs per step
+  constexpr int AR = Frag16<A_T>::kReads, BR = Frag16<B_T>::kReads;
+  constexpr int NRA = HM * 2 * AR, NRB = NI * 2 * BR;
+  constexpr int WIN = 2 * NMMA;
+  constexpr int kEarly = (NMMA * LPS + WIN - 1) / WIN;
+  static_assert(MI % 2 == 0, "two halves of the 32-row blocks");
+  Frag16<A_T> fa[2][HM][2];
+  Frag16<B_T> fb[2][NI][2];
+  // fragment reads of step t (of the stage in st): read r < NRA is A, else B (t even only)
+  auto read = [&](const lds_char* st, int t, int r) {
+    const int j = t >> 1, h = t & 1;
+    if (r < NRA) {
+      const int f = r / AR, q = r % AR, mil = f >> 1, a = f & 1;
+      fa[t & 1][mil][a].template read_piece<BM, KS>(st, wm0 + 32 * (h * HM + mil) + 16 * a, j, q);
+    } else {
+      const int rb = r - NRA, f = rb / BR, q = rb % BR, ni = f >> 1, b = f & 1;
+      fb[j & 1][ni][b].template read_piece<BN, KS>(st + BM * KS * 2, wn0 + 32 * ni + 16 * b, j, q);
+    }
+  };
+  auto nread = [](int t) { return (t & 1) ? NRA : NRA + NRB; };
+  auto tie = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < HM; ++i) {
+      fa[t & 1][i][0].tie();
+      fa[t & 1][i][1].tie();
+    }
+    if ((t & 1) == 0) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        fb[(t >> 1) & 1][i][0].tie();
+        fb[(t >> 1) & 1][i][1].tie();
+      }
+    }
+  };
+  auto mma = [&](int t, int i) {
+    const int b = i & 1, ni = (i >> 1) % NI, a = (i / (2 * NI)) & 1, mil = i / (4 * NI);
+    f32x4_t& c = acc[(t & 1) * HM + mil][ni][2 * a + b];
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[(t >> 1) & 1][ni][b].value(), fa[t & 1][mil][a].value(), c, 0, 0,
+                                                0);
+  };
+  // step t: MFMAs of step t, reads of step (t + 1) % 4 from rst, loads of window slots
+  // [w0, w0 + NMMA) of stage lkt into buffer lbuf
+  auto step = [&](int t, const lds_char* rst, int w0, int lbuf, int lkt, bool lon) {
+    const int tn = (t + 1) & 3;
+    const int nr = nread(tn);
+    constexpr int RPS = (NRA + NRB + NMMA - 1) / NMMA;
+    __builtin_amdgcn_sched_barrier(0);
+    if (w0 >= 0) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NMMA; ++i) {
+      mma(t, i);
+#pragma unroll
+      for (int j = 0; j < LPS; ++j)
+        if (w0 >= 0 && j * WIN / LPS == w0 + i) dma(j, lbuf, lkt, lon);
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+        if (i * RPS + r < nr) read(rst, tn, i * RPS + r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm_wait_lgkm<0>();
+    tie(tn);
+  };
+  if (nk <= 0) {
+    after_prologue_loads();
+    return;
+  }
+  prefetch(0);
+#pragma unroll
+  for (int j = 0; j < LPS; ++j) dma(j, 0, 0, true);
+  prefetch(1);
+#pragma unroll
+  for (int j = 0; j < kEarly; ++j) dma(j, 1, 1, nk > 1);
+  after_prologue_loads();
+  __builtin_amdgcn_s_waitcnt(vm_wait(kEarly));  // stage 0 landed (stage 1's early loads may not have)
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < NRA + NRB; ++r) read(lds, 0, r);
+  asm_wait_lgkm<0>();
+  tie(0);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const lds_char* st = lds + buf * kStage;
+    const lds_char* nst = lds + (buf ^ 1) * kStage;
+    step(0, st, NMMA, buf ^ 1, kt + 1, kt + 1 < nk);  // rest of stage kt + 1's loads
+    prefetch(kt + 2);
+    step(1, st, -1, 0, 0, false);
+    step(2, st, -1, 0, 0, false);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    asm volatile("s_barrier" ::: "memory");
+    step(3, nst, 0, buf, kt + 2, kt + 2 < nk);  // first part of stage kt + 2's loads
+  }
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
+  __builtin_amdgcn_s_setprio(0);
+}
+
 // Epilogues: each wave stages its own WM x WN accumulator block in its own LDS area
 // (bf16, rows of WN * 2 + 16 bytes) and writes it out row-contiguously, 16 bytes
 // per lane, so every store instruction covers whole 128-byte lines. The MFMA layout
@@ -1170,15 +1326,46 @@ __device__ __forceinline__ void wave_stage_bf16(char* st, const f32x16_t (&acc)[
   }
 }
 
+// The same staging from kloop64_m16's 16 x 16 accumulators (lane (r = lane % 16, g = lane / 16)
+// holds, in acc[mi][ni][2 a + b], row 32 mi + 16 a + r, columns 32 ni + 16 b + 4 g + 0..3).
+template <int MI, int NI>
+__device__ __forceinline__ void wave_stage_bf16(char* st, const f32x4_t (&acc)[MI][NI][4], int mi0, int mi1,
+                                                const uint16_t* bias_cols = nullptr, int bias_ncols = 0) {
+  constexpr int PITCH = WaveStage<NI * 32>::PITCH;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    if (mi < mi0 || mi >= mi1) continue;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int ab = 0; ab < 4; ++ab) {
+        const int a = ab >> 1, b = ab & 1;
+        const int col = 32 * ni + 16 * b + 4 * g;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = acc[mi][ni][ab][u];
+        if (bias_cols != nullptr && col < bias_ncols) {
+          float bv[4];
+          unpack4_bf16(*reinterpret_cast<const uint2*>(bias_cols + col), bv);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] += bv[u];
+        }
+        *reinterpret_cast<uint2*>(st + (32 * (mi - mi0) + 16 * a + r) * PITCH + col * 2) = pack4_bf16(v);
+      }
+  }
+}
+
 // The store loops below run in batches of EPI_BATCH chunks per lane: every LDS read
 // (staged values, output-row numbers) and global read (H, D) of a batch is issued
 // before the first store of the batch, so their latencies overlap instead of adding up
 // chunk by chunk.
 constexpr int EPI_BATCH = 8;
 
-template <int BM, int BN, int EPI, int MI, int NI>
+template <int BM, int BN, int EPI, int MI, int NI, typename AccT>
 __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st, const int* row_table,
-                                                   const f32x16_t (&acc)[MI][NI], int e, int64_t row0, int rows,
+                                                   const AccT (&acc)[MI][NI], int e, int64_t row0, int rows,
                                                    int nt, int wm0, int wn0, int mt = 0,
                                                    const float* scale_table = nullptr) {
   using S = WaveStage<NI * 32>;
@@ -1415,8 +1602,8 @@ __device__ __forceinline__ void rows_epilogue_bf16(const RowsParams& p, char* st
   }
 }
 
-template <int MI, int NI>
-__device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* st, const f32x16_t (&acc)[MI][NI],
+template <int MI, int NI, typename AccT>
+__device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* st, const AccT (&acc)[MI][NI],
                                                     int e, int m0, int n0, int wm0, int wn0) {
   using S = WaveStage<NI * 32>;
   constexpr int ITERS = 32 * MI * S::CPR / 64;
@@ -1447,9 +1634,9 @@ __device__ __forceinline__ void wgrad_epilogue_bf16(const WgradParams& p, char* 
 // area of a block of at least 64 rows), then written row-contiguously, 16 bytes per lane, so
 // every store covers whole 128-byte lines (from the MFMA layout directly, a store would be 16
 // bytes of each of 32 rows). Wave-local: LDS operations of one wave complete in order.
-template <int MI, int NI>
+template <int MI, int NI, typename AccT>
 __device__ __forceinline__ void wgrad_epilogue_f32_staged(const WgradParams& p, char* st,
-                                                          const f32x16_t (&acc)[MI][NI], int e, int m0, int n0,
+                                                          const AccT (&acc)[MI][NI], int e, int m0, int n0,
                                                           int wm0, int wn0) {
   static_assert(MI >= 2, "the fp32 rows of one 32-row block fit the staging area of two");
   constexpr int WN = NI * 32;
@@ -1463,14 +1650,26 @@ __device__ __forceinline__ void wgrad_epilogue_f32_staged(const WgradParams& p, 
   float* DW = reinterpret_cast<float*>(p.dw) + (int64_t)e * p.Ndy * p.Kx;
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
+    if constexpr (std::is_same<AccT, f32x16_t>::value) {
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
+      for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = 32 * ni + 8 * q + 4 * g;
-        *reinterpret_cast<float4*>(st + r * PITCH + col * 4) =
-            make_float4(acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
-      }
+        for (int q = 0; q < 4; ++q) {
+          const int col = 32 * ni + 8 * q + 4 * g;
+          *reinterpret_cast<float4*>(st + r * PITCH + col * 4) = make_float4(
+              acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
+        }
+    } else {  // 16 x 16 blocks (kloop64_m16)
+      const int r16 = lane & 15, g16 = lane >> 4;
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int ab = 0; ab < 4; ++ab) {
+          const int col = 32 * ni + 16 * (ab & 1) + 4 * g16;
+          *reinterpret_cast<float4*>(st + (16 * (ab >> 1) + r16) * PITCH + col * 4) =
+              make_float4(acc[mi][ni][ab][0], acc[mi][ni][ab][1], acc[mi][ni][ab][2], acc[mi][ni][ab][3]);
+        }
+    }
 #pragma unroll
     for (int i0 = 0; i0 < ITERS; i0 += B) {
       uint4 v[B];
@@ -1596,13 +1795,23 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
 
   const int wave = threadIdx.x >> 6;
   const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
-  f32x16_t acc[MI][NI];
+  // 8 waves with the store and SwiGLU epilogues run the 16 x 16 x 32 K loop (kloop64_m16):
+  // C3 step 1.0-1.3% faster than on 32 x 32 x 16 MFMAs, the dense GEMM 2-3%
+  constexpr bool M16 = (EPI == EPI_STORE || EPI == EPI_SWIGLU) && NW == 8;
+  using Acc = typename std::conditional<M16, f32x4_t[4], f32x16_t>::type;
+  Acc acc[MI][NI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
+    for (int ni = 0; ni < NI; ++ni) {
+      if constexpr (M16) {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+        for (int q = 0; q < 4; ++q) acc[mi][ni][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+      }
+    }
 
   // The tile's output rows go to an LDS table above the operand stages: the index
   // loads are issued before the first operand loads and stored once those are in
@@ -1627,7 +1836,10 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
       if constexpr (EPI == EPI_SWIGLU_BWD || EPI == EPI_SWIGLU) scale_table[threadIdx.x] = scale_v;
     }
   };
-  kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
+  if constexpr (M16)
+    kloop64_m16<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
+  else
+    kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
   // every wave is done with the operand stages (and has written its row-table entries)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,
@@ -1892,13 +2104,23 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
 
   const int wave = threadIdx.x >> 6;
   const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
-  f32x16_t acc[MI][NI];
+  // 8 waves run the 16 x 16 x 32 K loop, except with the DY gather (dW2), which measured
+  // 1-3% slower on it at C3 and C4
+  constexpr bool M16 = NW == 8 && !DYG;
+  using Acc = typename std::conditional<M16, f32x4_t[4], f32x16_t>::type;
+  Acc acc[MI][NI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
+    for (int ni = 0; ni < NI; ++ni) {
+      if constexpr (M16) {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+        for (int q = 0; q < 4; ++q) acc[mi][ni][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[mi][ni][q] = 0.f;
+      }
+    }
 
   if constexpr (GATHER != 0) {
     if (nk > 0) pend = issue_idx(0);
@@ -1906,7 +2128,10 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   auto prefetch = [&](int kt) {
     if constexpr (GATHER != 0) fetch_src(kt);
   };
-  kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
+  if constexpr (M16)
+    kloop64_m16<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
+  else
+    kloop64<LPS, MI, NI, true, true, BM, BN>(nk, lds, wm0, wn0, acc, dma, prefetch, [] {});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the stages
   char* st = smem + wave * 32 * MI * WaveStage<WN>::PITCH;
   if constexpr (OUT_F32)
