@@ -1211,12 +1211,12 @@ __device__ __forceinline__ void kloop64_m16(int nk, lds_char* lds, int wm0, int 
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[(t >> 1) & 1][ni][b].value(), fa[t & 1][mil][a].value(), c, 0, 0,
                                                 0);
   };
-  // step t: MFMAs of step t, reads of step (t + 1) % 4 from rst, loads of window slots
-  // [w0, w0 + NMMA) of stage lkt into buffer lbuf
+  // step t: MFMAs of step t, reads of step (t + 1) % 4 from rst (spread evenly over the
+  // step's MFMA slots: 1.5-2% faster per launch at C3 than issued in the first slots), loads
+  // of window slots [w0, w0 + NMMA) of stage lkt into buffer lbuf
   auto step = [&](int t, const lds_char* rst, int w0, int lbuf, int lkt, bool lon) {
     const int tn = (t + 1) & 3;
     const int nr = nread(tn);
-    constexpr int RPS = (NRA + NRB + NMMA - 1) / NMMA;
     __builtin_amdgcn_sched_barrier(0);
     if (w0 >= 0) __builtin_amdgcn_s_setprio(1);
     else __builtin_amdgcn_s_setprio(0);
@@ -1228,8 +1228,8 @@ __device__ __forceinline__ void kloop64_m16(int nk, lds_char* lds, int wm0, int 
       for (int j = 0; j < LPS; ++j)
         if (w0 >= 0 && j * WIN / LPS == w0 + i) dma(j, lbuf, lkt, lon);
 #pragma unroll
-      for (int r = 0; r < RPS; ++r)
-        if (i * RPS + r < nr) read(rst, tn, i * RPS + r);
+      for (int r = 0; r < NRA + NRB; ++r)
+        if (r < nr && (r * NMMA) / nr == i) read(rst, tn, r);
       __builtin_amdgcn_sched_barrier(0);
     }
     asm_wait_lgkm<0>();
@@ -2104,9 +2104,10 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
 
   const int wave = threadIdx.x >> 6;
   const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
-  // 8 waves run the 16 x 16 x 32 K loop, except with the DY gather (dW2), which measured
-  // 1-3% slower on it at C3 and C4
-  constexpr bool M16 = NW == 8 && !DYG;
+  // 8 waves run the 16 x 16 x 32 K loop, except with the DY gather (dW2), which measured 1-3%
+  // slower on it at C3 and C4, and in the launch with the few-rows form inline (dW1 under
+  // skewed routing: 2-4% slower at C4)
+  constexpr bool M16 = NW == 8 && !DYG && !FEW;
   using Acc = typename std::conditional<M16, f32x4_t[4], f32x16_t>::type;
   Acc acc[MI][NI];
 #pragma unroll
