@@ -21,9 +21,9 @@
 //     ds_read_b64_tr_b16 for operands whose reduction dimension is strided. Each
 //     stage has its own scalar buffer descriptor (the k advance and the tail
 //     clipping), so issuing a load costs no vector ALU.
-//   * v_mfma_f32_16x16x32_bf16 on 8 waves (kloop64_m16; the SwiGLU-backward and
-//     Newton-Schulz epilogues, 4-wave tiles and the DY-gathered weight grads keep
-//     v_mfma_f32_32x32x16_bf16, kloop64), with the B tile as the first operand: each
+//   * v_mfma_f32_16x16x32_bf16 on 8 waves (kloop64_m16; the SwiGLU-backward epilogue,
+//     4-wave tiles, the DY-gathered weight grads and the weight grads with the few-rows form
+//     inline keep v_mfma_f32_32x32x16_bf16, kloop64), with the B tile as the first operand: each
 //     lane ends up holding 4 consecutive output columns of one output row. Every MFMA
 //     slot of the K loop is pinned with sched_barrier so loads, fragment reads and the
 //     one barrier per stage interleave with the MFMAs.
@@ -1795,9 +1795,10 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
 
   const int wave = threadIdx.x >> 6;
   const int wm0 = WG::wm0(wave), wn0 = WG::wn0(wave);
-  // 8 waves with the store and SwiGLU epilogues run the 16 x 16 x 32 K loop (kloop64_m16):
-  // C3 step 1.0-1.3% faster than on 32 x 32 x 16 MFMAs, the dense GEMM 2-3%
-  constexpr bool M16 = (EPI == EPI_STORE || EPI == EPI_SWIGLU) && NW == 8;
+  // 8 waves run the 16 x 16 x 32 K loop (kloop64_m16; the C3 step 2.8% faster than on 32 x 32 x 16
+  // MFMAs, the Newton-Schulz pass 2.5%), except with the SwiGLU-backward epilogue, which has no
+  // registers left for its extra fragments
+  constexpr bool M16 = EPI != EPI_SWIGLU_BWD && NW == 8;
   using Acc = typename std::conditional<M16, f32x4_t[4], f32x16_t>::type;
   Acc acc[MI][NI];
 #pragma unroll
