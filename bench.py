@@ -56,14 +56,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "3206131745e4c190fdd39ae96bfa5e0c6248cf3ee1b66018d280d35d0e0d18a4"
+TRAFFIC_C3_GEMM_SHA256 = "acd4b6289717de4b1364b63211d173029079aa12fd2719a75514df58168d8be8"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6097900757,
-    "scatter2scatter#0": 2888153280,
-    "glu_w2_backward_dh#0": 2364568512,
-    "scatter2scatter#1": 5763346581,
-    "group_bwd_w#0": 2156162069,
-    "group_bwd_w#1": 3650406400,
+    "glu_w1_forward#0": 6049233290,
+    "scatter2scatter#0": 2873574101,
+    "glu_w2_backward_dh#0": 2340988117,
+    "scatter2scatter#1": 5684362261,
+    "group_bwd_w#0": 2167831786,
+    "group_bwd_w#1": 3665939413,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
