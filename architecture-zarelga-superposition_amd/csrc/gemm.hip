@@ -15,7 +15,8 @@
 // bf16 tile machinery (BM x BN = 256 x 256 on 8 waves in a 2x4 grid, two waves per
 // SIMD and 128 x 64 outputs per wave; or 128 x 128 on 4 waves in a 2x2 grid):
 //   * Operands go HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) in
-//     64-deep stages, double-buffered, every wave loading its own share: 128-byte
+//     64-deep stages, double-buffered (a rows tile of at most 64 rows: three stages of its
+//     64 rows and the weight block, kloop_small), every wave loading its own share: 128-byte
 //     rows with the reduction dimension contiguous (16-byte chunks XOR-swizzled by
 //     row so that each 8- or 16-lane group of a fragment read hits distinct banks), or K-major tiles read with
 //     ds_read_b64_tr_b16 for operands whose reduction dimension is strided. Each
@@ -858,7 +859,7 @@ __device__ __forceinline__ uint32_t t_off(int krow, int col, int row_bytes) {
 // Fragment reads are inline asm: LLVM's waitcnt pass makes any LDS read it cannot
 // disambiguate (the ds_read_tr intrinsic carries no alias info) wait for every
 // in-flight LDS-DMA load, which would serialise the stage pipeline. Being asm,
-// these reads are invisible to that pass, so mma_stage_bf16 issues its own
+// these reads are invisible to that pass, so the K loops issue their own
 // lgkmcnt waits and ties the fragment registers to them with empty asm (data
 // dependencies keep every MFMA after the wait that covers its operands).
 typedef int v4i32_t __attribute__((ext_vector_type(4)));
@@ -1267,6 +1268,94 @@ __device__ __forceinline__ void kloop64_m16(int nk, lds_char* lds, int wm0, int 
   }
   __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
   __builtin_amdgcn_s_setprio(0);
+}
+
+// The K loop of an 8-wave 256 x BN tile that holds at most kSmallRows rows (an expert's only or
+// last m-tile, e.g. the rare experts of a skewed routing): such a tile is bound by its operand
+// loads (a few rows against a BN-column block of the weights streamed through the whole
+// reduction), not by its MFMAs, and kloop64_m16 gives it one stage of loads in flight. Here only
+// the first kSmallRows A rows are loaded (the waves whose RowLoad<256, 8> rows those are), so a
+// stage takes (kSmallRows + BN) x 64 x 2 bytes and three of them fit in the kernel's LDS: two
+// stages are in flight while one is read (C4: W2 forward 8%, W1 input grad 5% faster; at C3,
+// where only last m-tiles are this short, W2 forward and dA 1.5%). Waves 0-3 (the tile's rows
+// 0-127) run the MFMAs of rows 0 .. kSmallRows - 1 with the accumulator layout of kloop64_m16;
+// waves 4-7 only load. Per stage: wait for this wave's loads of it, barrier (every wave's loads
+// are in and every wave is done with the buffer read two stages ago), issue the loads of the
+// stage two ahead into that buffer, then read and multiply. dma_a(q, stage, kt, on) and
+// dma_b(q, stage, kt, on) issue A / B load q of stage kt into the A / B part of a stage.
+constexpr int kSmallRows = 64;
+template <int NQA, int NQB, int MI, int NI, bool B_T, int BN, typename DmaA, typename DmaB, typename Hook>
+__device__ __forceinline__ void kloop_small(int nk, lds_char* lds, int wm0, int wn0, f32x4_t (&acc)[MI][NI][4],
+                                            DmaA dma_a, DmaB dma_b, Hook after_prologue_loads) {
+  constexpr int KS = 64;
+  constexpr int kA = kSmallRows * KS * 2;
+  constexpr int kS = kA + BN * KS * 2;
+  constexpr int SM = kSmallRows / 32;              // 32-row blocks with rows
+  constexpr int AR = Frag16<false>::kReads, BR = Frag16<B_T>::kReads;
+  constexpr int kAWaves = kSmallRows / (8 * NQA);  // RowLoad<256, 8>: wave w loads rows 8 NQA w ..
+  static_assert(SM * 32 == kSmallRows && SM <= MI && MI * 32 == 128, "the rows lie in waves 0-3's blocks");
+  static_assert(kAWaves * 8 * NQA == kSmallRows, "whole waves load the first kSmallRows rows");
+  const int wu = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const bool a_wave = wu < kAWaves;  // wave-uniform
+  const bool mma_wave = __builtin_amdgcn_readfirstlane(wm0) == 0;
+  auto issue = [&](int buf, int kt, bool on) {
+    lds_char* st = lds + buf * kS;
+    if (a_wave) {
+#pragma unroll
+      for (int q = 0; q < NQA; ++q) dma_a(q, st, kt, on);
+    }
+#pragma unroll
+    for (int q = 0; q < NQB; ++q) dma_b(q, st + kA, kt, on);
+  };
+  if (nk <= 0) {
+    after_prologue_loads();
+    return;
+  }
+  issue(0, 0, true);
+  issue(1, 1, nk > 1);
+  after_prologue_loads();
+  int cur = 0;  // buffer of stage kt
+  for (int kt = 0; kt < nk; ++kt) {
+    // stage kt has landed once at most stage kt + 1's loads are outstanding
+    if (a_wave) __builtin_amdgcn_s_waitcnt(vm_wait(NQA + NQB));
+    else __builtin_amdgcn_s_waitcnt(vm_wait(NQB));
+    asm volatile("s_barrier" ::: "memory");
+    issue(cur == 0 ? 2 : cur - 1, kt + 2, kt + 2 < nk);
+    if (mma_wave) {
+      const lds_char* st = lds + cur * kS;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        Frag16<false> fa[SM][2];
+        Frag16<B_T> fb[NI][2];
+#pragma unroll
+        for (int f = 0; f < 2 * SM; ++f)
+#pragma unroll
+          for (int q = 0; q < AR; ++q) fa[f >> 1][f & 1].template read_piece<kSmallRows, KS>(st, 16 * f, j, q);
+#pragma unroll
+        for (int f = 0; f < 2 * NI; ++f)
+#pragma unroll
+          for (int q = 0; q < BR; ++q)
+            fb[f >> 1][f & 1].template read_piece<BN, KS>(st + kA, wn0 + 16 * f, j, q);
+        asm_wait_lgkm<0>();
+#pragma unroll
+        for (int f = 0; f < 2 * SM; ++f) fa[f >> 1][f & 1].tie();
+#pragma unroll
+        for (int f = 0; f < 2 * NI; ++f) fb[f >> 1][f & 1].tie();
+#pragma unroll
+        for (int mil = 0; mil < SM; ++mil)
+#pragma unroll
+          for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+              for (int b = 0; b < 2; ++b)
+                acc[mil][ni][2 * a + b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    fb[ni][b].value(), fa[mil][a].value(), acc[mil][ni][2 * a + b], 0, 0, 0);
+      }
+    }
+    cur = cur == 2 ? 0 : cur + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));  // loads past the end (zeros) are done before LDS is reused
 }
 
 // Epilogues: each wave stages its own WM x WN accumulator block in its own LDS area
@@ -1700,13 +1789,15 @@ struct WaveGrid {
   __device__ __forceinline__ static int wn0(int wave) { return (wave % GN) * WN; }
 };
 
-// LDS of the bf16 kernels: two operand stages, reused by the wave staging areas
-// after the K loop, then the rows kernel's output-row table.
+// LDS of the bf16 kernels: two operand stages (three short ones in kloop_small), reused by
+// the wave staging areas after the K loop, then the rows kernel's output-row table.
 template <int BM, int BN, int NW = 4>
 constexpr int bf16_stage_bytes() {
   constexpr int loop = 2 * (BM + BN) * 64 * 2;
+  constexpr int small = (BM == 256 && NW == 8) ? 3 * (kSmallRows + BN) * 64 * 2 : 0;
   constexpr int epi = NW * WaveGrid<BM, BN, NW>::WM * WaveStage<WaveGrid<BM, BN, NW>::WN>::PITCH;
-  return loop > epi ? loop : epi;
+  constexpr int ops = loop > small ? loop : small;
+  return ops > epi ? ops : epi;
 }
 
 template <int BM, int BN, bool B_T, int EPI, int NW = 4>
@@ -1778,19 +1869,23 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
   const char* b_base = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(p.b) + (int64_t)e * p.b_estride);
   constexpr int NQA = LA::NQ;
   constexpr int LPS = NQA + (B_T ? LBT::NQ : LBN::NQ);  // loads per wave per stage
-  auto dma = [&](int q, int buf, int kt, bool on) {
-    lds_char* sa = lds + buf * kStage;
-    lds_char* sb = sa + BM * KS * 2;
+  auto dma_a = [&](int q, lds_char* sa, int kt, bool on) {
     const int64_t k0 = (int64_t)kt * KS;
-    const bool last = kt == nk - 1;
-    if (q < NQA) {
-      la.issue(q, stage_rsrc(a_base, p.a_bytes, 2 * k0, (int64_t)p.a_bytes, on), sa, wu, last);
-    } else if constexpr (!B_T) {
-      lbn.issue(q - NQA, stage_rsrc(b_base, p.b_bytes, 2 * k0, (int64_t)p.b_bytes, on), sb, wu, last);
+    la.issue(q, stage_rsrc(a_base, p.a_bytes, 2 * k0, (int64_t)p.a_bytes, on), sa, wu, kt == nk - 1);
+  };
+  auto dma_b = [&](int q, lds_char* sb, int kt, bool on) {
+    const int64_t k0 = (int64_t)kt * KS;
+    if constexpr (!B_T) {
+      lbn.issue(q, stage_rsrc(b_base, p.b_bytes, 2 * k0, (int64_t)p.b_bytes, on), sb, wu, kt == nk - 1);
     } else {
       const int64_t pitch = p.ldb * 2;
-      lbt.issue(q - NQA, stage_rsrc(b_base, p.b_bytes, k0 * pitch, ((int64_t)p.K - k0) * pitch, on), sb, wu);
+      lbt.issue(q, stage_rsrc(b_base, p.b_bytes, k0 * pitch, ((int64_t)p.K - k0) * pitch, on), sb, wu);
     }
+  };
+  auto dma = [&](int q, int buf, int kt, bool on) {
+    lds_char* sa = lds + buf * kStage;
+    if (q < NQA) dma_a(q, sa, kt, on);
+    else dma_b(q - NQA, sa + BM * KS * 2, kt, on);
   };
 
   const int wave = threadIdx.x >> 6;
@@ -1837,10 +1932,15 @@ __global__ __launch_bounds__(NW * 64) void rows_bf16_kernel(RowsParams p) {
       if constexpr (EPI == EPI_SWIGLU_BWD || EPI == EPI_SWIGLU) scale_table[threadIdx.x] = scale_v;
     }
   };
-  if constexpr (M16)
-    kloop64_m16<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
-  else
+  if constexpr (M16) {
+    // a tile of at most kSmallRows rows streams its weight block three stages deep
+    if (BM == 256 && __builtin_amdgcn_readfirstlane(rows) <= kSmallRows)
+      kloop_small<NQA, LPS - NQA, MI, NI, B_T, BN>(nk, lds, wm0, wn0, acc, dma_a, dma_b, hook);
+    else
+      kloop64_m16<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
+  } else {
     kloop64<LPS, MI, NI, false, B_T, BM, BN>(nk, lds, wm0, wn0, acc, dma, [](int) {}, hook);
+  }
   // every wave is done with the operand stages (and has written its row-table entries)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   rows_epilogue_bf16<BM, BN, EPI>(p, smem + wave * 32 * MI * WaveStage<WN>::PITCH, row_table, acc, e, row0, rows,

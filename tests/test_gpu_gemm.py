@@ -91,6 +91,66 @@ def test_scatter2scatter_banded_tile_order(hip_device, dtype, w_layout, case):
     assert_close(np64(Y), ref, **TOL[dtype], what=f"scatter2scatter {case}")
 
 
+# Rows per expert for the 256 x 256 rows launches (R / E >= 256): experts of 0-64 rows (an only m-tile
+# of at most 64 rows), just past it (65, 128, 129), and partial last m-tiles of 5 and 64 rows
+SMALL_TILE_COUNTS = np.array([0, 1, 17, 63, 64, 65, 300, 261, 576, 2000, 128, 129])
+
+
+def _fixed_routing(counts, k, hip_device, seed):
+    """Top-k slots that give expert e exactly counts[e] rows (sum(counts) divisible by k)."""
+    from zmoe import ops
+
+    slots = np.repeat(np.arange(len(counts)), counts)
+    np.random.default_rng(seed).shuffle(slots)
+    idx = torch.from_numpy(slots.reshape(-1, k)).to(hip_device)
+    se, ss, off, _ = ops.flatten_sort_count(idx, len(counts))
+    assert np.array_equal(np.diff(np.concatenate([[0], off.cpu().numpy()])), counts)
+    return se, ss, off
+
+
+@pytest.mark.parametrize("xg,yg", [(False, True), (True, False)])
+@pytest.mark.parametrize("w_layout", ["param", "contiguous"])
+def test_scatter2scatter_small_tiles(hip_device, xg, yg, w_layout):
+    """256 x 256 tiles that hold at most 64 rows (experts of 1-64 rows, last m-tiles of 5 and 64
+    rows) beside full ones, with a partial K stage (K = 200) and a partial n-tile (N = 264), for
+    both weight layouts (B read row- or K-major) and both A forms (rows gathered or in place)."""
+    from zmoe import ops
+
+    counts, k, K, N = SMALL_TILE_COUNTS, 2, 200, 264
+    E, R = len(counts), int(counts.sum())
+    se, ss, off = _fixed_routing(counts, k, hip_device, seed=11)
+    g = gen(R + N)
+    X = torch.randn(R if xg else R // k, K, generator=g).to(torch.bfloat16)
+    Wp = (torch.randn(E, N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    W = Wp.to(hip_device).permute(0, 2, 1) if w_layout == "param" else Wp.permute(0, 2, 1).contiguous().to(hip_device)
+    Y = ops.scatter2scatter(X.to(hip_device), W, se, ss, 1 if xg else k, x_grouped=xg, y_grouped=yg,
+                            expert_offsets=off)
+    ref = O.scatter2scatter(np64(X), np64(Wp).transpose(0, 2, 1), se.cpu().numpy(), ss.cpu().numpy(),
+                            1 if xg else k, x_grouped=xg, y_grouped=yg)
+    assert_close(np64(Y), ref, **TOL[torch.bfloat16], what=f"scatter2scatter small tiles xg={xg} yg={yg}")
+
+
+def test_glu_w1_forward_scaled_small_tiles(hip_device):
+    """The W1 forward's SwiGLU epilogue (H and the row-scaled A) on 256 x 256 pair tiles that hold
+    at most 64 rows beside full ones (f = 136: a partial pair tile; d = 200: a partial K stage)."""
+    from zmoe import ops
+
+    counts, k, d, f = SMALL_TILE_COUNTS, 2, 200, 136
+    E, R = len(counts), int(counts.sum())
+    se, ss, off = _fixed_routing(counts, k, hip_device, seed=12)
+    g = gen(R + f)
+    x = torch.randn(R // k, d, generator=g).to(torch.bfloat16)
+    W1 = (torch.randn(E, 2 * f, d, generator=g) / d ** 0.5).to(torch.bfloat16)
+    rs = (torch.rand(R, generator=g) + 0.05).to(hip_device)
+    H, A = ops.glu_w1_forward(x.to(hip_device), W1.to(hip_device), se, ss, off, k, row_scale=rs)
+    refH = O.scatter2scatter(np64(x), np64(W1).transpose(0, 2, 1), se.cpu().numpy(), ss.cpu().numpy(), k,
+                             x_grouped=False, y_grouped=True)
+    tol = TOL[torch.bfloat16]
+    assert_close(np64(H), refH, **tol, what="H")
+    refA = O.bf16_round((rs.double().cpu().numpy()[:, None] * O.swiglu(np64(H))).astype(np.float32))
+    assert_close(np64(A), refA.astype(np.float64), **tol, what="scaled A")
+
+
 def test_glu_w1_forward_banded_pair_tiles(hip_device):
     """SwiGLU W1 forward with f = 2200 (18 pair-column tiles of 128 pairs): banded n order."""
     from zmoe import ops
