@@ -285,9 +285,10 @@ __host__ __device__ __forceinline__ int slab_size(int64_t total) {
   const int64_t per_xcd = (total + kXcds - 1) / kXcds;
   return per_xcd < kSlab ? (int)(per_xcd > 0 ? per_xcd : 1) : kSlab;
 }
-__device__ __forceinline__ int slab_logical_tile(int total) {
+__device__ __forceinline__ int slab_logical_tile(int total, int b = -1) {
+  if (b < 0) b = (int)blockIdx.x;
   const int slab = slab_size(total);
-  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+  const int xcd = b % kXcds, slot = b / kXcds;
   const int logical = ((slot / slab) * kXcds + xcd) * slab + slot % slab;
   return logical < total ? logical : -1;
 }
@@ -345,6 +346,9 @@ struct WgradParams {
   // >= 0: a dense split-K launch over this many rows, "expert" e being split e of E (the
   // ranges of split_end below; offsets unused); < 0: the row ranges come from offsets
   int64_t split_rows = -1;
+  // > 0 (the launch with the few-rows form inline): workgroups 0 .. fillers - 1 write the
+  // zeros of every empty expert's grad, each a contiguous share; the tiles of empty experts exit
+  int fillers = 0;
   // tile order within an expert: n-tiles outer (1, the tiles sharing an X block run
   // together) or m-tiles outer (0, those sharing a DY block)
   int n_major = 0;
@@ -2073,6 +2077,49 @@ __device__ __forceinline__ void wgrad_few_rows_tile(const WgradParams& p, char* 
     wgrad_epilogue_bf16(p, st, acc, e, m0, n0, wm0, wn0);
 }
 
+// Zero filler f of p.fillers: the grads of the experts with no rows, concatenated in expert
+// order, are cut into equal contiguous shares of 16-byte units; this workgroup writes share f.
+// One workgroup stores ~150 GB/s and 32 reach 4.6 TB/s (a fill probe on MI355X), so a few
+// long-lived fillers write the zeros beside the K-loop tiles on the other CUs, where one
+// 128 KB zero tile per workgroup took every CU in turn for each empty expert.
+template <int NTH, bool OUT_F32>
+__device__ __forceinline__ void wgrad_zero_fill(const WgradParams& p, char* smem, int f) {
+  constexpr int ES = OUT_F32 ? 4 : 2;
+  int* empty = reinterpret_cast<int*>(smem);  // [E] ranks -> expert ids
+  int* tmp = empty + kGemmMaxE;
+  const int ept = (p.E + NTH - 1) / NTH;  // experts per thread (E <= 1024, NTH = 512: <= 2)
+  int flags = 0, cnt = 0;
+  for (int q = 0; q < ept; ++q) {
+    const int e = (int)threadIdx.x * ept + q;
+    if (e < p.E) {
+      const int64_t b = e ? p.offsets[e - 1] : 0;
+      if (p.offsets[e] <= b) {
+        flags |= 1 << q;
+        ++cnt;
+      }
+    }
+  }
+  int n_empty;
+  int rank = block_exclusive_scan<NTH>(cnt, tmp, &n_empty);
+  for (int q = 0; q < ept; ++q)
+    if (flags & (1 << q)) empty[rank++] = (int)threadIdx.x * ept + q;
+  __syncthreads();
+  if (n_empty == 0) return;
+  const int64_t units_e = (int64_t)p.Ndy * p.Kx * ES / 16;  // 16-byte units per expert grad
+  const int64_t total = units_e * n_empty;
+  const int64_t u0 = total * f / p.fillers, u1 = total * (f + 1) / p.fillers;
+  uint4* dw = reinterpret_cast<uint4*>(p.dw);
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  for (int64_t u = u0; u < u1;) {
+    const int k = (int)(u / units_e);
+    const int64_t in = u - (int64_t)k * units_e;
+    const int64_t run = min(units_e - in, u1 - u);
+    uint4* dst = dw + (int64_t)empty[k] * units_e + in;
+    for (int64_t i = threadIdx.x; i < run; i += NTH) dst[i] = z;
+    u += run;
+  }
+}
+
 // GATHER: 0 = x rows in sorted order; 1 = gathered, row = index >> shift; 2 = gathered,
 // row = index / x_div. Both gathered forms keep the K loop free of branches. DYG: the
 // gather applies to the DY rows instead (x rows then in sorted order).
@@ -2087,7 +2134,13 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   constexpr int kStage = (BM + BN) * KS * 2;
 
   const int per_e = p.m_tiles * p.n_tiles;
-  const int logical = slab_logical_tile(p.E * per_e);
+  if constexpr (FEW) {
+    if ((int)blockIdx.x < p.fillers) {
+      wgrad_zero_fill<NW * 64, OUT_F32>(p, smem, (int)blockIdx.x);
+      return;
+    }
+  }
+  const int logical = slab_logical_tile(p.E * per_e, (int)blockIdx.x - (FEW ? p.fillers : 0));
   if (logical < 0) return;
   const int e = logical / per_e;
   const int rem = logical % per_e;
@@ -2101,7 +2154,7 @@ __global__ __launch_bounds__(NW * 64) void wgrad_bf16_kernel(WgradParams p) {
   if (nrows < p.rows_lo || nrows > p.rows_hi) return;  // the other launch of a split covers this expert
   const int m0 = mt * BM, n0 = nt * BN;
   if (nrows == 0) {
-    wgrad_zero_tile<BM, BN, NW * 64, OUT_F32>(p, e, m0, n0);
+    if (!FEW || p.fillers == 0) wgrad_zero_tile<BM, BN, NW * 64, OUT_F32>(p, e, m0, n0);
     return;
   }
   if constexpr (FEW) {  // an expert of at most kFewRows rows: the write-bound form, no K loop
@@ -2374,6 +2427,7 @@ int launch_wgrad_kernel(K kern, int lds, int BM, int BN, WgradParams p, hipStrea
   int64_t total = (int64_t)p.E * p.m_tiles * p.n_tiles;
   const int slab = slab_size(total);
   total = cdiv(total, (int64_t)kXcds * slab) * kXcds * slab;  // whole slabs on every XCD (slab_logical_tile)
+  total += p.fillers;  // a multiple of kXcds: the tiles keep their XCDs
   ZMOE_REQUIRE(total < (int64_t)0x7fffffff, ZMOE_ERR_SHAPE, "group_bwd_w: too many tiles");
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(threads), lds, s, p);
   return check_launch("grouped wgrad kernel");
@@ -2397,6 +2451,10 @@ inline bool use_big_tiles(int64_t R, int E, int64_t N) { return R >= (int64_t)E 
 // tiles, two workgroups per CU) before the K-loop launch, each launch covering every
 // expert's tiles and the workgroups of the other launch's experts exiting at once: the
 // inline form measured 10% slower there (3.13 -> 3.45 ms at C4).
+// Zero fillers of the launch with the few-rows form inline (wgrad_zero_fill): C4's dW1
+// 6.12-6.15 -> 6.02-6.03 ms with 32 (16: 6.28, the fill outlasts the tiles; 64: 6.05).
+// A multiple of kXcds, so that every tile keeps its XCD.
+constexpr int kZeroFillers = 32;
 inline int wgrad_small_rows(int64_t R, int E) { return R < (int64_t)E * 1024 ? kFewRows : 0; }
 
 // ==================================================================== small-M streaming path
@@ -2890,7 +2948,8 @@ int group_bwd_w_bf16(WgradParams p, int64_t M, int E, int64_t N, int64_t K, hipS
   };
   const int split = big ? wgrad_small_rows(M, E) : 0;
   if constexpr (!DYG) {
-    if (split > 0) {  // one launch: each workgroup picks its form
+    if (split > 0) {  // one launch: each workgroup picks its form; the first ones fill the empty experts' zeros
+      p.fillers = kZeroFillers;
       if (gather == 1) return launch_wgrad_big<1, OUT_F32, false, true>(p, s);
       if (gather == 2) return launch_wgrad_big<2, OUT_F32, false, true>(p, s);
       return launch_wgrad_big<0, OUT_F32, false, true>(p, s);

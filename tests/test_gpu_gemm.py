@@ -320,6 +320,43 @@ def test_group_bwd_w_empty_experts_on_the_k_loop_launch(hip_device, out_f32):
         assert (DWt[e] == 0).all(), f"empty expert {e} must get exact zeros"
 
 
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("gather", [False, True])
+def test_group_bwd_w_zero_fillers(hip_device, out_f32, gather):
+    """The launch with the few-rows form inline (fewer than 1024 rows per expert on average):
+    the empty experts' grads come from the zero-filler workgroups (each a contiguous share of
+    their concatenation, shares crossing expert boundaries), not from their tiles; the output
+    starts as NaN so that every zero must be written. Empty experts first, last and adjacent."""
+    from zmoe import ops
+
+    counts = np.array([0, 0, 1, 64, 65, 700, 0, 2400, 3, 0, 0, 300, 0])
+    E, k, N, K = len(counts), 2, 512, 264
+    off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
+    R = int(counts.sum())
+    assert 256 * E <= R < 1024 * E  # 256 x 256 tiles, few-rows form inline
+    g = gen(R + 5)
+    DY = torch.randn(R, N, generator=g).to(torch.bfloat16)
+    if gather:
+        ss = torch.from_numpy(np.random.default_rng(9).permutation(R)).to(hip_device)
+        X = torch.randn(R // k + 1, K, generator=g).to(torch.bfloat16)
+        Xg = O.group(np64(X), ss.cpu().numpy(), fan_out=k)
+    else:
+        ss = None
+        X = torch.randn(R, K, generator=g).to(torch.bfloat16)
+        Xg = np64(X)
+    DWt = torch.full((E, N, K), float("nan"), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                     device=hip_device)
+    ops.group_bwd_w(DY.to(hip_device), X.to(hip_device), off, E, x_gather=ss, x_div=k, out=DWt,
+                    out_dtype=torch.float32 if out_f32 else None)
+    ref, _ = O.group_bwd_w(np64(DY), Xg, off.cpu().numpy(), E)
+    if out_f32:
+        assert_close_fro(np64(DWt), ref.transpose(0, 2, 1), what="group_bwd_w f32")
+    else:
+        assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[torch.bfloat16], what="group_bwd_w")
+    for e in np.nonzero(counts == 0)[0]:
+        assert (DWt[e] == 0).all(), f"empty expert {e} must get exact zeros"
+
+
 @pytest.mark.parametrize("T,d,f,E,k,skew", [(300, 256, 512, 8, 2, 0.0), (2048, 512, 768, 8, 2, 0.0),
                                             (1200, 200, 136, 4, 2, 0.3), (128, 512, 136, 64, 4, 1.5),
                                             (32, 256, 256, 32, 8, 0.0)])
