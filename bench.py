@@ -56,14 +56,14 @@ GEMM_OPS = ("glu_w1_forward", "scatter2scatter", "glu_w2_backward_dh", "group_bw
 # one after the other): when those differ, the line reports traffic null and says why.
 TRAFFIC_C3_PROFILE = "profiles/grouped_gemm_c3_hbm_bytes.md"
 TRAFFIC_C3_SOURCES = ("gemm.hip", "zmoe_internal.h")  # what the grouped GEMM kernels compile from
-TRAFFIC_C3_GEMM_SHA256 = "1b50db88948afd88f06214672d5290a736421559ad8a63b6edf13736a3747a24"
+TRAFFIC_C3_GEMM_SHA256 = "d38eed6a4335a73af29503a97c1226584f471d8cc58f3fd5205c9aaf7c53e814"
 TRAFFIC_C3 = {
-    "glu_w1_forward#0": 6072920149,
-    "scatter2scatter#0": 2906146858,
-    "glu_w2_backward_dh#0": 2447342101,
-    "scatter2scatter#1": 5832785834,
-    "group_bwd_w#0": 2163977450,
-    "group_bwd_w#1": 3659105920,
+    "glu_w1_forward#0": 6035677760,
+    "scatter2scatter#0": 2891170624,
+    "glu_w2_backward_dh#0": 2458364202,
+    "scatter2scatter#1": 5833844736,
+    "group_bwd_w#0": 2165850346,
+    "group_bwd_w#1": 3661097280,
 }
 ROW_OPS = ("route_topk", "flatten_sort_count", "combine", "combine_backward", "combine_backward_scale",
            "swiglu_backward_gates", "sum_k")
