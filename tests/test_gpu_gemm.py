@@ -321,13 +321,36 @@ def test_group_bwd_w_empty_experts_on_the_k_loop_launch(hip_device, out_f32):
 
 
 @pytest.mark.parametrize("out_f32", [False, True])
-@pytest.mark.parametrize("gather", [False, True])
+@pytest.mark.parametrize("gather", [False, True, "dy"])
 def test_group_bwd_w_zero_fillers(hip_device, out_f32, gather):
-    """The launch with the few-rows form inline (fewer than 1024 rows per expert on average):
-    the empty experts' grads come from the zero-filler workgroups (each a contiguous share of
-    their concatenation, shares crossing expert boundaries), not from their tiles; the output
-    starts as NaN so that every zero must be written. Empty experts first, last and adjacent."""
+    """Fewer than 1024 rows per expert on average: the empty experts' grads come from the
+    zero-filler workgroups of the 256 x 256 launch with the few-rows form inline (each a
+    contiguous share of their concatenation, shares crossing expert boundaries), not from their
+    tiles; with the gather on DY, from the separate few-rows launch. The output starts as NaN so
+    that every zero must be written. Empty experts first, last and adjacent."""
     from zmoe import ops
+
+    if gather == "dy":
+        counts = np.array([0, 0, 1, 64, 65, 700, 0, 2400, 3, 0, 0, 300, 0])
+        E, k, N, K = len(counts), 2, 264, 512
+        off = torch.from_numpy(np.cumsum(counts)).to(hip_device)
+        R = int(counts.sum())
+        g = gen(R + 6)
+        ss = torch.from_numpy(np.random.default_rng(10).permutation(R)).to(hip_device)
+        DY = torch.randn(R // k + 1, N, generator=g).to(torch.bfloat16)
+        X = torch.randn(R, K, generator=g).to(torch.bfloat16)
+        DWt = torch.full((E, N, K), float("nan"), dtype=torch.float32 if out_f32 else torch.bfloat16,
+                         device=hip_device)
+        ops.group_bwd_w_gather_dy(DY.to(hip_device), ss, k, X.to(hip_device), off, E, out=DWt,
+                                  out_dtype=torch.float32 if out_f32 else None)
+        ref, _ = O.group_bwd_w(O.group(np64(DY), ss.cpu().numpy(), fan_out=k), np64(X), off.cpu().numpy(), E)
+        if out_f32:
+            assert_close_fro(np64(DWt), ref.transpose(0, 2, 1), what="group_bwd_w_gather_dy f32")
+        else:
+            assert_close(np64(DWt), ref.transpose(0, 2, 1), **TOL[torch.bfloat16], what="group_bwd_w_gather_dy")
+        for e in np.nonzero(counts == 0)[0]:
+            assert (DWt[e] == 0).all(), f"empty expert {e} must get exact zeros"
+        return
 
     counts = np.array([0, 0, 1, 64, 65, 700, 0, 2400, 3, 0, 0, 300, 0])
     E, k, N, K = len(counts), 2, 512, 264
