@@ -108,15 +108,17 @@ def _fixed_routing(counts, k, hip_device, seed):
     return se, ss, off
 
 
+@pytest.mark.parametrize("K", [200, 64, 120])
 @pytest.mark.parametrize("xg,yg", [(False, True), (True, False)])
 @pytest.mark.parametrize("w_layout", ["param", "contiguous"])
-def test_scatter2scatter_small_tiles(hip_device, xg, yg, w_layout):
+def test_scatter2scatter_small_tiles(hip_device, xg, yg, w_layout, K):
     """256 x 256 tiles that hold at most 64 rows (experts of 1-64 rows, last m-tiles of 5 and 64
-    rows) beside full ones, with a partial K stage (K = 200) and a partial n-tile (N = 264), for
-    both weight layouts (B read row- or K-major) and both A forms (rows gathered or in place)."""
+    rows) beside full ones, with a partial n-tile (N = 264), for both weight layouts (B read row-
+    or K-major) and both A forms (rows gathered or in place). K = 200: four stages, the last
+    partial; 64: a single stage; 120: two, the second partial (the three-stage ring's edges)."""
     from zmoe import ops
 
-    counts, k, K, N = SMALL_TILE_COUNTS, 2, 200, 264
+    counts, k, N = SMALL_TILE_COUNTS, 2, 264
     E, R = len(counts), int(counts.sum())
     se, ss, off = _fixed_routing(counts, k, hip_device, seed=11)
     g = gen(R + N)
